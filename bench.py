@@ -1,0 +1,399 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused layer-kernel hot path on one MI355X.
+
+Headline workload (one "step"): the epilogue chain of one T2S decode step for B = 64 sequences,
+d_model 512, FFN 2048, 24 layers, fp16 storage / fp32 arithmetic — the decode-input gather +
+alpha*PE, then per layer residual+LayerNorm (norm1), bias+ReLU on the FFN activations, residual+
+LayerNorm (norm2): 73 launches, replayed as one HIP graph per step. `value` is the algorithmic
+bytes of a step (every input read once, every output written once, parameters once) divided by
+the measured step time, with all inputs resident in HBM.
+
+Also reported (same JSON line):
+  roofline      the dominant kernel of the step (residual+LayerNorm [64,512]) — bytes per launch
+                over its average launch duration from HIP events, against 8 TB/s;
+  cpu_baseline  the oracle's C restatement of the same step on the host cores;
+  kernels       every fused kernel of the configurations at its stated shape (single call) and as a
+                replicated batch of independent instances (> 1 GB moved, MALL flushed between
+                repetitions), in GB/s and fraction of 8 TB/s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
+       python bench.py --only KERNEL   (one kernel's replicated launch loop, for rocprofv3 runs)
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "gpt-sovits-native_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of MI355X peak) per fused kernel; T2S decode-step µs"
+SEED = 20250823
+
+B, D, FF, LAYERS, VOCAB, MAX_POS = 64, 512, 2048, 24, 1025, 2048
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---- algorithmic bytes ---------------------------------------------------------------------------
+
+def ln_bytes(rows, n, esz, bias=True, res=True):
+    """x (+ residual) read, y written, gamma/beta (+ bias) fp32 read once."""
+    return rows * n * esz * (2 + (1 if res else 0)) + n * 4 * (2 + (1 if bias else 0))
+
+
+def bias_act_bytes(rows, n, esz, bias=True):
+    return 2 * rows * n * esz + (n * 4 if bias else 0)
+
+
+def embed_bytes(rows, d, out_esz, tab_esz, id_esz=8, per_row_pos=True):
+    return rows * (id_esz + (8 if per_row_pos else 0) + d * tab_esz + d * 4 + d * out_esz)
+
+
+def gn_bytes(C, T, esz):
+    return 2 * C * T * esz + 2 * C * 4
+
+
+def step_bytes():
+    return (embed_bytes(B, D, 2, 2) + 2 * LAYERS * ln_bytes(B, D, 2)
+            + LAYERS * bias_act_bytes(B, FF, 2))
+
+
+# ---- T2S decode-step buffers ---------------------------------------------------------------------
+
+def make_step_buffers(torch, gsvk, dev):
+    g = torch.Generator(device="cpu").manual_seed(SEED + 2000)
+
+    def rn(*shape, std=1.0, mean=0.0, dtype=torch.float16):
+        return (torch.randn(*shape, generator=g) * std + mean).to(dtype).to(dev)
+
+    bufs = {
+        "table": rn(VOCAB, D, std=0.02),
+        "ids": torch.randint(0, VOCAB, (B,), generator=g).to(dev),
+        "pos": torch.randint(512, MAX_POS, (B,), generator=g).to(dev),
+        "pe": torch.from_numpy(gsvk.pe_table(MAX_POS, D)).to(dev),
+        "alpha": float(torch.empty(1).uniform_(0.5, 1.5, generator=g)),
+        "x": torch.empty(B, D, dtype=torch.float16, device=dev),
+        "h": torch.empty(B, D, dtype=torch.float16, device=dev),
+        "err": torch.zeros(1, dtype=torch.int32, device=dev),
+    }
+    for name, shape in (("attn_out", (B, D)), ("ff", (B, FF)), ("ffn_out", (B, D))):
+        bufs[name] = [rn(*shape) for _ in range(LAYERS)]
+    for name, n in (("bout", D), ("b1", FF), ("b2", D)):
+        bufs[name] = [rn(n, std=0.02, dtype=torch.float32) for _ in range(LAYERS)]
+    for name in ("n1g", "n2g"):
+        bufs[name] = [rn(D, std=0.1, mean=1.0, dtype=torch.float32) for _ in range(LAYERS)]
+    for name in ("n1b", "n2b"):
+        bufs[name] = [rn(D, std=0.1, dtype=torch.float32) for _ in range(LAYERS)]
+    return bufs
+
+
+def time_loop(torch, fn, iters, warmup=3):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / iters  # ms
+
+
+def graph_of(torch, fn, n):
+    """Capture n calls of fn into a CUDA/HIP graph on a side stream."""
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        fn()  # warm
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=st):
+        for _ in range(n):
+            fn()
+    torch.cuda.synchronize()
+    return gr
+
+
+# ---- per-kernel suite ------------------------------------------------------------------------------
+
+class Flusher:
+    """Writes a 512 MiB scratch buffer between timed repetitions so the 256 MB MALL holds none of
+    the kernel's inputs."""
+
+    def __init__(self, torch, dev):
+        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def __call__(self):
+        self.buf.fill_(1)
+
+
+def measure_reps(torch, fn, flush, reps=9):
+    """Median of single-launch durations (HIP events), MALL flushed before each."""
+    times = []
+    fn()
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        flush()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
+
+
+def kernel_suite(torch, gsvk, dev, only=None):
+    """Each fused kernel at its stated shape and as a replicated batch (> 1 GB moved)."""
+    f16, f32 = torch.float16, torch.float32
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    flush = Flusher(torch, dev)
+    out = []
+
+    def rn(*shape, dtype=f16, std=1.0, mean=0.0):
+        t = torch.empty(*shape, dtype=f32, device=dev).normal_(mean, std, generator=g)
+        return t.to(dtype)
+
+    def run(name, cfg, stated, replicated, bytes_fn, count):
+        """stated / replicated: (setup -> launch fn) builders taking a replication factor."""
+        if only and only != name:
+            return
+        rec = {"kernel": name, "config": cfg}
+        fn1 = stated()
+        ms1 = time_loop(torch, fn1, 50)
+        rec["stated_shape"] = {"us": round(ms1 * 1e3, 3), "bytes": bytes_fn(1),
+                               "GBps": round(bytes_fn(1) / ms1 / 1e6, 1), "calls_per_config": count}
+        del fn1
+        rep, fnr = replicated()
+        msr = measure_reps(torch, fnr, flush)
+        gbs = bytes_fn(rep) / msr / 1e6
+        rec["replicated"] = {"instances": rep, "bytes": bytes_fn(rep), "us": round(msr * 1e3, 2),
+                             "GBps": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        del fnr
+        torch.cuda.empty_cache()
+        out.append(rec)
+        log(f"  {name}: stated {rec['stated_shape']['us']} us, replicated "
+            f"{rec['replicated']['GBps']} GB/s ({100 * gbs / PEAK_GBS:.1f}%)")
+
+    def ln_case(rows, n, dt, eps, bias, res, rep):
+        def make(k):
+            x = rn(rows * k, n, dtype=dt)
+            r = rn(rows * k, n, dtype=dt) if res else None
+            gm, bt = rn(n, dtype=f32, std=0.1, mean=1.0), rn(n, dtype=f32, std=0.1)
+            bi = rn(n, dtype=f32, std=0.02) if bias else None
+            y = torch.empty_like(x)
+            return lambda: gsvk.add_layernorm(x, gm, bt, y, eps, bias=bi, residual=r)
+        esz = 4 if dt == f32 else 2
+        return (lambda: make(1), lambda: (rep, make(rep)),
+                lambda k: ln_bytes(rows * k, n, esz, bias, res))
+
+    def ba_case(rows, n, act, rep):
+        def make(k):
+            x = rn(rows * k, n)
+            bi = rn(n, dtype=f32, std=0.02)
+            return lambda: gsvk.bias_act(act, x, x, bias=bi)
+        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: bias_act_bytes(rows * k, n, 2))
+
+    # config 1: residual + LayerNorm fp32 [256, 512]
+    run("residual_layernorm_f32_256x512", 1, *ln_case(256, 512, f32, 1e-5, False, True, 1024), 1)
+    # config 2: gather + PE prefill/decode, LN [64,512], bias+ReLU [64,2048]
+    pe = torch.from_numpy(gsvk.pe_table(MAX_POS, D)).to(dev)
+
+    def emb_case(rows, rep):
+        def make(k):
+            tab = rn(VOCAB, D, std=0.02)
+            ids = torch.randint(0, VOCAB, (rows * k,), device=dev, generator=g)
+            pos = torch.randint(0, MAX_POS, (rows * k,), device=dev, generator=g)
+            o = torch.empty(rows * k, D, dtype=f16, device=dev)
+            return lambda: gsvk.embed_pe(tab, ids, pe, 0.93, o, pos=pos)
+        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: embed_bytes(rows * k, D, 2, 2))
+
+    run("embed_pe_prefill_1024x512", 2, *emb_case(1024, 512), 1)
+    run("embed_pe_decode_64x512", 2, *emb_case(64, 8192), 1)
+    run("residual_layernorm_f16_64x512", 2, *ln_case(64, 512, f16, 1e-5, True, True, 8192), 48)
+    run("bias_relu_f16_64x2048", 2, *ba_case(64, 2048, gsvk.ACT_RELU, 4096), 24)
+    # config 3: bias + GELU [512, 4096], residual + LN(1024, eps 1e-12)
+    run("bias_gelu_f16_512x4096", 3, *ba_case(512, 4096, gsvk.ACT_GELU_ERF, 128), 1)
+    run("residual_layernorm_f16_512x1024_eps1e-12", 3,
+        *ln_case(512, 1024, f16, 1e-12, False, True, 512), 24)
+    # config 4: GroupNorm + GELU [512, 31999] fp32, LN(768), bias + GELU [499, 3072]
+
+    def gn_case(rep):
+        def make(k):
+            x = rn(512 * k, 31999, dtype=f32, std=0.5)
+            gm, bt = rn(512 * k, dtype=f32, std=0.1, mean=1.0), rn(512 * k, dtype=f32, std=0.1)
+            y = torch.empty_like(x)
+            return lambda: gsvk.groupnorm_gelu(x, gm, bt, y, 1e-5)
+        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: gn_bytes(512 * k, 31999, 4))
+
+    run("groupnorm_gelu_f32_512x31999", 4, *gn_case(8), 1)
+    run("residual_layernorm_f16_499x768", 4, *ln_case(499, 768, f16, 1e-5, True, True, 512), 24)
+    run("bias_gelu_f16_499x3072", 4, *ba_case(499, 3072, gsvk.ACT_GELU_ERF, 192), 12)
+
+    # config 5: SoVITS ResBlock epilogues at the largest stage [24, 320000]
+    def sv_case(kind, dt, rep):
+        E = 24 * 320000
+        esz = 4 if dt == f32 else 2
+
+        def make(k):
+            n = E * k
+            if kind == "K1":
+                t = rn(n, dtype=dt)
+                return lambda: gsvk.leaky_relu(t, t, 0.1)
+            if kind == "K2":
+                cur, tb, tin = rn(n, dtype=dt), rn(n, dtype=dt), torch.empty(n, dtype=dt, device=dev)
+                return lambda: gsvk.resblock_add_lrelu(cur, tb, tin, 0.1)
+            curs = [rn(n, dtype=dt) for _ in range(3)]
+            tbs = [rn(n, dtype=dt) for _ in range(3)]
+            o = torch.empty(n, dtype=dt, device=dev)
+            return lambda: gsvk.resblock_branch_mean(curs, tbs, o, True, 0.1)
+        per = {"K1": 2, "K2": 4, "K3": 7}[kind]
+        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: per * E * k * esz)
+
+    for kind, count in (("K3", 1), ("K2", 6), ("K1", 9)):
+        for dt, nm, rep in ((f32, "f32", 8), (f16, "f16", 16)):
+            run(f"sovits_{kind}_{nm}_24x320000", 5, *sv_case(kind, dt, rep), count)
+    return out
+
+
+# ---- CPU baseline ----------------------------------------------------------------------------------
+
+def cpu_baseline(torch, bufs, budget_s=8.0):
+    """The oracle's restatement of the same decode step on host copies of the same buffers."""
+    import numpy as np
+
+    import oracle as O
+
+    def hostcopy(t):
+        a = t.detach().cpu().contiguous()
+        if a.dtype == torch.float16:
+            return a.view(torch.int16).numpy().view(np.uint16).copy()
+        return a.numpy().copy()
+
+    hb = {k: ([hostcopy(t) for t in v] if isinstance(v, list) else
+              (hostcopy(v) if hasattr(v, "device") else v)) for k, v in bufs.items()}
+    hb["table_dtype"] = O.F16
+    threads_all = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads_all = max(1, min(threads_all, 16, B))
+    res = {}
+    for threads in sorted({1, threads_all}):
+        O.t2s_step(O.F16, hb, threads=threads)  # warm
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s / 2:
+            O.t2s_step(O.F16, hb, threads=threads)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res[threads] = (dt, n)
+    return res, threads_all
+
+
+# ---- main --------------------------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None, help="run one kernel of the suite and exit")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every kernel here is row- or element-local, so more "
+              "GPUs would each run an independent share (no figure at several GPUs is produced).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import gsvk
+    gsvk.lib()  # fails loudly when libgsvk.so is missing
+    dev = torch.device("cuda:0")
+
+    if a.only:
+        kernel_suite(torch, gsvk, dev, only=a.only)
+        return
+
+    bufs = make_step_buffers(torch, gsvk, dev)
+    step = gsvk.T2SStep(bufs, eps=1e-5, graph=True)
+    nbytes = step_bytes()
+    for _ in range(a.warmup):
+        step.run()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(a.steps):
+        step.run()
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e) / a.steps
+    assert int(bufs["err"].item()) == 0
+    log(f"decode step (graph, {step.launches} launches): {ms * 1e3:.2f} us")
+
+    # per-op breakdown at the step's shapes: graphs of 48 back-to-back launches of each op
+    x, h = bufs["x"], bufs["h"]
+    L0 = lambda: gsvk.add_layernorm(bufs["attn_out"][0], bufs["n1g"][0], bufs["n1b"][0], h, 1e-5,
+                                    bias=bufs["bout"][0], residual=x)
+    R0 = lambda: gsvk.bias_act(gsvk.ACT_RELU, bufs["ff"][0], bufs["ff"][0], bias=bufs["b1"][0])
+    E0 = lambda: gsvk.embed_pe(bufs["table"], bufs["ids"], bufs["pe"], bufs["alpha"], x,
+                               pos=bufs["pos"], err=bufs["err"])
+    per_op = {}
+    for name, fn, cnt, byt in (("residual_layernorm", L0, 48, ln_bytes(B, D, 2)),
+                               ("bias_relu", R0, 24, bias_act_bytes(B, FF, 2)),
+                               ("embed_pe", E0, 1, embed_bytes(B, D, 2, 2))):
+        gr = graph_of(torch, fn, 48)
+        us = time_loop(torch, gr.replay, 20) * 1e3 / 48
+        per_op[name] = {"us_per_launch": round(us, 3), "launches_per_step": cnt, "bytes": byt,
+                        "GBps": round(byt / us / 1e3, 1)}
+        del gr
+    dom = max(per_op, key=lambda k: per_op[k]["us_per_launch"] * per_op[k]["launches_per_step"])
+    d = per_op[dom]
+    ach = d["bytes"] / d["us_per_launch"] / 1e3
+    roofline = {"kernel": f"{dom} [{B},{D if dom != 'bias_relu' else FF}] f16",
+                "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_GBS, 5), "traffic": None,
+                "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_launch"]}
+
+    cpu = None
+    if not a.no_cpu:
+        res, tall = cpu_baseline(torch, bufs)
+        t_best = res[tall][0]
+        cpu = {"value": round(nbytes / t_best / 1e9, 3), "unit": "GB/s", "cores": tall,
+               "kind": "port",
+               "sample": f"{res[tall][1]} decode steps (B={B}, {LAYERS} layers, fp16 storage) of the "
+                         f"oracle's C restatement, rows split over {tall} threads",
+               "us_per_step": round(t_best * 1e6, 1),
+               "single_thread_us_per_step": round(res[1][0] * 1e6, 1)}
+
+    kernels = None if a.no_kernels else kernel_suite(torch, gsvk, dev)
+
+    line = {
+        "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded normal activations / parameters, uniform ids and positions)",
+        "config": {"workload": "t2s_decode_step_epilogues", "batch": B, "d_model": D, "ffn": FF,
+                   "layers": LAYERS, "storage": "f16", "launches_per_step": step.launches,
+                   "bytes_per_step": nbytes, "us_per_step": round(ms * 1e3, 3),
+                   "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_GBS, 5), "graph": True},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_op": per_op,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    step.close()
+
+
+if __name__ == "__main__":
+    main()

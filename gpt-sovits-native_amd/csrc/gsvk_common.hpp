@@ -1,0 +1,170 @@
+// gsvk_common.hpp — storage traits, 128-bit row access and wave64 reductions shared by the gfx950
+// kernels. Everything here is device code for CDNA4 (wave64); nothing is portable on purpose.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "gsvk.h"
+
+namespace gsvk {
+
+constexpr int kWave = 64;
+
+// ---- scalar conversions (exact upcast, round-to-nearest-even downcast) -------------------------
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+__device__ __forceinline__ uint32_t f2h(float v) {
+  // The value must be rounded to fp32 first and then to fp16 (the reference computes in fp32 and
+  // the fp16 store rounds that result). Without the empty asm below, the compiler folds a
+  // producing fmaf into v_fma_mixlo_f16, which rounds the exact result to fp16 once and differs
+  // in the last bit for some inputs; the asm makes v an opaque fp32 register value.
+  __asm__("" : "+v"(v));
+  // v_cvt_f16_f32 rounds to nearest even, overflows to inf and keeps NaN (as vcvt_f16_f32 does)
+  // for results in the normal half range. For results below 2^-14 (half subnormals) it was
+  // measured on MI355X to round exact ties away from zero, so that range is rounded here: the
+  // scaling by 2^24 is exact and v_rndne_f32 rounds half to even, giving the subnormal's bits.
+  const float a = __builtin_fabsf(v);
+  const uint32_t sign = (__builtin_bit_cast(uint32_t, v) >> 16) & 0x8000u;
+  const uint32_t sub = sign | static_cast<uint32_t>(__builtin_rintf(a * 0x1p24f));
+  const uint32_t hw = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  return a < 0x1p-14f ? sub : hw;
+}
+__device__ __forceinline__ float bf2f(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+__device__ __forceinline__ uint32_t f2bf(float v) {
+  // Round to nearest even on the top 16 bits; every NaN becomes the canonical quiet NaN 0x7FC0.
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// ---- storage traits: one 16-byte chunk = VEC elements ----------------------------------------
+
+template <int DT>
+struct Store;
+
+template <>
+struct Store<GSVK_F32> {
+  using T = float;
+  static constexpr int VEC = 4;
+  __device__ static __forceinline__ void load(const void* base, size_t i, float (&v)[VEC]) {
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i);
+    v[0] = __builtin_bit_cast(float, q.x);
+    v[1] = __builtin_bit_cast(float, q.y);
+    v[2] = __builtin_bit_cast(float, q.z);
+    v[3] = __builtin_bit_cast(float, q.w);
+  }
+  __device__ static __forceinline__ void store(void* base, size_t i, const float (&v)[VEC]) {
+    uint4 q;
+    q.x = __builtin_bit_cast(uint32_t, v[0]);
+    q.y = __builtin_bit_cast(uint32_t, v[1]);
+    q.z = __builtin_bit_cast(uint32_t, v[2]);
+    q.w = __builtin_bit_cast(uint32_t, v[3]);
+    *reinterpret_cast<uint4*>(static_cast<float*>(base) + i) = q;
+  }
+  __device__ static __forceinline__ float load1(const void* base, size_t i) {
+    return static_cast<const float*>(base)[i];
+  }
+  __device__ static __forceinline__ void store1(void* base, size_t i, float v) {
+    static_cast<float*>(base)[i] = v;
+  }
+};
+
+template <int DT>
+struct Store16 {  // f16 and bf16 share the 16-bit packing
+  static constexpr int VEC = 8;
+  __device__ static __forceinline__ float up(uint32_t b) { return DT == GSVK_F16 ? h2f(b) : bf2f(b); }
+  __device__ static __forceinline__ uint32_t down(float v) { return DT == GSVK_F16 ? f2h(v) : f2bf(v); }
+  __device__ static __forceinline__ void load(const void* base, size_t i, float (&v)[VEC]) {
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = up(w[k] & 0xffffu);
+      v[2 * k + 1] = up(w[k] >> 16);
+    }
+  }
+  __device__ static __forceinline__ void store(void* base, size_t i, const float (&v)[VEC]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = down(v[2 * k]) | (down(v[2 * k + 1]) << 16);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  __device__ static __forceinline__ float load1(const void* base, size_t i) {
+    return up(static_cast<const uint16_t*>(base)[i]);
+  }
+  __device__ static __forceinline__ void store1(void* base, size_t i, float v) {
+    static_cast<uint16_t*>(base)[i] = static_cast<uint16_t>(down(v));
+  }
+};
+template <>
+struct Store<GSVK_F16> : Store16<GSVK_F16> {};
+template <>
+struct Store<GSVK_BF16> : Store16<GSVK_BF16> {};
+
+// fp32 parameter vectors (gamma / beta / bias): 4 floats per 16 bytes.
+__device__ __forceinline__ void load_f32x4(const float* p, size_t i, float* v) {
+  const float4 q = *reinterpret_cast<const float4*>(p + i);
+  v[0] = q.x;
+  v[1] = q.y;
+  v[2] = q.z;
+  v[3] = q.w;
+}
+
+// ---- wave64 reductions -------------------------------------------------------------------------
+// Inside each 16-lane DPP row: quad_perm xor-1, quad_perm xor-2, row_half_mirror, row_mirror give
+// every lane its row's sum; ds_swizzle (xor 16) folds rows pairwise inside each 32-lane half and
+// two readlanes fold the halves. The result is wave-uniform and bitwise identical on every lane.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  return lo + hi;
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// ---- host-side helpers shared by the launchers ------------------------------------------------
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline size_t dtype_size(int dt) { return dt == GSVK_F32 ? 4 : 2; }
+
+inline bool valid_dtype(int dt) { return dt == GSVK_F32 || dt == GSVK_F16 || dt == GSVK_BF16; }
+
+// True when [a, a+abytes) and [b, b+bbytes) intersect.
+inline bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  if (!a || !b || !abytes || !bbytes) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+// Bytes spanned by a [rows, n] view with row stride ld.
+inline size_t span_bytes(size_t rows, size_t n, size_t ld, size_t esz) {
+  return rows ? ((rows - 1) * ld + n) * esz : 0;
+}
+
+int launch_status();  // GSVK_OK, or GSVK_E_HIP after a failed launch (reads hipGetLastError)
+
+}  // namespace gsvk

@@ -1,0 +1,189 @@
+// gsvk_embed.hip — token-embedding gather fused with the scaled sinusoidal positional add (gfx950).
+//
+// One wave64 per output row. The wave reads its id and position once (wave-uniform scalar loads),
+// then each lane moves 8 consecutive columns: the table row chunk (16 B for f16/bf16, 32 B for f32),
+// the PE row chunk (32 B fp32), optionally the mm row chunk and the bias chunk, and writes 8 output
+// columns. The arithmetic is the reference's exactly (fmaf is the contraction AppleClang applies to
+// `e + alpha * pe`), so the result is bit-identical to the CPU restatement for every input.
+#include "gsvk_common.hpp"
+
+namespace gsvk {
+namespace {
+
+struct EmbArgs {
+  const void* table;
+  const void* ids;
+  const int64_t* pos;
+  const float* pe;
+  const void* mm;
+  const float* bias;
+  void* out;
+  int32_t* err;
+  long vocab;
+  long max_pos;
+  long rows;
+  long D;
+  int64_t pos0;
+  float alpha;
+  int ids32;
+};
+
+constexpr int kBlock = 256;
+
+// 8 consecutive elements starting at element i (i multiple of 8, 16-byte aligned for every dtype).
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, size_t i, float (&v)[8]) {
+  if constexpr (DT == GSVK_F32) {
+    float a[4], b[4];
+    Store<GSVK_F32>::load(p, i, a);
+    Store<GSVK_F32>::load(p, i + 4, b);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[k] = a[k];
+      v[4 + k] = b[k];
+    }
+  } else {
+    Store<DT>::load(p, i, v);
+  }
+}
+template <int DT>
+__device__ __forceinline__ void store8(void* p, size_t i, const float (&v)[8]) {
+  if constexpr (DT == GSVK_F32) {
+    const float a[4] = {v[0], v[1], v[2], v[3]}, b[4] = {v[4], v[5], v[6], v[7]};
+    Store<GSVK_F32>::store(p, i, a);
+    Store<GSVK_F32>::store(p, i + 4, b);
+  } else {
+    Store<DT>::store(p, i, v);
+  }
+}
+
+// Row check shared by both paths: returns the table row and PE row element offsets, or -1.
+__device__ __forceinline__ bool row_source(const EmbArgs& a, long r, size_t& trow, size_t& prow) {
+  const int64_t id = a.ids32 ? static_cast<int64_t>(static_cast<const int32_t*>(a.ids)[r])
+                             : static_cast<const int64_t*>(a.ids)[r];
+  const int64_t p = a.pos ? a.pos[r] : a.pos0 + r;
+  if (id < 0 || id >= a.vocab || p < 0 || p >= a.max_pos) return false;
+  trow = static_cast<size_t>(id) * a.D;
+  prow = static_cast<size_t>(p) * a.D;
+  return true;
+}
+
+template <int OUT, int TAB>
+__global__ __launch_bounds__(kBlock) void embed_pe_vec(EmbArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long wave = static_cast<long>(blockIdx.x) * (kBlock / kWave) + (threadIdx.x / kWave);
+  const long nwaves = static_cast<long>(gridDim.x) * (kBlock / kWave);
+  const long nch = a.D / 8;
+  for (long r = wave; r < a.rows; r += nwaves) {
+    size_t trow = 0, prow = 0;
+    const bool ok = row_source(a, r, trow, prow);
+    const size_t orow = static_cast<size_t>(r) * a.D;
+    if (!ok) {
+      if (lane == 0 && a.err) *a.err = 1;
+      float nan8[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) nan8[k] = __builtin_nanf("");
+      for (long c = lane; c < nch; c += kWave) store8<OUT>(a.out, orow + c * 8, nan8);
+      continue;
+    }
+    for (long c = lane; c < nch; c += kWave) {
+      float e[8], pe[8], o[8];
+      load8<TAB>(a.table, trow + c * 8, e);
+      load8<GSVK_F32>(a.pe, prow + c * 8, pe);
+      if (a.bias) {
+        float b[8];
+        load8<GSVK_F32>(a.bias, c * 8, b);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = e[k] + b[k];
+      }
+      if (a.mm) {
+        float m[8];
+        load8<OUT>(a.mm, orow + c * 8, m);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = m[k] + e[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = __builtin_fmaf(a.alpha, pe[k], e[k]);
+      store8<OUT>(a.out, orow + c * 8, o);
+    }
+  }
+}
+
+template <int OUT, int TAB>
+__global__ __launch_bounds__(kBlock) void embed_pe_scalar(EmbArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long wave = static_cast<long>(blockIdx.x) * (kBlock / kWave) + (threadIdx.x / kWave);
+  const long nwaves = static_cast<long>(gridDim.x) * (kBlock / kWave);
+  for (long r = wave; r < a.rows; r += nwaves) {
+    size_t trow = 0, prow = 0;
+    const bool ok = row_source(a, r, trow, prow);
+    const size_t orow = static_cast<size_t>(r) * a.D;
+    if (!ok && lane == 0 && a.err) *a.err = 1;
+    for (long d = lane; d < a.D; d += kWave) {
+      float o = __builtin_nanf("");
+      if (ok) {
+        float e = Store<TAB>::load1(a.table, trow + d);
+        if (a.bias) e = e + a.bias[d];
+        if (a.mm) e = Store<OUT>::load1(a.mm, orow + d) + e;
+        o = __builtin_fmaf(a.alpha, a.pe[prow + d], e);
+      }
+      Store<OUT>::store1(a.out, orow + d, o);
+    }
+  }
+}
+
+template <int OUT, int TAB>
+void launch_embed(const EmbArgs& a, bool vec_ok, hipStream_t st) {
+  long g = (a.rows + (kBlock / kWave) - 1) / (kBlock / kWave);
+  if (g > 2048) g = 2048;
+  if (vec_ok) hipLaunchKernelGGL((embed_pe_vec<OUT, TAB>), dim3(g), dim3(kBlock), 0, st, a);
+  else hipLaunchKernelGGL((embed_pe_scalar<OUT, TAB>), dim3(g), dim3(kBlock), 0, st, a);
+}
+
+template <int OUT>
+void launch_embed_tab(int tab, const EmbArgs& a, bool vec_ok, hipStream_t st) {
+  switch (tab) {
+    case GSVK_F32: launch_embed<OUT, GSVK_F32>(a, vec_ok, st); break;
+    case GSVK_F16: launch_embed<OUT, GSVK_F16>(a, vec_ok, st); break;
+    default: launch_embed<OUT, GSVK_BF16>(a, vec_ok, st); break;
+  }
+}
+
+}  // namespace
+}  // namespace gsvk
+
+using namespace gsvk;
+
+extern "C" int gsvk_embed_pe(int out_dtype, int table_dtype, int index_type, const void* table,
+                             size_t vocab, const void* ids, const int64_t* pos, int64_t pos0,
+                             const float* pe, size_t max_pos, float alpha, const void* mm,
+                             const float* bias, void* out, size_t rows, size_t D, int32_t* err,
+                             void* stream) {
+  if (!valid_dtype(out_dtype) || !valid_dtype(table_dtype)) return GSVK_E_DTYPE;
+  if (index_type != GSVK_I64 && index_type != GSVK_I32) return GSVK_E_DTYPE;
+  if (!table || !ids || !pe || !out) return GSVK_E_NULL;
+  if (rows == 0 || D == 0 || vocab == 0 || max_pos == 0 || rows > (1ul << 40) ||
+      D > (1ul << 30) || vocab > (1ul << 40) || max_pos > (1ul << 40))
+    return GSVK_E_SIZE;
+  if (D % 2) return GSVK_E_ARG;
+  const size_t osz = dtype_size(out_dtype), obytes = rows * D * osz;
+  const size_t isz = index_type == GSVK_I64 ? 8 : 4;
+  if (mm && mm != out && overlaps(out, obytes, mm, obytes)) return GSVK_E_ALIAS;
+  if (overlaps(out, obytes, table, vocab * D * dtype_size(table_dtype)) ||
+      overlaps(out, obytes, ids, rows * isz) || overlaps(out, obytes, pos, pos ? rows * 8 : 0) ||
+      overlaps(out, obytes, pe, max_pos * D * 4) || overlaps(out, obytes, bias, bias ? D * 4 : 0) ||
+      overlaps(out, obytes, err, err ? 4 : 0))
+    return GSVK_E_ALIAS;
+  EmbArgs a{table, ids, pos, pe, mm, bias, out, err, static_cast<long>(vocab),
+            static_cast<long>(max_pos), static_cast<long>(rows), static_cast<long>(D), pos0,
+            alpha, index_type == GSVK_I32};
+  const bool vec_ok = D % 8 == 0 && aligned16(table) && aligned16(pe) && aligned16(out) &&
+                      (!mm || aligned16(mm)) && (!bias || aligned16(bias));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case GSVK_F32: launch_embed_tab<GSVK_F32>(table_dtype, a, vec_ok, st); break;
+    case GSVK_F16: launch_embed_tab<GSVK_F16>(table_dtype, a, vec_ok, st); break;
+    default: launch_embed_tab<GSVK_BF16>(table_dtype, a, vec_ok, st); break;
+  }
+  return launch_status();
+}

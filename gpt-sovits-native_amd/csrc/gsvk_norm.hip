@@ -1,0 +1,448 @@
+// gsvk_norm.hip — residual-add + LayerNorm over rows and per-channel GroupNorm + GELU for gfx950.
+//
+// LayerNorm: one wave64 per row. Each lane owns the 16-byte chunks lane, lane+64, ... of its row
+// (so every load/store instruction of the wave covers 1 KiB contiguously), keeps them in VGPRs,
+// and the row statistics are an exact two-pass mean / centred second moment over those registers,
+// reduced with DPP + ds_swizzle. gamma / beta / bias chunks for the lane's columns stay in VGPRs
+// across all rows the wave visits (waves stride over rows), so per-row traffic is the row itself.
+//
+// GroupNorm(groups = channels): one 1024-thread workgroup per channel row of length T, the whole
+// row held in VGPRs (up to 8 chunks of 16 bytes per thread: T <= 32768 fp32 / 65536 fp16),
+// double-precision block reduction through LDS, then normalize + GELU(erf) and a single write:
+// one HBM read and one write per element.
+#include <cmath>
+
+#include "gsvk_common.hpp"
+
+namespace gsvk {
+namespace {
+
+struct LnArgs {
+  const void* x;
+  const float* bias;
+  const void* res;
+  const float* gamma;
+  const float* beta;
+  void* y;
+  long rows;
+  int n;
+  long ld;
+  double eps;
+};
+
+constexpr int kLnBlock = 256;  // 4 waves -> 4 rows in flight per workgroup
+
+__device__ __forceinline__ float finish_rstd(float var, double eps) {
+  return static_cast<float>(1.0 / sqrt(static_cast<double>(var) + eps));
+}
+
+// Vector path: n % VEC == 0, every row start 16-byte aligned, n <= 64 * CPL * VEC.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  constexpr bool kCache = CPL * V <= 16;  // keep per-column parameters in VGPRs across rows
+  const int lane = threadIdx.x & (kWave - 1);
+  const long wave = static_cast<long>(blockIdx.x) * (kLnBlock / kWave) + (threadIdx.x / kWave);
+  const long nwaves = static_cast<long>(gridDim.x) * (kLnBlock / kWave);
+  const int nch = a.n / V;
+  const bool has_bias = a.bias != nullptr, has_res = a.res != nullptr;
+  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
+
+  float pg[kCache ? CPL : 1][V], pb[kCache ? CPL : 1][V], pbias[kCache ? CPL : 1][V];
+  auto load_params = [&](int idx, float (&g)[V], float (&b)[V], float (&bi)[V]) {
+#pragma unroll
+    for (int k = 0; k < V; k += 4) {
+      if (has_g) load_f32x4(a.gamma, static_cast<size_t>(idx) * V + k, &g[k]);
+      else g[k] = g[k + 1] = g[k + 2] = g[k + 3] = 1.f;
+      if (has_b) load_f32x4(a.beta, static_cast<size_t>(idx) * V + k, &b[k]);
+      else b[k] = b[k + 1] = b[k + 2] = b[k + 3] = 0.f;
+      if (has_bias) load_f32x4(a.bias, static_cast<size_t>(idx) * V + k, &bi[k]);
+      else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
+    }
+  };
+  if constexpr (kCache) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int idx = lane + c * kWave;
+      if (idx < nch) load_params(idx, pg[c], pb[c], pbias[c]);
+    }
+  }
+
+  for (long row = wave; row < a.rows; row += nwaves) {
+    const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.ld);
+    float h[CPL][V];
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int idx = lane + c * kWave;
+      if (idx < nch) {
+        S::load(a.x, base + static_cast<size_t>(idx) * V, h[c]);
+        float bi[V];
+        if constexpr (kCache) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) bi[k] = pbias[c][k];
+        } else {
+#pragma unroll
+          for (int k = 0; k < V; k += 4) {
+            if (has_bias) load_f32x4(a.bias, static_cast<size_t>(idx) * V + k, &bi[k]);
+            else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
+          }
+        }
+        if (has_bias) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + bi[k];
+        }
+        if (has_res) {
+          float r[V];
+          S::load(a.res, base + static_cast<size_t>(idx) * V, r);
+#pragma unroll
+          for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + r[k];
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k) s += h[c][k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) h[c][k] = 0.f;
+      }
+    }
+    const float sum = wave_sum(s);
+    const float mean = static_cast<float>(static_cast<double>(sum) / static_cast<double>(a.n));
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int idx = lane + c * kWave;
+      if (idx < nch) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+          const float d = h[c][k] - mean;
+          q = __builtin_fmaf(d, d, q);
+        }
+      }
+    }
+    const float sq = wave_sum(q);
+    const float var = static_cast<float>(static_cast<double>(sq) / static_cast<double>(a.n));
+    const float rstd = finish_rstd(var, a.eps);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int idx = lane + c * kWave;
+      if (idx < nch) {
+        float g[V], b[V], bi_unused[V];
+        if constexpr (kCache) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+            g[k] = pg[c][k];
+            b[k] = pb[c][k];
+          }
+        } else {
+          load_params(idx, g, b, bi_unused);
+        }
+        float o[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) o[k] = __builtin_fmaf((h[c][k] - mean) * rstd, g[k], b[k]);
+        S::store(a.y, base + static_cast<size_t>(idx) * V, o);
+      }
+    }
+  }
+}
+
+// Generic path: any n, any alignment. One wave per row, three strided sweeps (the row is re-read
+// from cache instead of held in registers).
+template <int DT>
+__global__ __launch_bounds__(kLnBlock) void ln_rows_generic(LnArgs a) {
+  using S = Store<DT>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const long wave = static_cast<long>(blockIdx.x) * (kLnBlock / kWave) + (threadIdx.x / kWave);
+  const long nwaves = static_cast<long>(gridDim.x) * (kLnBlock / kWave);
+  for (long row = wave; row < a.rows; row += nwaves) {
+    const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.ld);
+    auto hval = [&](int j) {
+      float v = S::load1(a.x, base + j);
+      if (a.bias) v = v + a.bias[j];
+      if (a.res) v = v + S::load1(a.res, base + j);
+      return v;
+    };
+    float s = 0.f;
+    for (int j = lane; j < a.n; j += kWave) s += hval(j);
+    const float mean = static_cast<float>(static_cast<double>(wave_sum(s)) / static_cast<double>(a.n));
+    float q = 0.f;
+    for (int j = lane; j < a.n; j += kWave) {
+      const float d = hval(j) - mean;
+      q = __builtin_fmaf(d, d, q);
+    }
+    const float var = static_cast<float>(static_cast<double>(wave_sum(q)) / static_cast<double>(a.n));
+    const float rstd = finish_rstd(var, a.eps);
+    // Every lane has read all of its elements before any lane writes: the sweeps above end in a
+    // wave-wide reduction, so in-place (y == x or y == res) is safe.
+    for (int j = lane; j < a.n; j += kWave) {
+      const float g = a.gamma ? a.gamma[j] : 1.f, b = a.beta ? a.beta[j] : 0.f;
+      S::store1(a.y, base + j, __builtin_fmaf((hval(j) - mean) * rstd, g, b));
+    }
+  }
+}
+
+// ---- GroupNorm(groups = channels) + GELU --------------------------------------------------------
+
+struct GnArgs {
+  const void* x;
+  const float* gamma;
+  const float* beta;
+  void* y;
+  long channels;
+  long T;
+  long ld;
+  double eps;
+  int gelu;
+};
+
+constexpr int kGnBlock = 1024;
+constexpr int kGnWaves = kGnBlock / kWave;
+
+__device__ __forceinline__ float gelu_erf(float v) {
+  return 0.5f * v * (1.f + erff(v * 0.70710678118654752440f));
+}
+
+// Sum of one double per thread over the 1024-thread block; every thread gets the same value.
+__device__ __forceinline__ double block_sum(double v, double* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kGnWaves; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+// Row held in VGPRs as raw 16-byte chunks (packed halves stay packed: 4 VGPRs per chunk for every
+// dtype): head elements up to the first 16-byte boundary, CPT chunks per thread, then tail
+// elements. x and y rows share their 16-byte phase (checked on the host).
+template <int DT>
+__device__ __forceinline__ void unpack(const uint4& q, float (&v)[Store<DT>::VEC]) {
+  if constexpr (DT == GSVK_F32) {
+    v[0] = __builtin_bit_cast(float, q.x);
+    v[1] = __builtin_bit_cast(float, q.y);
+    v[2] = __builtin_bit_cast(float, q.z);
+    v[3] = __builtin_bit_cast(float, q.w);
+  } else {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = Store<DT>::up(w[k] & 0xffffu);
+      v[2 * k + 1] = Store<DT>::up(w[k] >> 16);
+    }
+  }
+}
+
+template <int DT, int CPT>
+__global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  constexpr int ESZ = DT == GSVK_F32 ? 4 : 2;
+  __shared__ double red[kGnWaves];
+  const long ch = blockIdx.x;
+  const int t = threadIdx.x;
+  const size_t base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x) + base * ESZ;
+  long head = static_cast<long>(((16u - (addr & 15u)) & 15u) / ESZ);
+  if (head > a.T) head = a.T;
+  const long nbody = (a.T - head) / V;
+  const long tail = a.T - head - nbody * V;
+  const size_t body0 = base + head;  // element index of the first aligned chunk
+  const uint4* xb = reinterpret_cast<const uint4*>(static_cast<const char*>(a.x) + body0 * ESZ);
+
+  uint4 raw[CPT];
+  float e = 0.f;  // this thread's head/tail element, if any
+  long e_idx = -1;
+  if (t < head) e_idx = t;
+  else if (t < head + tail) e_idx = head + nbody * V + (t - head);
+
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGnBlock;
+    if (k < nbody) raw[c] = xb[k];
+    else raw[c] = make_uint4(0, 0, 0, 0);  // zero bits are 0.0 in every dtype
+  }
+  if (e_idx >= 0) e = S::load1(a.x, base + e_idx);
+  float s = e;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    float v[V];
+    unpack<DT>(raw[c], v);
+#pragma unroll
+    for (int i = 0; i < V; ++i) s += v[i];
+  }
+  const double mean_d = block_sum(static_cast<double>(s), red) / static_cast<double>(a.T);
+  const float mean = static_cast<float>(mean_d);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGnBlock;
+    if (k < nbody) {
+      float v[V];
+      unpack<DT>(raw[c], v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float d = v[i] - mean;
+        q = __builtin_fmaf(d, d, q);
+      }
+    }
+  }
+  if (e_idx >= 0) {
+    const float d = e - mean;
+    q = __builtin_fmaf(d, d, q);
+  }
+  // Centred on the fp32 mean, corrected by (mean_d - mean)^2 so the variance is about mean_d.
+  const double dm = mean_d - static_cast<double>(mean);
+  const double var = block_sum(static_cast<double>(q), red) / static_cast<double>(a.T) - dm * dm;
+  const float rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
+  const float g = a.gamma ? a.gamma[ch] : 1.f;
+  const float b = a.beta ? a.beta[ch] : 0.f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGnBlock;
+    if (k < nbody) {
+      float v[V], o[V];
+      unpack<DT>(raw[c], v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float y = __builtin_fmaf((v[i] - mean) * rstd, g, b);
+        o[i] = a.gelu ? gelu_erf(y) : y;
+      }
+      S::store(a.y, body0 + static_cast<size_t>(k) * V, o);
+    }
+  }
+  if (e_idx >= 0) {
+    const float y = __builtin_fmaf((e - mean) * rstd, g, b);
+    S::store1(a.y, base + e_idx, a.gelu ? gelu_erf(y) : y);
+  }
+}
+
+// Any T / alignment: three strided sweeps over the channel row.
+template <int DT>
+__global__ __launch_bounds__(kGnBlock) void gn_gelu_generic(GnArgs a) {
+  using S = Store<DT>;
+  __shared__ double red[kGnWaves];
+  const long ch = blockIdx.x;
+  const size_t base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
+  float s = 0.f;
+  for (long j = threadIdx.x; j < a.T; j += kGnBlock) s += S::load1(a.x, base + j);
+  const double mean_d = block_sum(static_cast<double>(s), red) / static_cast<double>(a.T);
+  const float mean = static_cast<float>(mean_d);
+  float q = 0.f;
+  for (long j = threadIdx.x; j < a.T; j += kGnBlock) {
+    const float d = S::load1(a.x, base + j) - mean;
+    q = __builtin_fmaf(d, d, q);
+  }
+  const double dm = mean_d - static_cast<double>(mean);
+  const double var = block_sum(static_cast<double>(q), red) / static_cast<double>(a.T) - dm * dm;
+  const float rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
+  const float g = a.gamma ? a.gamma[ch] : 1.f;
+  const float b = a.beta ? a.beta[ch] : 0.f;
+  // block_sum ends with a barrier after every thread's last read, so in-place writes are safe.
+  for (long j = threadIdx.x; j < a.T; j += kGnBlock) {
+    const float y = __builtin_fmaf((S::load1(a.x, base + j) - mean) * rstd, g, b);
+    S::store1(a.y, base + j, a.gelu ? gelu_erf(y) : y);
+  }
+}
+
+// ---- launchers ----------------------------------------------------------------------------------
+
+int ln_grid(long rows) {
+  // 2048 workgroups (8 per CU on 256 CUs) is enough to keep HBM busy; waves stride over the rest.
+  const long need = (rows + (kLnBlock / kWave) - 1) / (kLnBlock / kWave);
+  return static_cast<int>(need < 2048 ? need : 2048);
+}
+
+template <int DT>
+int launch_ln(const LnArgs& a, bool vec_ok, hipStream_t st) {
+  constexpr int V = Store<DT>::VEC;
+  const int grid = ln_grid(a.rows);
+  const int nch = a.n / V;
+  if (vec_ok) {
+    if (nch <= 1 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 1>), dim3(grid), dim3(kLnBlock), 0, st, a);
+    else if (nch <= 2 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 2>), dim3(grid), dim3(kLnBlock), 0, st, a);
+    else if (nch <= 4 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 4>), dim3(grid), dim3(kLnBlock), 0, st, a);
+    else if (nch <= 8 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 8>), dim3(grid), dim3(kLnBlock), 0, st, a);
+    else vec_ok = false;
+  }
+  if (!vec_ok) hipLaunchKernelGGL((ln_rows_generic<DT>), dim3(grid), dim3(kLnBlock), 0, st, a);
+  return launch_status();
+}
+
+template <int DT>
+int launch_gn(const GnArgs& a, bool vec_ok, hipStream_t st) {
+  constexpr int V = Store<DT>::VEC;
+  const dim3 grid(static_cast<unsigned>(a.channels));
+  const long nb = a.T / V + 1;  // upper bound on body chunks
+  if (vec_ok) {
+    if (nb <= 1L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 1>), grid, dim3(kGnBlock), 0, st, a);
+    else if (nb <= 2L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 2>), grid, dim3(kGnBlock), 0, st, a);
+    else if (nb <= 4L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 4>), grid, dim3(kGnBlock), 0, st, a);
+    else if (nb <= 8L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 8>), grid, dim3(kGnBlock), 0, st, a);
+    else vec_ok = false;
+  }
+  if (!vec_ok) hipLaunchKernelGGL((gn_gelu_generic<DT>), grid, dim3(kGnBlock), 0, st, a);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace gsvk
+
+using namespace gsvk;
+
+extern "C" int gsvk_add_layernorm(int dtype, const void* x, const float* bias, const void* residual,
+                                  const float* gamma, const float* beta, void* y, size_t rows,
+                                  size_t n, size_t ld, double eps, void* stream) {
+  if (!valid_dtype(dtype)) return GSVK_E_DTYPE;
+  if (!x || !y) return GSVK_E_NULL;
+  if (rows == 0 || n == 0 || ld < n || n > (1u << 30) || rows > (1ul << 40)) return GSVK_E_SIZE;
+  if (!(eps >= 0.0) || !std::isfinite(eps)) return GSVK_E_ARG;
+  const size_t esz = dtype_size(dtype);
+  const size_t span = span_bytes(rows, n, ld, esz);
+  // y may be exactly x or exactly residual; any other overlap with an input is rejected.
+  if (y != x && overlaps(y, span, x, span)) return GSVK_E_ALIAS;
+  if (residual && y != residual && overlaps(y, span, residual, span)) return GSVK_E_ALIAS;
+  for (const float* p : {bias, gamma, beta})
+    if (p && overlaps(y, span, p, n * sizeof(float))) return GSVK_E_ALIAS;
+
+  LnArgs a{x, bias, residual, gamma, beta, y, static_cast<long>(rows), static_cast<int>(n),
+           static_cast<long>(ld), eps};
+  const int V = dtype == GSVK_F32 ? 4 : 8;
+  bool vec_ok = (n % V == 0) && (ld % V == 0) && aligned16(x) && aligned16(y) &&
+                (!residual || aligned16(residual));
+  for (const float* p : {bias, gamma, beta}) vec_ok = vec_ok && (!p || aligned16(p));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case GSVK_F32: return launch_ln<GSVK_F32>(a, vec_ok, st);
+    case GSVK_F16: return launch_ln<GSVK_F16>(a, vec_ok, st);
+    default: return launch_ln<GSVK_BF16>(a, vec_ok, st);
+  }
+}
+
+extern "C" int gsvk_groupnorm_gelu(int dtype, const void* x, const float* gamma, const float* beta,
+                                   void* y, size_t channels, size_t T, size_t ld, double eps,
+                                   int apply_gelu, void* stream) {
+  if (!valid_dtype(dtype)) return GSVK_E_DTYPE;
+  if (!x || !y) return GSVK_E_NULL;
+  if (channels == 0 || T == 0 || ld < T || channels > 0x7fffffffu || T > (1ul << 40))
+    return GSVK_E_SIZE;
+  if (!(eps >= 0.0) || !std::isfinite(eps)) return GSVK_E_ARG;
+  const size_t esz = dtype_size(dtype);
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % esz) return GSVK_E_ARG;
+  const size_t span = span_bytes(channels, T, ld, esz);
+  if (y != x && overlaps(y, span, x, span)) return GSVK_E_ALIAS;
+  for (const float* p : {gamma, beta})
+    if (p && overlaps(y, span, p, channels * sizeof(float))) return GSVK_E_ALIAS;
+  GnArgs a{x, gamma, beta, y, static_cast<long>(channels), static_cast<long>(T),
+           static_cast<long>(ld), eps, apply_gelu ? 1 : 0};
+  // The register path needs x and y rows in the same 16-byte phase.
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) - reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case GSVK_F32: return launch_gn<GSVK_F32>(a, vec_ok, st);
+    case GSVK_F16: return launch_gn<GSVK_F16>(a, vec_ok, st);
+    default: return launch_gn<GSVK_BF16>(a, vec_ok, st);
+  }
+}

@@ -1,0 +1,191 @@
+// gsvk/kern.hpp — C++ host mirror of the reference's kernel-layer interface over the gsvk C ABI.
+//
+// The functions keep the reference's names, argument order and argument meaning so an engine's
+// call sites compile unchanged after swapping the include:
+//   gsv::kern::layernorm / relu                      (src/kern/kern.hpp:25, 33)
+//   gsv::sovits::leaky_relu_io / leaky_relu_write / add_inplace / add_scaled_inplace / mul_write
+//                                                    (src/sovits/nn_ops.hpp:48-105)
+//   gsv::bert::gelu_erf over a buffer                (src/bert/bert_ops.hpp:25-27, 394)
+// Differences, all deliberate: pointers are device pointers; every call is enqueued on the calling
+// thread's current stream (gsvk::set_stream) and returns before the GPU finishes (call
+// gsvk::sync() before reading results on the host); a rejected argument or a HIP launch failure
+// throws std::runtime_error (the reference's error style at load time, t2s_engine.cpp:559-562)
+// instead of being undefined behaviour. Row-batched forms (one launch per tensor) sit next to the
+// per-row ones, because a GPU call per row is the wrong granularity.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "gsvk.h"
+
+namespace gsvk {
+
+inline hipStream_t& current_stream_ref() {
+  static thread_local hipStream_t s = nullptr;
+  return s;
+}
+inline void set_stream(hipStream_t s) { current_stream_ref() = s; }
+inline hipStream_t current_stream() { return current_stream_ref(); }
+
+inline void check(int rc, const char* what) {
+  if (rc != GSVK_OK)
+    throw std::runtime_error(std::string(what) + ": " + gsvk_status_string(rc));
+}
+inline void sync() {
+  if (hipStreamSynchronize(current_stream()) != hipSuccess)
+    throw std::runtime_error("gsvk::sync: hipStreamSynchronize failed");
+}
+
+}  // namespace gsvk
+
+namespace gsv::kern {
+
+// y = (x - mean) / sqrt(var + eps) * g + b over one row of n floats (kern.hpp:25). y may be x.
+inline void layernorm(const float* x, const float* g, const float* b, float* y, size_t n,
+                      double eps) {
+  gsvk::check(gsvk_add_layernorm(GSVK_F32, x, nullptr, nullptr, g, b, y, 1, n, n, eps,
+                                 gsvk::current_stream()),
+              "gsv::kern::layernorm");
+}
+
+// The same over `rows` consecutive rows: one launch replaces the per-row loops at
+// t2s_engine.cpp:985-987 / hubert.cpp:701-703.
+inline void layernorm_rows(const float* x, const float* g, const float* b, float* y, size_t rows,
+                           size_t n, double eps) {
+  gsvk::check(gsvk_add_layernorm(GSVK_F32, x, nullptr, nullptr, g, b, y, rows, n, n, eps,
+                                 gsvk::current_stream()),
+              "gsv::kern::layernorm_rows");
+}
+
+// y = LN((mm + bias) + residual): the residual/bias loop and the LayerNorm that follows it
+// (t2s_engine.cpp:1096-1098, 1117-1119) in one launch.
+inline void add_layernorm(const float* mm, const float* bias, const float* residual, const float* g,
+                          const float* b, float* y, size_t rows, size_t n, double eps) {
+  gsvk::check(gsvk_add_layernorm(GSVK_F32, mm, bias, residual, g, b, y, rows, n, n, eps,
+                                 gsvk::current_stream()),
+              "gsv::kern::add_layernorm");
+}
+
+// y = max(x, 0) (kern.hpp:33).
+inline void relu(const float* x, float* y, size_t n) {
+  gsvk::check(gsvk_bias_act(GSVK_F32, GSVK_ACT_RELU, x, nullptr, y, 1, n, n, 0.f,
+                            gsvk::current_stream()),
+              "gsv::kern::relu");
+}
+
+// ff = relu(ff + b1) over [rows, n] (t2s_engine.cpp:995-996, 1111-1112).
+inline void bias_relu(float* ff, const float* b1, size_t rows, size_t n) {
+  gsvk::check(gsvk_bias_act(GSVK_F32, GSVK_ACT_RELU, ff, b1, ff, rows, n, n, 0.f,
+                            gsvk::current_stream()),
+              "gsv::kern::bias_relu");
+}
+
+}  // namespace gsv::kern
+
+namespace gsv::bert {
+
+// x = gelu_erf(x + bias) over [rows, n]; bias may be nullptr (bert_ops.hpp:255-257 then 394).
+inline void bias_gelu_erf(float* x, const float* bias, size_t rows, size_t n) {
+  gsvk::check(gsvk_bias_act(GSVK_F32, GSVK_ACT_GELU_ERF, x, bias, x, rows, n, n, 0.f,
+                            gsvk::current_stream()),
+              "gsv::bert::bias_gelu_erf");
+}
+
+// LayerNorm1D::forward on a [rows, cols] matrix in place, eps 1e-12 (bert_ops.hpp:261-286).
+inline void layernorm1d_forward(float* x, const float* g, const float* bta, size_t rows,
+                                size_t cols, float eps = 1e-12f) {
+  gsvk::check(gsvk_add_layernorm(GSVK_F32, x, nullptr, nullptr, g, bta, x, rows, cols, cols, eps,
+                                 gsvk::current_stream()),
+              "gsv::bert::layernorm1d_forward");
+}
+
+}  // namespace gsv::bert
+
+namespace gsv::encoder {
+
+// HuBERT conv layer 0: GroupNorm(groups = C) then GELU, in place on [C, T] (hubert.cpp:487-503).
+inline void groupnorm_gelu(float* x, const float* g, const float* b, size_t C, size_t T,
+                           double eps) {
+  gsvk::check(gsvk_groupnorm_gelu(GSVK_F32, x, g, b, x, C, T, T, eps, 1, gsvk::current_stream()),
+              "gsv::encoder::groupnorm_gelu");
+}
+
+// HubertEngine::gelu(float* x, size_t n) (hubert.cpp:233-236).
+inline void gelu(float* x, size_t n) {
+  gsvk::check(gsvk_bias_act(GSVK_F32, GSVK_ACT_GELU_ERF, x, nullptr, x, 1, n, n, 0.f,
+                            gsvk::current_stream()),
+              "gsv::encoder::gelu");
+}
+
+}  // namespace gsv::encoder
+
+namespace gsv::sovits {
+
+inline void leaky_relu_io(float* io, size_t n, float slope) {
+  gsvk::check(gsvk_leaky_relu(GSVK_F32, io, io, n, slope, gsvk::current_stream()),
+              "gsv::sovits::leaky_relu_io");
+}
+
+inline void leaky_relu_write(const float* src, float* dst, size_t n, float slope) {
+  gsvk::check(gsvk_leaky_relu(GSVK_F32, src, dst, n, slope, gsvk::current_stream()),
+              "gsv::sovits::leaky_relu_write");
+}
+
+inline void add_inplace(float* dst, const float* src, size_t n) {
+  gsvk::check(gsvk_resblock_add_lrelu(GSVK_F32, dst, src, nullptr, n, 0.f, gsvk::current_stream()),
+              "gsv::sovits::add_inplace");
+}
+
+inline void add_scaled_inplace(float* acc, const float* src, size_t n, float scale) {
+  gsvk::check(gsvk_scaled_add(GSVK_F32, acc, src, acc, n, scale, gsvk::current_stream()),
+              "gsv::sovits::add_scaled_inplace");
+}
+
+inline void mul_write(float* dst, const float* src, size_t n, float scale) {
+  gsvk::check(gsvk_scaled_add(GSVK_F32, nullptr, src, dst, n, scale, gsvk::current_stream()),
+              "gsv::sovits::mul_write");
+}
+
+// cur += t_b; t_in = lrelu(cur, slope): add_inplace (dec.hpp:326) fused with the next conv pair's
+// leaky_relu_write (dec.hpp:322).
+inline void add_then_leaky_write(float* cur, const float* t_b, float* t_in, size_t n, float slope) {
+  gsvk::check(gsvk_resblock_add_lrelu(GSVK_F32, cur, t_b, t_in, n, slope, gsvk::current_stream()),
+              "gsv::sovits::add_then_leaky_write");
+}
+
+// x_next = lrelu(sum_j (cur_j + t_b_j) / 3, slope): the end of a Generator stage (dec.hpp:326-336)
+// fused with the next stage's leaky_relu_io (dec.hpp:284 / 342).
+inline void branch_mean_leaky(const float* const cur[3], const float* const t_b[3], float* x_next,
+                              size_t n, float slope) {
+  const void* c[3] = {cur[0], cur[1], cur[2]};
+  const void* t[3] = {t_b ? t_b[0] : nullptr, t_b ? t_b[1] : nullptr, t_b ? t_b[2] : nullptr};
+  gsvk::check(gsvk_resblock_branch_mean(GSVK_F32, c, t, 3, x_next, n, 1, slope,
+                                        gsvk::current_stream()),
+              "gsv::sovits::branch_mean_leaky");
+}
+
+}  // namespace gsv::sovits
+
+namespace gsv::ar {
+
+// T2SEngine::pe_row for every position 0..max_pos-1 into host memory (t2s_engine.cpp:711-720).
+inline void pe_table(float* host_out, size_t max_pos, size_t d_model) {
+  gsvk::check(gsvk_pe_table(host_out, max_pos, d_model), "gsv::ar::pe_table");
+}
+
+// x[r] = e[id_r] + alpha * pe[pos_r] over B rows (t2s_engine.cpp:1781-1786, 1866-1869).
+inline void embed_pe(const uint16_t* table_f16, size_t vocab, const int64_t* ids,
+                     const int64_t* pos, const float* pe, size_t max_pos, float alpha, float* x,
+                     size_t rows, size_t D, int32_t* err = nullptr) {
+  gsvk::check(gsvk_embed_pe(GSVK_F32, GSVK_F16, GSVK_I64, table_f16, vocab, ids, pos, 0, pe,
+                            max_pos, alpha, nullptr, nullptr, x, rows, D, err,
+                            gsvk::current_stream()),
+              "gsv::ar::embed_pe");
+}
+
+}  // namespace gsv::ar

@@ -1,0 +1,171 @@
+/*
+ * gsvk.h — C ABI of the MI355X (gfx950) fused layer kernels for GPT-SoVITS-native.
+ *
+ * Every entry point enqueues work on a HIP stream and returns without waiting. Pointers named
+ * "device" must be device-accessible memory (hipMalloc or equivalent); all sizes are element counts.
+ * The stream argument is a hipStream_t passed as void* (NULL = the legacy default stream), so the
+ * header needs no HIP include and binds directly from ctypes / cgo / JNI.
+ *
+ * Status: every function returns GSVK_OK (0) or a negative gsvk_status. Argument checks happen on the
+ * host before anything is launched, so a rejected call leaves the stream untouched.
+ *
+ * Storage vs math: activations are stored as f32, f16 or bf16 (gsvk_dtype); all arithmetic is fp32
+ * (fp64 where the reference finalizes in double) and results are rounded to the storage type once,
+ * round-to-nearest-even. Per-column parameters (gamma, beta, bias) and the PE table are always fp32,
+ * as the reference keeps them (t2s_engine.cpp:615-626, hubert.cpp:135-139).
+ *
+ * Aliasing: y == x (exact same pointer, same layout) is allowed wherever the reference calls the
+ * primitive in place; any other overlap between an output and an input is rejected (GSVK_E_ALIAS).
+ */
+#ifndef GSVK_H
+#define GSVK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum gsvk_dtype {
+  GSVK_F32 = 0,
+  GSVK_F16 = 1,
+  GSVK_BF16 = 2,
+} gsvk_dtype;
+
+typedef enum gsvk_index_type {
+  GSVK_I64 = 0, /* int64_t ids, as T2SEngine::generate takes them (t2s_engine.hpp:114-115) */
+  GSVK_I32 = 1, /* int32_t ids, as the sampler returns them (t2s_engine.hpp:168-175) */
+} gsvk_index_type;
+
+typedef enum gsvk_act {
+  GSVK_ACT_NONE = 0,       /* y = x + bias                                         */
+  GSVK_ACT_RELU = 1,       /* kern::relu after the bias pass (kern.cpp:85-91)      */
+  GSVK_ACT_GELU_ERF = 2,   /* bert::gelu_erf / HubertEngine::gelu (bert_ops.hpp:25-27) */
+  GSVK_ACT_LEAKY_RELU = 3, /* sovits::leaky_relu_write semantics (nn_ops.hpp:64-74) */
+} gsvk_act;
+
+typedef enum gsvk_status {
+  GSVK_OK = 0,
+  GSVK_E_NULL = -1,   /* a required pointer is NULL                                  */
+  GSVK_E_SIZE = -2,   /* zero or out-of-range size, or ld < n                         */
+  GSVK_E_DTYPE = -3,  /* unknown dtype / index type / activation                      */
+  GSVK_E_ALIAS = -4,  /* output overlaps an input other than the allowed exact alias  */
+  GSVK_E_ARG = -5,    /* other invalid argument (negative or non-finite eps, odd D, …) */
+  GSVK_E_HIP = -6,    /* the HIP runtime reported an error at launch                  */
+} gsvk_status;
+
+/* Library identification and error text (host only, no GPU needed). */
+const char* gsvk_version(void);
+const char* gsvk_status_string(int status);
+
+/* ------------------------------------------------------------------------------------------------
+ * Residual add + LayerNorm over rows.
+ *   h[r,c] = (x[r,c] + bias[c]) + residual[r,c]        (bias / residual may be NULL)
+ *   y[r,c] = (h - mean_r) * rstd_r * gamma[c] + beta[c] (gamma / beta may be NULL: 1 / 0)
+ * mean and biased variance per row; rstd = 1/sqrt(var + eps) finalized in double.
+ * Replaces gsv::kern::layernorm(const float* x, const float* g, const float* b, float* y, size_t n,
+ * double eps) (src/kern/kern.hpp:25, kern.cpp:27-59) called once per row, together with the residual
+ * and bias loops that feed it: T2S prefill t2s_engine.cpp:980-987 and 1018-1025, decode 1096-1098
+ * and 1117-1119, HuBERT hubert.cpp:697-703 and 725-731, and bert::LayerNorm1D::forward
+ * (src/bert/bert_ops.hpp:261-286, eps 1e-12) after the residual add at bert_ops.hpp:389 and 397.
+ * Layout: row-major [rows, n] with row stride ld >= n (elements) shared by x, residual and y.
+ * y == x and y == residual are allowed (in place).
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_add_layernorm(int dtype, const void* x, const float* bias, const void* residual,
+                       const float* gamma, const float* beta, void* y, size_t rows, size_t n,
+                       size_t ld, double eps, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Bias + activation epilogue over rows: y[r,c] = act(x[r,c] + bias[c]).
+ * Replaces the bias loop + gsv::kern::relu(const float* x, float* y, size_t n) (kern.hpp:33,
+ * kern.cpp:85-91; t2s_engine.cpp:995-996, 1111-1112), the Linear bias + bert::gelu_erf pass
+ * (bert_ops.hpp:25-27, 255-257, 394), and HubertEngine::gelu after the f1 bias (hubert.cpp:233-236,
+ * 714-716). bias may be NULL. slope is used by GSVK_ACT_LEAKY_RELU only. y == x allowed.
+ * ReLU keeps NaN and maps -0 to +0 (vmaxq_f32 semantics); LeakyReLU keeps -0 and NaN.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_bias_act(int dtype, int act, const void* x, const float* bias, void* y, size_t rows,
+                  size_t n, size_t ld, float slope, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * GroupNorm with one group per channel, optionally followed by GELU(erf).
+ *   mean_c, var_c over the T frames of channel c (biased); y = (x - mean)*rstd*gamma[c] + beta[c];
+ *   y = gelu_erf(y) when apply_gelu != 0.
+ * Replaces the HuBERT conv-layer-0 GroupNorm loop and the GELU pass after it
+ * (src/encoder/hubert.cpp:487-503). Layout: channel-major [channels, T] with channel stride ld >= T.
+ * gamma / beta may be NULL (1 / 0). y == x allowed.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_groupnorm_gelu(int dtype, const void* x, const float* gamma, const float* beta, void* y,
+                        size_t channels, size_t T, size_t ld, double eps, int apply_gelu,
+                        void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * LeakyReLU over a flat buffer: y[k] = x[k] < 0 ? x[k]*slope : x[k].
+ * x == y is sovits::leaky_relu_io (nn_ops.hpp:48-59); x != y is leaky_relu_write (nn_ops.hpp:64-74).
+ * Call sites: Generator::forward stage entry and final slope 0.01 (dec.hpp:284, 342), ResBlock
+ * pre-conv (dec.hpp:322, 324).
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_leaky_relu(int dtype, const void* x, void* y, size_t n, float slope, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * ResBlock residual step: cur[k] += t_b[k]; then, if t_in != NULL, t_in[k] = lrelu(cur[k], slope).
+ * Fuses sovits::add_inplace (nn_ops.hpp:77-83; dec.hpp:326) with the next conv pair's
+ * leaky_relu_write (dec.hpp:322; batched prepare hook dec.hpp:226-228).
+ * cur, t_b and t_in must not overlap (the reference marks them __restrict).
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_resblock_add_lrelu(int dtype, void* cur, const void* t_b, void* t_in, size_t n,
+                            float slope, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * ResBlock branch average (+ the next stage's LeakyReLU):
+ *   v_j = cur[j][k] (+ t_b[j][k] when t_b != NULL and t_b[j] != NULL),  kinv = 1.f / nbranch
+ *   s = v_0 * kinv;  s = s + v_j * kinv  for j = 1..nbranch-1   (multiply and add rounded separately)
+ *   out[k] = apply_lrelu ? lrelu(s, slope) : s
+ * Fuses the last add_inplace of each branch, sovits::mul_write / add_scaled_inplace
+ * (nn_ops.hpp:86-105; dec.hpp:328-333, batched dec.hpp:247-254) and the next stage's
+ * leaky_relu_io (dec.hpp:284, slope 0.1; dec.hpp:342, slope 0.01). nbranch in 1..4 (the reference
+ * uses 3). out must not overlap any input.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_resblock_branch_mean(int dtype, const void* const* cur, const void* const* t_b,
+                              int nbranch, void* out, size_t n, int apply_lrelu, float slope,
+                              void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Scaled accumulate: out[k] = acc ? acc[k] + src[k]*scale : src[k]*scale (multiply and add rounded
+ * separately). acc == out is sovits::add_scaled_inplace (nn_ops.hpp:86-95); acc == NULL is
+ * sovits::mul_write (nn_ops.hpp:98-105). out must not overlap src; acc is either out or disjoint.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_scaled_add(int dtype, const void* acc, const void* src, void* out, size_t n, float scale,
+                    void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Token-embedding gather fused with the scaled sinusoidal positional add, bit-exact.
+ *   p = pos ? pos[r] : pos0 + r
+ *   e = float(table[id_r, :])                           (exact upcast of f16 / bf16 / f32 rows)
+ *   without mm:  out[r, :] = fmaf(alpha, pe[p, :], e (+ bias))                 (audio / decode)
+ *   with mm:     out[r, :] = fmaf(alpha, pe[p, :], mm[r, :] + (e (+ bias)))    (text rows)
+ * Replaces the T2S input rebuild loops: text rows t2s_engine.cpp:1774-1780, prompt rows 1781-1786,
+ * the decode-step input 1866-1869, with the PE row of T2SEngine::pe_row (t2s_engine.cpp:711-720)
+ * read from a table made by gsvk_pe_table. An id outside [0, vocab) or a position outside
+ * [0, max_pos) (undefined behaviour in the reference) writes a NaN row and, when err != NULL,
+ * stores 1 into *err (device int32); nothing is read out of bounds.
+ * Layout: table [vocab, D] (table_dtype), pe [max_pos, D] f32, mm / out [rows, D] (out_dtype),
+ * bias [D] f32 (or NULL). D must be even.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_embed_pe(int out_dtype, int table_dtype, int index_type, const void* table, size_t vocab,
+                  const void* ids, const int64_t* pos, int64_t pos0, const float* pe,
+                  size_t max_pos, float alpha, const void* mm, const float* bias, void* out,
+                  size_t rows, size_t D, int32_t* err, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Host helper: the sinusoidal PE table, row p = T2SEngine::pe_row(pe, p) (t2s_engine.cpp:711-720):
+ *   log_inc = float(-ln(10000)/D); div = expf(float(d)*log_inc); pe[2i] = sinf(p*div),
+ *   pe[2i+1] = cosf(p*div), all in fp32. host_out holds max_pos * D floats. Host memory, no GPU.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_pe_table(float* host_out, size_t max_pos, size_t D);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSVK_H */

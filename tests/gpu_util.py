@@ -1,0 +1,86 @@
+"""Helpers for the GPU parity tests: host <-> device transfer of storage arrays and the comparison
+rules. Tolerances are the ones the target states for this path:
+  bit-exact ops (gathers, ReLU, LeakyReLU, residual add, branch mean, bias + ReLU): equal bits,
+      NaN compared as NaN;
+  fp32 norms / activations: |got - want| <= 1e-6 + 1e-5 * |want|;
+  fp16 storage: |got - want| <= 2e-3, or one fp16 step of `want` where that step is larger
+      (|want| >= 4, where a single rounding step is 3.9e-3);
+  bf16 storage: |got - want| <= 2e-3, or one bf16 step of `want` where that step is larger.
+"""
+import sys
+
+import numpy as np
+import torch
+
+import oracle as O
+
+F32, F16, BF16 = O.F32, O.F16, O.BF16
+TORCH_DT = {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}
+ALL_DT = (F32, F16, BF16)
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(arr, dt):
+    """numpy storage array -> CUDA tensor of the storage dtype (same bits)."""
+    a = np.ascontiguousarray(arr)
+    if dt == F32:
+        t = torch.from_numpy(a.astype(np.float32, copy=False))
+    else:
+        t = torch.from_numpy(a.view(np.int16)).view(TORCH_DT[dt])
+    return t.cuda()
+
+
+def devf(arr):
+    return torch.from_numpy(np.ascontiguousarray(arr, dtype=np.float32)).cuda()
+
+
+def host(t, dt):
+    t = t.detach().cpu().contiguous()
+    if dt == F32:
+        return t.numpy().copy()
+    return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def bits(dt, a):
+    return a.view(np.uint32) if dt == F32 else a.view(np.uint16)
+
+
+def assert_bitexact(dt, got, want, what=""):
+    g32, w32 = O.to_f32(dt, got), O.to_f32(dt, want)
+    gn, wn = np.isnan(g32), np.isnan(w32)
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
+    gb, wb = bits(dt, got)[~gn], bits(dt, want)[~wn]
+    bad = np.flatnonzero(gb != wb)
+    assert bad.size == 0, f"{what}: {bad.size} elements differ, first {bad[:5]}: " \
+                          f"{g32[~gn][bad[:5]]} vs {w32[~wn][bad[:5]]}"
+
+
+def tol(dt, w):
+    w = np.abs(w.astype(np.float64))
+    if dt == F32:
+        return 1e-6 + 1e-5 * w
+    if dt == F16:
+        step = np.spacing(np.minimum(w, 65504).astype(np.float16)).astype(np.float64)
+    else:
+        e = np.floor(np.log2(np.maximum(w, 2.0 ** -126)))
+        step = 2.0 ** (e - 7)
+    return np.maximum(2e-3, step)
+
+
+def assert_close(dt, got, want, what=""):
+    g = O.to_f32(dt, got).astype(np.float64)
+    w = O.to_f32(dt, want).astype(np.float64)
+    gn, wn = np.isnan(g), np.isnan(w)
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
+    err = np.abs(g - w)
+    t = tol(dt, w)
+    err[gn] = 0
+    bad = np.flatnonzero(err > t)
+    assert bad.size == 0, f"{what}: {bad.size}/{g.size} out of tolerance, worst " \
+                          f"{err.ravel()[bad].max():.3e} at {bad[:3]} got {g.ravel()[bad[:3]]} " \
+                          f"want {w.ravel()[bad[:3]]}"
+    return float(err.max()) if err.size else 0.0

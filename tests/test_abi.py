@@ -1,0 +1,151 @@
+"""The C ABI on the CPU: libgsvk.so loads, exports every function include/*.h declares, host-only
+helpers work, and argument validation rejects bad calls before anything reaches a GPU (every call
+here fails validation or is host-only, so no device is needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+import gsvk
+
+
+def _declared_functions():
+    names = []
+    for h in ("gsvk.h", "gsvk_t2s.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(gsvk_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol(gsvk_lib):
+    declared = _declared_functions()
+    assert len(declared) >= 16
+    out = subprocess.run(["nm", "-D", "--defined-only", gsvk.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (gsvk_\w+)", out))
+    missing = [n for n in declared if n not in exported]
+    assert not missing, missing
+    assert set(declared) == set(gsvk.SIGNATURES), "binding table out of sync with the headers"
+
+
+def test_version_and_status_strings(gsvk_lib):
+    assert b"gfx950" in gsvk_lib.gsvk_version()
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert gsvk_lib.gsvk_status_string(code)
+    assert gsvk_lib.gsvk_status_string(-99) == b"unknown status"
+
+
+def test_pe_table_host_builder_matches_oracle_bitwise(gsvk_lib):
+    import oracle as O
+    got = gsvk.pe_table(2048, 512)
+    want = O.pe_table(2048, 512)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert gsvk_lib.gsvk_pe_table(None, 4, 4) == gsvk.E_NULL
+    buf = np.empty(12, np.float32)
+    assert gsvk_lib.gsvk_pe_table(buf.ctypes.data, 4, 3) == gsvk.E_ARG  # odd D
+    assert gsvk_lib.gsvk_pe_table(buf.ctypes.data, 0, 4) == gsvk.E_SIZE
+
+
+# Fake, never-dereferenced addresses: validation must reject these calls before any launch.
+A, B, C = 0x100000, 0x200000, 0x300000
+
+
+def test_layernorm_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_add_layernorm
+    assert f(7, A, None, None, None, None, B, 4, 8, 8, 1e-5, None) == gsvk.E_DTYPE
+    assert f(0, None, None, None, None, None, B, 4, 8, 8, 1e-5, None) == gsvk.E_NULL
+    assert f(0, A, None, None, None, None, None, 4, 8, 8, 1e-5, None) == gsvk.E_NULL
+    assert f(0, A, None, None, None, None, B, 0, 8, 8, 1e-5, None) == gsvk.E_SIZE
+    assert f(0, A, None, None, None, None, B, 4, 0, 8, 1e-5, None) == gsvk.E_SIZE
+    assert f(0, A, None, None, None, None, B, 4, 8, 7, 1e-5, None) == gsvk.E_SIZE  # ld < n
+    assert f(0, A, None, None, None, None, B, 4, 8, 8, -1.0, None) == gsvk.E_ARG
+    assert f(0, A, None, None, None, None, B, 4, 8, 8, float("nan"), None) == gsvk.E_ARG
+    # partial overlap of y with x (y == x is allowed, y == x + 4 bytes is not)
+    assert f(0, A, None, None, None, None, A + 4, 4, 8, 8, 1e-5, None) == gsvk.E_ALIAS
+    assert f(0, A, None, B, None, None, B + 16, 4, 8, 8, 1e-5, None) == gsvk.E_ALIAS
+    assert f(0, A, None, None, C, None, C - 8, 4, 8, 8, 1e-5, None) == gsvk.E_ALIAS  # gamma
+
+
+def test_epilogue_validation(gsvk_lib):
+    L = gsvk_lib
+    assert L.gsvk_bias_act(0, 9, A, None, B, 1, 8, 8, 0.0, None) == gsvk.E_DTYPE
+    assert L.gsvk_bias_act(0, 1, A, None, A + 4, 1, 8, 8, 0.0, None) == gsvk.E_ALIAS
+    assert L.gsvk_bias_act(1, 1, A + 1, None, B, 1, 8, 8, 0.0, None) == gsvk.E_ARG  # misaligned f16
+    assert L.gsvk_leaky_relu(0, A, B, 0, 0.1, None) == gsvk.E_SIZE
+    assert L.gsvk_leaky_relu(0, A, A + 8, 16, 0.1, None) == gsvk.E_ALIAS
+    assert L.gsvk_resblock_add_lrelu(0, A, None, None, 8, 0.1, None) == gsvk.E_NULL
+    assert L.gsvk_resblock_add_lrelu(0, A, A, None, 8, 0.1, None) == gsvk.E_ALIAS
+    assert L.gsvk_resblock_add_lrelu(0, A, B, A + 4, 8, 0.1, None) == gsvk.E_ALIAS
+    vp = ctypes.c_void_p
+    curs = (vp * 3)(A, B, C)
+    assert L.gsvk_resblock_branch_mean(0, curs, None, 0, 0x400000, 8, 1, 0.1, None) == gsvk.E_ARG
+    assert L.gsvk_resblock_branch_mean(0, curs, None, 5, 0x400000, 8, 1, 0.1, None) == gsvk.E_ARG
+    assert L.gsvk_resblock_branch_mean(0, curs, None, 3, B + 4, 8, 1, 0.1, None) == gsvk.E_ALIAS
+    assert L.gsvk_resblock_branch_mean(0, None, None, 3, B, 8, 1, 0.1, None) == gsvk.E_NULL
+    assert L.gsvk_scaled_add(0, None, A, A, 8, 0.5, None) == gsvk.E_ALIAS
+    assert L.gsvk_scaled_add(0, B + 4, A, B, 8, 0.5, None) == gsvk.E_ALIAS
+    assert L.gsvk_groupnorm_gelu(0, A, None, None, B, 0, 8, 8, 1e-5, 1, None) == gsvk.E_SIZE
+    assert L.gsvk_groupnorm_gelu(0, A, None, None, A + 4, 2, 8, 8, 1e-5, 1, None) == gsvk.E_ALIAS
+
+
+def test_embed_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_embed_pe
+    args = dict(out=0, tab=1, it=0, table=A, vocab=10, ids=B, pos=None, pos0=0, pe=C, max_pos=4,
+                alpha=1.0, mm=None, bias=None, outp=0x900000, rows=2, D=8, err=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return f(a["out"], a["tab"], a["it"], a["table"], a["vocab"], a["ids"], a["pos"],
+                 a["pos0"], a["pe"], a["max_pos"], a["alpha"], a["mm"], a["bias"], a["outp"],
+                 a["rows"], a["D"], a["err"], None)
+
+    assert call(it=5) == gsvk.E_DTYPE
+    assert call(table=None) == gsvk.E_NULL
+    assert call(rows=0) == gsvk.E_SIZE
+    assert call(D=7) == gsvk.E_ARG
+    assert call(outp=A) == gsvk.E_ALIAS          # writes over the table
+    assert call(outp=C + 16) == gsvk.E_ALIAS     # writes over the PE table
+
+
+def test_t2s_step_validation(gsvk_lib):
+    out = ctypes.c_void_p()
+    assert gsvk_lib.gsvk_t2s_step_create(None, ctypes.byref(out)) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_t2s_step_eager(None, None) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_t2s_step_run(None, None) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_t2s_step_launches(None) == 0
+    gsvk_lib.gsvk_t2s_step_destroy(None)
+
+
+def test_host_mirror_header_compiles(tmp_path):
+    """host/gsvk/kern.hpp (the reference-named C++ API) compiles against the C ABI, and a call
+    site written like the reference's (kern.hpp:25, 33; nn_ops.hpp:48-105) compiles unchanged."""
+    src = r'''
+#include <gsvk/kern.hpp>
+void engine_like(float* x, const float* g, const float* b, float* ff, float* cur, const float* tb,
+                 float* tin, float* sum) {
+  gsv::kern::layernorm(x, g, b, x, 512, 1e-5);
+  gsv::kern::relu(ff, ff, 2048);
+  gsv::sovits::leaky_relu_io(cur, 1000, 0.1f);
+  gsv::sovits::leaky_relu_write(cur, tin, 1000, 0.1f);
+  gsv::sovits::add_inplace(cur, tb, 1000);
+  gsv::sovits::mul_write(sum, cur, 1000, 1.f / 3);
+  gsv::sovits::add_scaled_inplace(sum, cur, 1000, 1.f / 3);
+  gsv::bert::layernorm1d_forward(x, g, b, 4, 1024);
+  gsv::encoder::groupnorm_gelu(x, g, b, 512, 31999, 1e-5);
+}
+'''
+    path = str(tmp_path / "compat_probe.cpp")
+    open(path, "w").write(src)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "gpt-sovits-native_amd", "host"),
+           "-I", "/opt/rocm/include"]
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-fsyntax-only", "-x", "c++",
+                        "-D__HIP_PLATFORM_AMD__", *inc, path], capture_output=True, text=True)
+    if r.returncode != 0 and "No such file" in r.stderr and "hipcc" in r.stderr:
+        pytest.skip("hipcc not available")
+    assert r.returncode == 0, r.stderr[-2000:]
