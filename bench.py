@@ -12,12 +12,16 @@ Also reported (same JSON line):
   roofline      the dominant kernel of the step (residual+LayerNorm [64,512]) — bytes per launch
                 over its average launch duration from HIP events, against 8 TB/s;
   cpu_baseline  the oracle's C restatement of the same step on the host cores;
-  kernels       every fused kernel of the configurations at its stated shape (single call) and as a
-                replicated batch of independent instances (> 1 GB moved, MALL flushed between
-                repetitions), in GB/s and fraction of 8 TB/s.
+  kernels       every fused kernel of the configurations at its stated shape (device time per launch
+                in a graph of back-to-back launches, inputs cache-resident) and as a replicated
+                batch of independent instances (> 0.4 GB moved, the 256 MB MALL cleared between
+                repetitions by reading a 512 MiB buffer), in GB/s and fraction of 8 TB/s;
+  copy_GBps     a plain device-to-device copy of 1 GiB measured the same way (achievable-bandwidth
+                reference for the replicated figures).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
-       python bench.py --only KERNEL   (one kernel's replicated launch loop, for rocprofv3 runs)
+       python bench.py --only KERNEL   (one kernel of the suite, for rocprofv3 runs)
+       python bench.py --pmc           (dominant kernel + a 256 MiB copy, for rocprofv3 --pmc runs)
 """
 import argparse
 import json
@@ -55,6 +59,12 @@ def bias_act_bytes(rows, n, esz, bias=True):
 
 def embed_bytes(rows, d, out_esz, tab_esz, id_esz=8, per_row_pos=True):
     return rows * (id_esz + (8 if per_row_pos else 0) + d * tab_esz + d * 4 + d * out_esz)
+
+
+def embed_unique_bytes(rows, d, out_esz, tab_esz, vocab=VOCAB, max_pos=MAX_POS):
+    """HBM floor of a gather over one shared table: ids, positions and output rows once per row,
+    the table and the PE table once (their rows repeat and are served from L2 / MALL)."""
+    return rows * (8 + 8 + d * out_esz) + vocab * d * tab_esz + max_pos * d * 4
 
 
 def gn_bytes(C, T, esz):
@@ -127,14 +137,17 @@ def graph_of(torch, fn, n):
 # ---- per-kernel suite ------------------------------------------------------------------------------
 
 class Flusher:
-    """Writes a 512 MiB scratch buffer between timed repetitions so the 256 MB MALL holds none of
-    the kernel's inputs."""
+    """Reads a 512 MiB buffer between timed repetitions so the 256 MB MALL holds none of the
+    kernel's inputs. A read, not a write: a written flush buffer leaves dirty MALL lines whose
+    write-back then runs inside the timed kernel (measured on MI355X: it halves a 64 MB read)."""
 
     def __init__(self, torch, dev):
-        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        self.torch = torch
+        self.buf = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+        self.out = torch.empty((), dtype=torch.float32, device=dev)
 
     def __call__(self):
-        self.buf.fill_(1)
+        self.torch.sum(self.buf, 0, out=self.out)
 
 
 def measure_reps(torch, fn, flush, reps=9):
@@ -153,8 +166,17 @@ def measure_reps(torch, fn, flush, reps=9):
     return statistics.median(times)
 
 
+def graph_us_per_launch(torch, fn, launches=32, replays=10):
+    """Device time per launch: a graph of `launches` back-to-back calls, replayed `replays` times
+    between HIP events on the launch stream."""
+    gr = graph_of(torch, fn, launches)
+    us = time_loop(torch, gr.replay, replays) * 1e3 / launches
+    del gr
+    return us
+
+
 def kernel_suite(torch, gsvk, dev, only=None):
-    """Each fused kernel at its stated shape and as a replicated batch (> 1 GB moved)."""
+    """Each fused kernel at its stated shape and as a replicated batch."""
     f16, f32 = torch.float16, torch.float32
     g = torch.Generator(device=dev).manual_seed(SEED)
     flush = Flusher(torch, dev)
@@ -164,25 +186,29 @@ def kernel_suite(torch, gsvk, dev, only=None):
         t = torch.empty(*shape, dtype=f32, device=dev).normal_(mean, std, generator=g)
         return t.to(dtype)
 
-    def run(name, cfg, stated, replicated, bytes_fn, count):
-        """stated / replicated: (setup -> launch fn) builders taking a replication factor."""
+    def run(name, cfg, stated, replicated, bytes_fn, count, rep_bytes_fn=None):
+        """stated / replicated: (setup -> launch fn) builders taking a replication factor.
+        rep_bytes_fn: HBM-unique bytes of the replicated launch when they differ from
+        bytes_fn (the gather re-reads shared tables from cache)."""
         if only and only != name:
             return
         rec = {"kernel": name, "config": cfg}
         fn1 = stated()
-        ms1 = time_loop(torch, fn1, 50)
-        rec["stated_shape"] = {"us": round(ms1 * 1e3, 3), "bytes": bytes_fn(1),
-                               "GBps": round(bytes_fn(1) / ms1 / 1e6, 1), "calls_per_config": count}
+        us1 = graph_us_per_launch(torch, fn1)
+        rec["stated_shape"] = {"us_per_launch": round(us1, 3), "bytes": bytes_fn(1),
+                               "GBps": round(bytes_fn(1) / us1 / 1e3, 1),
+                               "calls_per_config": count}
         del fn1
         rep, fnr = replicated()
         msr = measure_reps(torch, fnr, flush)
-        gbs = bytes_fn(rep) / msr / 1e6
-        rec["replicated"] = {"instances": rep, "bytes": bytes_fn(rep), "us": round(msr * 1e3, 2),
+        rb = (rep_bytes_fn or bytes_fn)(rep)
+        gbs = rb / msr / 1e6
+        rec["replicated"] = {"instances": rep, "bytes": rb, "us": round(msr * 1e3, 2),
                              "GBps": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
         del fnr
         torch.cuda.empty_cache()
         out.append(rec)
-        log(f"  {name}: stated {rec['stated_shape']['us']} us, replicated "
+        log(f"  {name}: stated {rec['stated_shape']['us_per_launch']} us, replicated "
             f"{rec['replicated']['GBps']} GB/s ({100 * gbs / PEAK_GBS:.1f}%)")
 
     def ln_case(rows, n, dt, eps, bias, res, rep):
@@ -216,10 +242,15 @@ def kernel_suite(torch, gsvk, dev, only=None):
             pos = torch.randint(0, MAX_POS, (rows * k,), device=dev, generator=g)
             o = torch.empty(rows * k, D, dtype=f16, device=dev)
             return lambda: gsvk.embed_pe(tab, ids, pe, 0.93, o, pos=pos)
-        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: embed_bytes(rows * k, D, 2, 2))
+        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: embed_bytes(rows * k, D, 2, 2),
+                lambda k: embed_unique_bytes(rows * k, D, 2, 2))
 
-    run("embed_pe_prefill_1024x512", 2, *emb_case(1024, 512), 1)
-    run("embed_pe_decode_64x512", 2, *emb_case(64, 8192), 1)
+    def run_emb(name, rows, rep):
+        st_, rp_, b_, ub_ = emb_case(rows, rep)
+        run(name, 2, st_, rp_, b_, 1, rep_bytes_fn=ub_)
+
+    run_emb("embed_pe_prefill_1024x512", 1024, 512)
+    run_emb("embed_pe_decode_64x512", 64, 8192)
     run("residual_layernorm_f16_64x512", 2, *ln_case(64, 512, f16, 1e-5, True, True, 8192), 48)
     run("bias_relu_f16_64x2048", 2, *ba_case(64, 2048, gsvk.ACT_RELU, 4096), 24)
     # config 3: bias + GELU [512, 4096], residual + LN(1024, eps 1e-12)
@@ -297,6 +328,96 @@ def cpu_baseline(torch, bufs, budget_s=8.0):
     return res, threads_all
 
 
+# ---- decode-step ops, copy reference, counter workload ---------------------------------------------
+
+def step_ops(gsvk, bufs):
+    """Layer-0 launches of the step's three ops (residual+LN, bias+ReLU, gather+PE)."""
+    x, h = bufs["x"], bufs["h"]
+    L0 = lambda: gsvk.add_layernorm(bufs["attn_out"][0], bufs["n1g"][0], bufs["n1b"][0], h, 1e-5,
+                                    bias=bufs["bout"][0], residual=x)
+    R0 = lambda: gsvk.bias_act(gsvk.ACT_RELU, bufs["ff"][0], bufs["ff"][0], bias=bufs["b1"][0])
+    E0 = lambda: gsvk.embed_pe(bufs["table"], bufs["ids"], bufs["pe"], bufs["alpha"], x,
+                               pos=bufs["pos"], err=bufs["err"])
+    return L0, R0, E0
+
+
+def copy_bandwidth(torch, dev, nbytes=1 << 30):
+    """A plain device-to-device copy of 1 GiB (read + write counted), timed like the replicated
+    kernels: the achievable-bandwidth reference of this GPU under the same method."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    ms = measure_reps(torch, lambda: dst.copy_(src), Flusher(torch, dev))
+    del src, dst
+    torch.cuda.empty_cache()
+    gbs = 2 * nbytes / ms / 1e6
+    log(f"  copy 1 GiB: {gbs:.1f} GB/s ({100 * gbs / PEAK_GBS:.1f}%)")
+    return round(gbs, 1)
+
+
+PMC_COPY_BYTES = 256 << 20
+PMC_LAUNCHES = 100
+
+
+def pmc_workload(torch, gsvk, bufs):
+    """For `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`: PMC_LAUNCHES launches of the step's
+    dominant kernel (residual+LN [64,512] f16, bias + residual) and 10 plain copies of
+    PMC_COPY_BYTES (the calibration: its counters per dispatch against its known bytes)."""
+    L0, _, _ = step_ops(gsvk, bufs)
+    for _ in range(PMC_LAUNCHES):
+        L0()
+    src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=bufs["x"].device)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc workload: {PMC_LAUNCHES} x residual+LN [64,512] f16, 10 x copy {PMC_COPY_BYTES} B")
+
+
+def measure_traffic(timeout_s=150):
+    """HBM-side traffic of one launch of the dominant kernel: two `rocprofv3 --pmc` child runs of
+    this script's --pmc workload (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what
+    the same counter reads for the PMC_COPY_BYTES copy in that workload. Returns (dict, None) or
+    (None, reason)."""
+    import csv
+    import glob
+    import subprocess
+    import tempfile
+
+    vals = {}
+    with tempfile.TemporaryDirectory(prefix="gsvk_pmc_") as td:
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            cmd = ["rocprofv3", "--pmc", ctr, "-f", "csv", "-d", td, "-o", ctr.lower(), "--",
+                   sys.executable, os.path.abspath(__file__), "--pmc"]
+            try:
+                subprocess.run(cmd, cwd=td, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                               timeout=timeout_s, env=dict(os.environ, TMPDIR=td))
+            except (OSError, subprocess.TimeoutExpired) as exc:
+                return None, f"{ctr}: {type(exc).__name__}"
+            # rocprofv3 can exit non-zero after writing complete results; the CSV decides
+            files = glob.glob(os.path.join(td, "**", f"{ctr.lower()}_counter_collection.csv"),
+                              recursive=True)
+            if not files:
+                return None, f"{ctr}: no counter file"
+            ln, cp = [], []
+            for r in csv.DictReader(open(files[0])):
+                if r["Counter_Name"] != ctr:
+                    continue
+                v = float(r["Counter_Value"])
+                if "ln_rows_tile" in r["Kernel_Name"]:
+                    ln.append(v)
+                elif "copyBuffer" in r["Kernel_Name"] or "copy" in r["Kernel_Name"].lower():
+                    cp.append(v)
+            if len(ln) < PMC_LAUNCHES or not cp:
+                return None, f"{ctr}: {len(ln)} kernel / {len(cp)} copy dispatches found"
+            vals[ctr] = (statistics.median(ln), max(cp))
+    kib = PMC_COPY_BYTES / 1024
+    f_fetch, f_write = kib / vals["FETCH_SIZE"][1], kib / vals["WRITE_SIZE"][1]
+    traffic = 1024 * (vals["FETCH_SIZE"][0] * f_fetch + vals["WRITE_SIZE"][0] * f_write)
+    return {"bytes": round(traffic), "fetch_kib": vals["FETCH_SIZE"][0],
+            "write_kib": vals["WRITE_SIZE"][0], "fetch_scale": round(f_fetch, 4),
+            "write_scale": round(f_write, 4)}, None
+
+
 # ---- main --------------------------------------------------------------------------------------------
 
 def main():
@@ -307,6 +428,10 @@ def main():
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run one kernel of the suite and exit")
+    ap.add_argument("--pmc", action="store_true",
+                    help="run the dominant kernel and a plain copy only (for rocprofv3 --pmc)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every kernel here is row- or element-local, so more "
@@ -325,6 +450,9 @@ def main():
         return
 
     bufs = make_step_buffers(torch, gsvk, dev)
+    if a.pmc:
+        pmc_workload(torch, gsvk, bufs)
+        return
     step = gsvk.T2SStep(bufs, eps=1e-5, graph=True)
     nbytes = step_bytes()
     for _ in range(a.warmup):
@@ -336,17 +464,13 @@ def main():
         step.run()
     e.record()
     e.synchronize()
+    torch.cuda.synchronize()
     ms = s.elapsed_time(e) / a.steps
     assert int(bufs["err"].item()) == 0
     log(f"decode step (graph, {step.launches} launches): {ms * 1e3:.2f} us")
 
     # per-op breakdown at the step's shapes: graphs of 48 back-to-back launches of each op
-    x, h = bufs["x"], bufs["h"]
-    L0 = lambda: gsvk.add_layernorm(bufs["attn_out"][0], bufs["n1g"][0], bufs["n1b"][0], h, 1e-5,
-                                    bias=bufs["bout"][0], residual=x)
-    R0 = lambda: gsvk.bias_act(gsvk.ACT_RELU, bufs["ff"][0], bufs["ff"][0], bias=bufs["b1"][0])
-    E0 = lambda: gsvk.embed_pe(bufs["table"], bufs["ids"], bufs["pe"], bufs["alpha"], x,
-                               pos=bufs["pos"], err=bufs["err"])
+    L0, R0, E0 = step_ops(gsvk, bufs)
     per_op = {}
     for name, fn, cnt, byt in (("residual_layernorm", L0, 48, ln_bytes(B, D, 2)),
                                ("bias_relu", R0, 24, bias_act_bytes(B, FF, 2)),
@@ -364,6 +488,16 @@ def main():
                 "frac": round(ach / PEAK_GBS, 5), "traffic": None,
                 "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_launch"]}
 
+    if not a.no_traffic:
+        tr, why = measure_traffic()
+        if tr:
+            roofline["traffic"] = tr["bytes"]
+            roofline["traffic_detail"] = tr
+            log(f"  traffic: {tr['bytes']} B per launch ({tr})")
+        else:
+            roofline["traffic_error"] = why
+            log(f"  traffic not measured: {why}")
+
     cpu = None
     if not a.no_cpu:
         res, tall = cpu_baseline(torch, bufs)
@@ -375,7 +509,10 @@ def main():
                "us_per_step": round(t_best * 1e6, 1),
                "single_thread_us_per_step": round(res[1][0] * 1e6, 1)}
 
-    kernels = None if a.no_kernels else kernel_suite(torch, gsvk, dev)
+    kernels = copy_gbs = None
+    if not a.no_kernels:
+        copy_gbs = copy_bandwidth(torch, dev)
+        kernels = kernel_suite(torch, gsvk, dev)
 
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
@@ -389,6 +526,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "per_op": per_op,
+        "copy_GBps": copy_gbs,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)

@@ -25,14 +25,14 @@ __device__ __forceinline__ uint32_t f2h(float v) {
   // in the last bit for some inputs; the asm makes v an opaque fp32 register value.
   __asm__("" : "+v"(v));
   // v_cvt_f16_f32 rounds to nearest even, overflows to inf and keeps NaN (as vcvt_f16_f32 does)
-  // for results in the normal half range. For results below 2^-14 (half subnormals) it was
-  // measured on MI355X to round exact ties away from zero, so that range is rounded here: the
-  // scaling by 2^24 is exact and v_rndne_f32 rounds half to even, giving the subnormal's bits.
+  // for results in the normal half range and for zeros. For half-subnormal results
+  // (|v| < 2^-14) it was measured on MI355X to round exact ties away from zero, so those are
+  // rounded first: 0.5f + |v| lies where fp32 spacing is 2^-24, the half-subnormal spacing, so the
+  // add rounds |v| to that grid with ties to even and the subtraction is exact; the converted
+  // value is then representable and the conversion exact. Branch-free: 6 VALU operations.
   const float a = __builtin_fabsf(v);
-  const uint32_t sign = (__builtin_bit_cast(uint32_t, v) >> 16) & 0x8000u;
-  const uint32_t sub = sign | static_cast<uint32_t>(__builtin_rintf(a * 0x1p24f));
-  const uint32_t hw = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
-  return a < 0x1p-14f ? sub : hw;
+  const float r = a < 0x1p-14f ? __builtin_copysignf((a + 0.5f) - 0.5f, v) : v;
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(r));
 }
 __device__ __forceinline__ float bf2f(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);
@@ -49,24 +49,50 @@ __device__ __forceinline__ uint32_t f2bf(float v) {
 template <int DT>
 struct Store;
 
+// 16-byte global access. NT = true marks the access non-temporal (the line is not kept in the caches
+// after use): streaming kernels read and write each byte once, so caching it only evicts data that
+// other waves still need.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  const u32x4* q = static_cast<const u32x4*>(p);
+  if constexpr (NT) return __builtin_nontemporal_load(q);
+  else return *q;
+}
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, u32x4 v) {
+  u32x4* q = static_cast<u32x4*>(p);
+  if constexpr (NT) __builtin_nontemporal_store(v, q);
+  else *q = v;
+}
+
 template <>
 struct Store<GSVK_F32> {
   using T = float;
   static constexpr int VEC = 4;
-  __device__ static __forceinline__ void load(const void* base, size_t i, float (&v)[VEC]) {
-    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i);
-    v[0] = __builtin_bit_cast(float, q.x);
-    v[1] = __builtin_bit_cast(float, q.y);
-    v[2] = __builtin_bit_cast(float, q.z);
-    v[3] = __builtin_bit_cast(float, q.w);
+  __device__ static __forceinline__ void unpack(const u32x4& q, float (&v)[VEC]) {
+    // Copy the lanes out first: __builtin_bit_cast applied directly to an ext_vector element
+    // (q.y) was compiled by this clang as a cast of element 0.
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __builtin_bit_cast(float, w[k]);
   }
-  __device__ static __forceinline__ void store(void* base, size_t i, const float (&v)[VEC]) {
-    uint4 q;
+  __device__ static __forceinline__ u32x4 pack(const float (&v)[VEC]) {
+    u32x4 q;
     q.x = __builtin_bit_cast(uint32_t, v[0]);
     q.y = __builtin_bit_cast(uint32_t, v[1]);
     q.z = __builtin_bit_cast(uint32_t, v[2]);
     q.w = __builtin_bit_cast(uint32_t, v[3]);
-    *reinterpret_cast<uint4*>(static_cast<float*>(base) + i) = q;
+    return q;
+  }
+  template <bool NT = false>
+  __device__ static __forceinline__ void load(const void* base, size_t i, float (&v)[VEC]) {
+    unpack(ld16<NT>(static_cast<const float*>(base) + i), v);
+  }
+  template <bool NT = false>
+  __device__ static __forceinline__ void store(void* base, size_t i, const float (&v)[VEC]) {
+    st16<NT>(static_cast<float*>(base) + i, pack(v));
   }
   __device__ static __forceinline__ float load1(const void* base, size_t i) {
     return static_cast<const float*>(base)[i];
@@ -81,8 +107,7 @@ struct Store16 {  // f16 and bf16 share the 16-bit packing
   static constexpr int VEC = 8;
   __device__ static __forceinline__ float up(uint32_t b) { return DT == GSVK_F16 ? h2f(b) : bf2f(b); }
   __device__ static __forceinline__ uint32_t down(float v) { return DT == GSVK_F16 ? f2h(v) : f2bf(v); }
-  __device__ static __forceinline__ void load(const void* base, size_t i, float (&v)[VEC]) {
-    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+  __device__ static __forceinline__ void unpack(const u32x4& q, float (&v)[VEC]) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -90,11 +115,21 @@ struct Store16 {  // f16 and bf16 share the 16-bit packing
       v[2 * k + 1] = up(w[k] >> 16);
     }
   }
+  __device__ static __forceinline__ u32x4 pack(const float (&v)[VEC]) {
+    u32x4 q;
+    q.x = down(v[0]) | (down(v[1]) << 16);
+    q.y = down(v[2]) | (down(v[3]) << 16);
+    q.z = down(v[4]) | (down(v[5]) << 16);
+    q.w = down(v[6]) | (down(v[7]) << 16);
+    return q;
+  }
+  template <bool NT = false>
+  __device__ static __forceinline__ void load(const void* base, size_t i, float (&v)[VEC]) {
+    unpack(ld16<NT>(static_cast<const uint16_t*>(base) + i), v);
+  }
+  template <bool NT = false>
   __device__ static __forceinline__ void store(void* base, size_t i, const float (&v)[VEC]) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w[k] = down(v[2 * k]) | (down(v[2 * k + 1]) << 16);
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+    st16<NT>(static_cast<uint16_t*>(base) + i, pack(v));
   }
   __device__ static __forceinline__ float load1(const void* base, size_t i) {
     return up(static_cast<const uint16_t*>(base)[i]);
@@ -116,6 +151,36 @@ __device__ __forceinline__ void load_f32x4(const float* p, size_t i, float* v) {
   v[2] = q.z;
   v[3] = q.w;
 }
+
+// ---- GELU(erf) ------------------------------------------------------------------------------------
+// gelu(x) = 0.5 x (1 + erf(x / sqrt2)), the reference's bert::gelu_erf / HubertEngine::gelu
+// (bert_ops.hpp:25-27, hubert.cpp:233-236). With e = erfc(|x| / sqrt2) one branch-free form holds
+// for both signs: gelu(x) = 0.5 (x + |x| (1 - e)) (x >= 0: x - 0.5 x e; x < 0: 0.5 x e).
+// erfc(z) = t (a1 + a2 t + a3 t^2 + a4 t^3 + a5 t^4) exp(-z^2), t = 1 / (1 + p z): Abramowitz &
+// Stegun, Handbook of Mathematical Functions, formula 7.1.26, absolute error below 1.5e-7 for every
+// z >= 0. The rounding of 1 - e adds at most |x| 2^-25 absolute. Both stay below the fp32 tolerance
+// of this path (1e-6 + 1e-5 |gelu|) over the whole range; past |x| ~ 13 e underflows to 0 and the
+// result is exactly x (x > 0) or 0 (x < 0). +inf gives inf, -inf and NaN give NaN, like the
+// reference. 12 VALU operations plus two transcendentals (v_rcp_f32, v_exp_f32) per element.
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float zz = ax * 0.84932180028801904f;  // |x| sqrt(log2(e) / 2): exp(-x^2/2) = 2^-(zz^2)
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.23164189925183054f, ax, 1.f));
+  float p = 1.061405429f;
+  p = __builtin_fmaf(p, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  const float e = (p * t) * __builtin_amdgcn_exp2f(-(zz * zz));
+  return 0.5f * __builtin_fmaf(ax, 1.f - e, x);
+}
+
+// ---- streaming threshold ---------------------------------------------------------------------------
+// A call that moves at least this many bytes streams its operands non-temporally: its working set
+// exceeds the 256 MB MALL, so caching its lines only evicts what other kernels still use. Smaller
+// calls keep normal cached access (their operands are often still in L2 / MALL from the producing
+// kernel, and their outputs are read next).
+constexpr size_t kStreamBytes = size_t(256) << 20;
 
 // ---- wave64 reductions -------------------------------------------------------------------------
 // Inside each 16-lane DPP row: quad_perm xor-1, quad_perm xor-2, row_half_mirror, row_mirror give

@@ -1,9 +1,11 @@
 // gsvk_embed.hip — token-embedding gather fused with the scaled sinusoidal positional add (gfx950).
 //
-// One wave64 per output row. The wave reads its id and position once (wave-uniform scalar loads),
-// then each lane moves 8 consecutive columns: the table row chunk (16 B for f16/bf16, 32 B for f32),
-// the PE row chunk (32 B fp32), optionally the mm row chunk and the bias chunk, and writes 8 output
-// columns. The arithmetic is the reference's exactly (fmaf is the contraction AppleClang applies to
+// One wave64 per output row, one-shot grid: one-wave workgroups for short calls (latency-bound),
+// four-wave workgroups (rows 4b..4b+3) for long ones. The wave reads its id
+// and position once (wave-uniform scalar loads), then each lane moves 8 consecutive columns: the
+// table row chunk (16 B for f16/bf16, 32 B for f32), the PE row chunk (32 B fp32), optionally the mm
+// row chunk and the bias chunk, and writes 8 output columns. Table and PE rows are read through the
+// caches (ids repeat); output rows of calls beyond kStreamBytes are written non-temporally. The arithmetic is the reference's exactly (fmaf is the contraction AppleClang applies to
 // `e + alpha * pe`), so the result is bit-identical to the CPU restatement for every input.
 #include "gsvk_common.hpp"
 
@@ -46,14 +48,14 @@ __device__ __forceinline__ void load8(const void* p, size_t i, float (&v)[8]) {
     Store<DT>::load(p, i, v);
   }
 }
-template <int DT>
+template <int DT, bool NT>
 __device__ __forceinline__ void store8(void* p, size_t i, const float (&v)[8]) {
   if constexpr (DT == GSVK_F32) {
     const float a[4] = {v[0], v[1], v[2], v[3]}, b[4] = {v[4], v[5], v[6], v[7]};
-    Store<GSVK_F32>::store(p, i, a);
-    Store<GSVK_F32>::store(p, i + 4, b);
+    Store<GSVK_F32>::store<NT>(p, i, a);
+    Store<GSVK_F32>::store<NT>(p, i + 4, b);
   } else {
-    Store<DT>::store(p, i, v);
+    Store<DT>::template store<NT>(p, i, v);
   }
 }
 
@@ -68,11 +70,11 @@ __device__ __forceinline__ bool row_source(const EmbArgs& a, long r, size_t& tro
   return true;
 }
 
-template <int OUT, int TAB>
-__global__ __launch_bounds__(kBlock) void embed_pe_vec(EmbArgs a) {
+template <int OUT, int TAB, bool NT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void embed_pe_vec(EmbArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const long wave = static_cast<long>(blockIdx.x) * (kBlock / kWave) + (threadIdx.x / kWave);
-  const long nwaves = static_cast<long>(gridDim.x) * (kBlock / kWave);
+  const long wave = static_cast<long>(blockIdx.x) * (BLOCK / kWave) + (threadIdx.x / kWave);
+  const long nwaves = static_cast<long>(gridDim.x) * (BLOCK / kWave);
   const long nch = a.D / 8;
   for (long r = wave; r < a.rows; r += nwaves) {
     size_t trow = 0, prow = 0;
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(kBlock) void embed_pe_vec(EmbArgs a) {
       float nan8[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) nan8[k] = __builtin_nanf("");
-      for (long c = lane; c < nch; c += kWave) store8<OUT>(a.out, orow + c * 8, nan8);
+      for (long c = lane; c < nch; c += kWave) store8<OUT, NT>(a.out, orow + c * 8, nan8);
       continue;
     }
     for (long c = lane; c < nch; c += kWave) {
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(kBlock) void embed_pe_vec(EmbArgs a) {
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) o[k] = __builtin_fmaf(a.alpha, pe[k], e[k]);
-      store8<OUT>(a.out, orow + c * 8, o);
+      store8<OUT, NT>(a.out, orow + c * 8, o);
     }
   }
 }
@@ -132,12 +134,37 @@ __global__ __launch_bounds__(kBlock) void embed_pe_scalar(EmbArgs a) {
   }
 }
 
+// Calls with fewer rows than this are latency-bound: one wave per workgroup.
+constexpr long kSmallRows = 8192;
+// Rows per launch: a dispatch holds at most 2^32 - 1 work-items, so longer jobs are split.
+constexpr long kMaxRowsPerLaunch = (1L << 22) * (kBlock / kWave);
+
 template <int OUT, int TAB>
-void launch_embed(const EmbArgs& a, bool vec_ok, hipStream_t st) {
-  long g = (a.rows + (kBlock / kWave) - 1) / (kBlock / kWave);
-  if (g > 2048) g = 2048;
-  if (vec_ok) hipLaunchKernelGGL((embed_pe_vec<OUT, TAB>), dim3(g), dim3(kBlock), 0, st, a);
-  else hipLaunchKernelGGL((embed_pe_scalar<OUT, TAB>), dim3(g), dim3(kBlock), 0, st, a);
+void launch_embed(EmbArgs a, bool vec_ok, hipStream_t st) {
+  constexpr size_t osz = OUT == GSVK_F32 ? 4 : 2;
+  const size_t isz = a.ids32 ? 4 : 8;
+  const long total = a.rows;
+  const EmbArgs a0 = a;
+  for (long r0 = 0; r0 < total; r0 += kMaxRowsPerLaunch) {
+    a.rows = total - r0 < kMaxRowsPerLaunch ? total - r0 : kMaxRowsPerLaunch;
+    a.ids = static_cast<const char*>(a0.ids) + static_cast<size_t>(r0) * isz;
+    a.pos = a0.pos ? a0.pos + r0 : nullptr;
+    a.pos0 = a0.pos0 + r0;
+    a.mm = a0.mm ? static_cast<const char*>(a0.mm) + static_cast<size_t>(r0) * a.D * osz : nullptr;
+    a.out = static_cast<char*>(a0.out) + static_cast<size_t>(r0) * a.D * osz;
+    const unsigned g = static_cast<unsigned>((a.rows + (kBlock / kWave) - 1) / (kBlock / kWave));
+    const bool nt = static_cast<size_t>(total) * a.D * osz >= kStreamBytes;
+    if (vec_ok && nt) {
+      hipLaunchKernelGGL((embed_pe_vec<OUT, TAB, true, kBlock>), dim3(g), dim3(kBlock), 0, st, a);
+    } else if (vec_ok && total < kSmallRows) {
+      hipLaunchKernelGGL((embed_pe_vec<OUT, TAB, false, kWave>), dim3(static_cast<unsigned>(a.rows)),
+                         dim3(kWave), 0, st, a);
+    } else if (vec_ok) {
+      hipLaunchKernelGGL((embed_pe_vec<OUT, TAB, false, kBlock>), dim3(g), dim3(kBlock), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((embed_pe_scalar<OUT, TAB>), dim3(g), dim3(kBlock), 0, st, a);
+    }
+  }
 }
 
 template <int OUT>

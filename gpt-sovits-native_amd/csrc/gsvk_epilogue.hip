@@ -2,10 +2,16 @@
 // steps (residual add + LeakyReLU, 3-branch average + next-stage LeakyReLU) for gfx950.
 //
 // All of these are pure streams: each output element depends on the same element of the inputs
-// (plus a per-column bias). Threads move 16-byte chunks; each thread issues UNROLL independent
-// chunk loads before it computes and stores, which gives every wave several 1 KiB requests in
-// flight. Bit-exactness: every result is the reference's sequence of single-rounded fp32 operations
-// (this file is built with -ffp-contract=off, so no multiply-add is fused unless written as fmaf).
+// (plus a per-column bias). Tiling is one-shot: workgroup b owns one contiguous tile of 16-byte
+// chunks and exits after a single load-compute-store pass, so the waves in flight on the chip always
+// cover one compact window of memory that advances with the dispatch order. Each thread loads all of
+// its chunks before it computes. Calls that move more than the MALL holds read and write their
+// operands non-temporally (kStreamBytes).
+// (Measured on MI355X: persistent grid-stride loops over the same data plateau at ~57% of 8 TB/s,
+// one-shot tiles of 4-16 KiB per operand reach 75-80%.)
+//
+// Bit-exactness: every result is the reference's sequence of single-rounded fp32 operations (this
+// file is built with -ffp-contract=off, so no multiply-add is fused unless written as fmaf).
 #include <cmath>
 
 #include "gsvk_common.hpp"
@@ -14,8 +20,9 @@ namespace gsvk {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
-constexpr long kMaxBlocks = 2048;  // 8 workgroups per CU on 256 CUs; threads stride over the rest
+// Workgroups per launch: a dispatch holds at most 2^32 - 1 work-items per dimension, so larger jobs
+// are split into several launches on the host.
+constexpr long kMaxGrid = 1L << 22;
 
 // ---- activations (reference semantics) ----------------------------------------------------------
 
@@ -27,15 +34,11 @@ __device__ __forceinline__ float relu_ref(float v) {
 }
 // v < 0 ? v * slope : v — keeps -0 and NaN (nn_ops.hpp:48-74).
 __device__ __forceinline__ float lrelu_ref(float v, float slope) { return v < 0.f ? v * slope : v; }
-// 0.5f * x * (1 + erff(x * 0.70710678f)) (bert_ops.hpp:25-27; hubert.cpp:233-236).
-__device__ __forceinline__ float gelu_ref(float v) {
-  return 0.5f * v * (1.f + erff(v * 0.70710678118654752440f));
-}
 
 template <int ACT>
 __device__ __forceinline__ float act_apply(float v, float slope) {
   if constexpr (ACT == GSVK_ACT_RELU) return relu_ref(v);
-  else if constexpr (ACT == GSVK_ACT_GELU_ERF) return gelu_ref(v);
+  else if constexpr (ACT == GSVK_ACT_GELU_ERF) return gelu_erf(v);
   else if constexpr (ACT == GSVK_ACT_LEAKY_RELU) return lrelu_ref(v, slope);
   else return v;
 }
@@ -46,46 +49,53 @@ struct BaArgs {
   const void* x;
   const float* bias;
   void* y;
-  long rows;
+  long rows;   // rows in this launch
   long n;
   long ld;
+  long nch;    // 16-byte chunks per row
+  int wshift;  // log2 of W, the threads per row slice (64, 128 or 256)
   float slope;
 };
 
-// grid.x covers the 16-byte column chunks of a row, grid.y strides over rows. Each thread keeps its
-// bias chunk in VGPRs and walks rows blockIdx.y, +gridDim.y, ... in groups of kUnroll.
-template <int DT, int ACT>
-__global__ __launch_bounds__(kBlock) void bias_act_vec(BaArgs a) {
+// Workgroup (bx, by) covers column tile bx (W chunks) of row group by (P = kBlock / W row slices of
+// U rows each, P*U consecutive rows); x-fastest dispatch order walks a row group's column tiles
+// back to back. A thread keeps its bias chunk in VGPRs for its U rows. When a row is shorter than
+// kBlock chunks, one workgroup covers several whole rows, so the tile stays contiguous for
+// row-major data.
+template <int DT, int ACT, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void bias_act_tile(BaArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
-  const long cc = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
-  if (cc >= a.n / V) return;
+  const long bx = blockIdx.x, by = blockIdx.y;
+  const int P = kBlock >> a.wshift;  // shifts, not divisions: nothing delays the first load
+  const int tc = threadIdx.x & ((1 << a.wshift) - 1), tr = threadIdx.x >> a.wshift;
+  const long c = (bx << a.wshift) + tc;
+  if (c >= a.nch) return;  // no barriers below: idle lanes of a partial tile just leave
   float bi[V];
 #pragma unroll
   for (int k = 0; k < V; k += 4) {
-    if (a.bias) load_f32x4(a.bias, static_cast<size_t>(cc) * V + k, &bi[k]);
+    if (a.bias) load_f32x4(a.bias, static_cast<size_t>(c) * V + k, &bi[k]);
     else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
   }
-  const long step = gridDim.y;
-  for (long r0 = blockIdx.y; r0 < a.rows; r0 += step * kUnroll) {
-    float v[kUnroll][V];
+  const long r0 = by * static_cast<long>(P) * U + tr;
+  float v[U][V];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const long r = r0 + u * step;
-      if (r < a.rows) S::load(a.x, static_cast<size_t>(r) * a.ld + cc * V, v[u]);
-    }
+  for (int u = 0; u < U; ++u) {
+    const long r = r0 + static_cast<long>(u) * P;
+    if (r < a.rows) S::template load<NT>(a.x, static_cast<size_t>(r) * a.ld + c * V, v[u]);
+  }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const long r = r0 + u * step;
-      if (r < a.rows) {
+  for (int u = 0; u < U; ++u) {
+    const long r = r0 + static_cast<long>(u) * P;
+    if (r < a.rows) {
 #pragma unroll
-        for (int k = 0; k < V; ++k) v[u][k] = act_apply<ACT>(v[u][k] + bi[k], a.slope);
-        S::store(a.y, static_cast<size_t>(r) * a.ld + cc * V, v[u]);
-      }
+      for (int k = 0; k < V; ++k) v[u][k] = act_apply<ACT>(v[u][k] + bi[k], a.slope);
+      S::template store<NT>(a.y, static_cast<size_t>(r) * a.ld + c * V, v[u]);
     }
   }
 }
 
+// Any width / alignment: one element per thread, grid-stride (fallback path).
 template <int DT, int ACT>
 __global__ __launch_bounds__(kBlock) void bias_act_generic(BaArgs a) {
   using S = Store<DT>;
@@ -104,76 +114,75 @@ __global__ __launch_bounds__(kBlock) void bias_act_generic(BaArgs a) {
 struct EwArgs {
   const void* in[8];  // operands (see each kernel)
   void* out[2];
-  long n;
+  long n;             // elements
   float slope;
   int flag;
   int nbranch;
 };
 
-// Each thread handles kUnroll chunks spaced one grid-stride apart, then moves kUnroll strides on.
-// Elements past the last whole chunk are done one per thread by the scalar tail pass.
-template <typename Body>
-__device__ __forceinline__ void flat_chunks(long nchunks, Body body) {
-  const long stride = static_cast<long>(gridDim.x) * kBlock;
-  for (long c0 = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; c0 < nchunks;
-       c0 += stride * kUnroll)
-    body(c0, stride);
+// Chunk u of this thread in the workgroup's tile: tile b = chunks [b*kBlock*U, (b+1)*kBlock*U).
+template <int U>
+__device__ __forceinline__ long tile_chunk(int u) {
+  return static_cast<long>(blockIdx.x) * (kBlock * U) + u * kBlock + threadIdx.x;
+}
+// The n % VEC trailing elements are handled one per thread by the last workgroup.
+template <int V>
+__device__ __forceinline__ long tail_elem(long n) {
+  if (blockIdx.x != gridDim.x - 1) return -1;
+  const long i = (n / V) * V + threadIdx.x;
+  return i < n ? i : -1;
 }
 
 // y = lrelu(x, slope)
-template <int DT>
-__global__ __launch_bounds__(kBlock) void lrelu_vec(EwArgs a) {
+template <int DT, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void lrelu_tile(EwArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   const long nch = a.n / V;
-  flat_chunks(nch, [&](long c0, long stride) {
-    float v[kUnroll][V];
+  float v[U][V];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      if (c0 + u * stride < nch) S::load(a.in[0], (c0 + u * stride) * V, v[u]);
+  for (int u = 0; u < U; ++u)
+    if (tile_chunk<U>(u) < nch) S::template load<NT>(a.in[0], tile_chunk<U>(u) * V, v[u]);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      if (c0 + u * stride < nch) {
+  for (int u = 0; u < U; ++u)
+    if (tile_chunk<U>(u) < nch) {
 #pragma unroll
-        for (int k = 0; k < V; ++k) v[u][k] = lrelu_ref(v[u][k], a.slope);
-        S::store(a.out[0], (c0 + u * stride) * V, v[u]);
-      }
-  });
-  const long i = nch * V + static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i < a.n) S::store1(a.out[0], i, lrelu_ref(S::load1(a.in[0], i), a.slope));
+      for (int k = 0; k < V; ++k) v[u][k] = lrelu_ref(v[u][k], a.slope);
+      S::template store<NT>(a.out[0], tile_chunk<U>(u) * V, v[u]);
+    }
+  const long i = tail_elem<V>(a.n);
+  if (i >= 0) S::store1(a.out[0], i, lrelu_ref(S::load1(a.in[0], i), a.slope));
 }
 
 // cur += t_b; t_in = lrelu(cur)   (flag = 1 when t_in is written)
-template <int DT>
-__global__ __launch_bounds__(kBlock) void res_add_lrelu_vec(EwArgs a) {
+template <int DT, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void res_add_lrelu_tile(EwArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   const long nch = a.n / V;
   void* cur = a.out[0];
   void* tin = a.out[1];
-  flat_chunks(nch, [&](long c0, long stride) {
-    float c[kUnroll][V], t[kUnroll][V];
+  float c[U][V], t[U][V];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      if (c0 + u * stride < nch) {
-        S::load(cur, (c0 + u * stride) * V, c[u]);
-        S::load(a.in[0], (c0 + u * stride) * V, t[u]);
+  for (int u = 0; u < U; ++u)
+    if (tile_chunk<U>(u) < nch) {
+      S::template load<NT>(cur, tile_chunk<U>(u) * V, c[u]);
+      S::template load<NT>(a.in[0], tile_chunk<U>(u) * V, t[u]);
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (tile_chunk<U>(u) < nch) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) c[u][k] = c[u][k] + t[u][k];
+      S::template store<NT>(cur, tile_chunk<U>(u) * V, c[u]);
+      if (a.flag) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) t[u][k] = lrelu_ref(c[u][k], a.slope);
+        S::template store<NT>(tin, tile_chunk<U>(u) * V, t[u]);
       }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      if (c0 + u * stride < nch) {
-#pragma unroll
-        for (int k = 0; k < V; ++k) c[u][k] = c[u][k] + t[u][k];
-        S::store(cur, (c0 + u * stride) * V, c[u]);
-        if (a.flag) {
-#pragma unroll
-          for (int k = 0; k < V; ++k) t[u][k] = lrelu_ref(c[u][k], a.slope);
-          S::store(tin, (c0 + u * stride) * V, t[u]);
-        }
-      }
-  });
-  const long i = nch * V + static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i < a.n) {
+    }
+  const long i = tail_elem<V>(a.n);
+  if (i >= 0) {
     const float v = S::load1(cur, i) + S::load1(a.in[0], i);
     S::store1(cur, i, v);
     if (a.flag) S::store1(tin, i, lrelu_ref(v, a.slope));
@@ -182,52 +191,39 @@ __global__ __launch_bounds__(kBlock) void res_add_lrelu_vec(EwArgs a) {
 
 // out = lrelu( sum_j (cur_j [+ tb_j]) * kinv ), summed left to right with separate roundings.
 // in[0..3] = cur_j, in[4..7] = tb_j (NULL when absent); flag = apply_lrelu. All 2*NB operand
-// chunks of U chunk positions are loaded before any arithmetic, so U*2*NB loads are in flight.
-template <int DT, int NB>
-__global__ __launch_bounds__(kBlock) void branch_mean_vec(EwArgs a) {
+// chunks are loaded before any arithmetic.
+template <int DT, int NB, bool NT>
+__global__ __launch_bounds__(kBlock) void branch_mean_tile(EwArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
-  constexpr int U = DT == GSVK_F32 ? kUnroll : kUnroll / 2;
   constexpr float kInv = 1.f / static_cast<float>(NB);
   const long nch = a.n / V;
-  const long stride = static_cast<long>(gridDim.x) * kBlock;
-  for (long c0 = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; c0 < nch; c0 += stride * U) {
-    float cv[U][NB][V], tv[U][NB][V];
+  const long c = tile_chunk<1>(0);
+  if (c < nch) {
+    float cv[NB][V], tv[NB][V];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long c = c0 + u * stride;
-      if (c < nch) {
+    for (int j = 0; j < NB; ++j) {
+      S::template load<NT>(a.in[j], c * V, cv[j]);
+      if (a.in[4 + j]) S::template load<NT>(a.in[4 + j], c * V, tv[j]);
+    }
+    float acc[V];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          S::load(a.in[j], c * V, cv[u][j]);
-          if (a.in[4 + j]) S::load(a.in[4 + j], c * V, tv[u][j]);
-        }
+    for (int j = 0; j < NB; ++j) {
+      const bool has_t = a.in[4 + j] != nullptr;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const float v = has_t ? cv[j][k] + tv[j][k] : cv[j][k];
+        acc[k] = j == 0 ? v * kInv : acc[k] + v * kInv;
       }
     }
+    if (a.flag) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long c = c0 + u * stride;
-      if (c < nch) {
-        float acc[V];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          const bool has_t = a.in[4 + j] != nullptr;
-#pragma unroll
-          for (int k = 0; k < V; ++k) {
-            const float v = has_t ? cv[u][j][k] + tv[u][j][k] : cv[u][j][k];
-            acc[k] = j == 0 ? v * kInv : acc[k] + v * kInv;
-          }
-        }
-        if (a.flag) {
-#pragma unroll
-          for (int k = 0; k < V; ++k) acc[k] = lrelu_ref(acc[k], a.slope);
-        }
-        S::store(a.out[0], c * V, acc);
-      }
+      for (int k = 0; k < V; ++k) acc[k] = lrelu_ref(acc[k], a.slope);
     }
+    S::template store<NT>(a.out[0], c * V, acc);
   }
-  const long i = nch * V + static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i < a.n) {
+  const long i = tail_elem<V>(a.n);
+  if (i >= 0) {
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
@@ -240,39 +236,37 @@ __global__ __launch_bounds__(kBlock) void branch_mean_vec(EwArgs a) {
 }
 
 // out = acc + src * scale (acc optional); in[0] = acc, in[1] = src, slope carries the scale.
-template <int DT>
-__global__ __launch_bounds__(kBlock) void scaled_add_vec(EwArgs a) {
+template <int DT, int U, bool NT>
+__global__ __launch_bounds__(kBlock) void scaled_add_tile(EwArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   const long nch = a.n / V;
   const bool has_acc = a.in[0] != nullptr;
-  flat_chunks(nch, [&](long c0, long stride) {
-    float s[kUnroll][V], q[kUnroll][V];
+  float s[U][V], q[U][V];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      if (c0 + u * stride < nch) {
-        S::load(a.in[1], (c0 + u * stride) * V, s[u]);
-        if (has_acc) S::load(a.in[0], (c0 + u * stride) * V, q[u]);
+  for (int u = 0; u < U; ++u)
+    if (tile_chunk<U>(u) < nch) {
+      S::template load<NT>(a.in[1], tile_chunk<U>(u) * V, s[u]);
+      if (has_acc) S::template load<NT>(a.in[0], tile_chunk<U>(u) * V, q[u]);
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (tile_chunk<U>(u) < nch) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const float v = s[u][k] * a.slope;
+        s[u][k] = has_acc ? q[u][k] + v : v;
       }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      if (c0 + u * stride < nch) {
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-          const float v = s[u][k] * a.slope;
-          s[u][k] = has_acc ? q[u][k] + v : v;
-        }
-        S::store(a.out[0], (c0 + u * stride) * V, s[u]);
-      }
-  });
-  const long i = nch * V + static_cast<long>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i < a.n) {
+      S::template store<NT>(a.out[0], tile_chunk<U>(u) * V, s[u]);
+    }
+  const long i = tail_elem<V>(a.n);
+  if (i >= 0) {
     const float v = S::load1(a.in[1], i) * a.slope;
     S::store1(a.out[0], i, has_acc ? S::load1(a.in[0], i) + v : v);
   }
 }
 
-// Scalar fallbacks for buffers that are not 16-byte aligned.
+// Scalar fallbacks for buffers that are not 16-byte aligned (grid-stride).
 template <int DT>
 __global__ __launch_bounds__(kBlock) void ew_scalar(EwArgs a, int op) {
   using S = Store<DT>;
@@ -302,30 +296,80 @@ __global__ __launch_bounds__(kBlock) void ew_scalar(EwArgs a, int op) {
 
 // ---- launch helpers -------------------------------------------------------------------------------
 
-unsigned flat_grid(long nchunks) {
-  long b = (nchunks + kBlock - 1) / kBlock;
-  if (b < 1) b = 1;  // the tail pass needs one block even when there is no whole chunk
-  return static_cast<unsigned>(b < kMaxBlocks ? b : kMaxBlocks);
+unsigned stride_grid(long items) {
+  long b = (items + kBlock - 1) / kBlock;
+  if (b < 1) b = 1;
+  return static_cast<unsigned>(b < 2048 ? b : 2048);
+}
+
+// One-shot grid over nch chunks with U chunks per thread; at least one workgroup so that the
+// tail elements are handled even when there is no whole chunk.
+unsigned tile_grid(long nch, int U) {
+  const long per = static_cast<long>(kBlock) * U;
+  long b = (nch + per - 1) / per;
+  return static_cast<unsigned>(b < 1 ? 1 : b);
+}
+
+// log2 of the threads per row slice: the width (64, 128 or 256) that leaves the fewest idle lanes
+// in the last column tile, preferring the wider one on a tie.
+int slice_shift(long nch) {
+  int best = 8;
+  long best_idle = -1;
+  for (int sh : {8, 7, 6}) {
+    const long w = 1L << sh;
+    const long idle = ((nch + w - 1) / w) * w - nch;
+    if (best_idle < 0 || idle < best_idle) {
+      best = sh;
+      best_idle = idle;
+    }
+  }
+  return best;
+}
+
+// Rows per thread in bias_act_tile: several for streaming calls (more bytes in flight per thread:
+// four for 16-bit storage, two for fp32), one for small calls (more workgroups: latency-bound
+// launches finish sooner). Row groups go on grid.y, at most 65535 per launch.
+template <int DT, int ACT, int U, bool NT>
+void launch_bias_act_tile(BaArgs a, hipStream_t st) {
+  const long W = 1L << a.wshift;
+  const long rows_per_group = (kBlock / W) * U;
+  const long rows_per_launch = 65535L * rows_per_group;
+  const unsigned gx = static_cast<unsigned>((a.nch + W - 1) / W);
+  const long total_rows = a.rows;
+  const void* x0 = a.x;
+  void* y0 = a.y;
+  constexpr size_t esz = DT == GSVK_F32 ? 4 : 2;
+  for (long r0 = 0; r0 < total_rows; r0 += rows_per_launch) {
+    a.rows = total_rows - r0 < rows_per_launch ? total_rows - r0 : rows_per_launch;
+    a.x = static_cast<const char*>(x0) + static_cast<size_t>(r0) * a.ld * esz;
+    a.y = static_cast<char*>(y0) + static_cast<size_t>(r0) * a.ld * esz;
+    const unsigned gy = static_cast<unsigned>((a.rows + rows_per_group - 1) / rows_per_group);
+    hipLaunchKernelGGL((bias_act_tile<DT, ACT, U, NT>), dim3(gx, gy), dim3(kBlock), 0, st, a);
+  }
 }
 
 template <int ACT>
-int launch_bias_act(int dt, const BaArgs& a, bool vec_ok, hipStream_t st) {
-  const int V = dt == GSVK_F32 ? 4 : 8;
+int launch_bias_act(int dt, BaArgs a, bool vec_ok, hipStream_t st) {
   if (vec_ok) {
-    const long nch = a.n / V;
-    const unsigned gx = static_cast<unsigned>((nch + kBlock - 1) / kBlock);
-    long gy = kMaxBlocks / gx;
-    if (gy < 1) gy = 1;
-    if (gy > a.rows) gy = a.rows;
-    if (gy > 65535) gy = 65535;
-    const dim3 grid(gx, static_cast<unsigned>(gy));
+    a.nch = a.n / (dt == GSVK_F32 ? 4 : 8);
+    a.wshift = slice_shift(a.nch);
+    const bool stream = 2 * static_cast<size_t>(a.rows) * a.n * dtype_size(dt) >= kStreamBytes;
     switch (dt) {
-      case GSVK_F32: hipLaunchKernelGGL((bias_act_vec<GSVK_F32, ACT>), grid, dim3(kBlock), 0, st, a); break;
-      case GSVK_F16: hipLaunchKernelGGL((bias_act_vec<GSVK_F16, ACT>), grid, dim3(kBlock), 0, st, a); break;
-      default: hipLaunchKernelGGL((bias_act_vec<GSVK_BF16, ACT>), grid, dim3(kBlock), 0, st, a); break;
+      case GSVK_F32:
+        if (stream) launch_bias_act_tile<GSVK_F32, ACT, 2, true>(a, st);
+        else launch_bias_act_tile<GSVK_F32, ACT, 1, false>(a, st);
+        break;
+      case GSVK_F16:
+        if (stream) launch_bias_act_tile<GSVK_F16, ACT, 4, true>(a, st);
+        else launch_bias_act_tile<GSVK_F16, ACT, 1, false>(a, st);
+        break;
+      default:
+        if (stream) launch_bias_act_tile<GSVK_BF16, ACT, 4, true>(a, st);
+        else launch_bias_act_tile<GSVK_BF16, ACT, 1, false>(a, st);
+        break;
     }
   } else {
-    const unsigned g = flat_grid(a.rows * a.n);
+    const unsigned g = stride_grid(a.rows * a.n);
     switch (dt) {
       case GSVK_F32: hipLaunchKernelGGL((bias_act_generic<GSVK_F32, ACT>), dim3(g), dim3(kBlock), 0, st, a); break;
       case GSVK_F16: hipLaunchKernelGGL((bias_act_generic<GSVK_F16, ACT>), dim3(g), dim3(kBlock), 0, st, a); break;
@@ -337,7 +381,7 @@ int launch_bias_act(int dt, const BaArgs& a, bool vec_ok, hipStream_t st) {
 
 template <int DT>
 void launch_scalar(const EwArgs& a, int op, hipStream_t st) {
-  hipLaunchKernelGGL((ew_scalar<DT>), dim3(flat_grid(a.n)), dim3(kBlock), 0, st, a, op);
+  hipLaunchKernelGGL((ew_scalar<DT>), dim3(stride_grid(a.n)), dim3(kBlock), 0, st, a, op);
 }
 
 void launch_scalar_dt(int dt, const EwArgs& a, int op, hipStream_t st) {
@@ -348,15 +392,98 @@ void launch_scalar_dt(int dt, const EwArgs& a, int op, hipStream_t st) {
   }
 }
 
+// Chunks per thread of the flat kernels: one for the single-operand LeakyReLU and the six-operand
+// branch mean, two for the two-operand residual add and scaled add.
+constexpr int kLreluU = 1, kResU = 2, kScaledU = 2;
+
+// Runs `launch(args, grid)` over the n elements in segments of at most kMaxGrid workgroups of
+// kBlock*U chunks each; every operand pointer is advanced to the segment start. Segment lengths are
+// multiples of the chunk size, so only the last segment has tail elements.
+template <int DT, typename L>
+void launch_flat(const EwArgs& a, int U, hipStream_t st, L launch) {
+  constexpr long V = Store<DT>::VEC;
+  constexpr size_t esz = DT == GSVK_F32 ? 4 : 2;
+  const long seg = kMaxGrid * kBlock * U * V;
+  for (long off = 0; off < a.n; off += seg) {
+    EwArgs b = a;
+    b.n = a.n - off < seg ? a.n - off : seg;
+    for (int i = 0; i < 8; ++i)
+      if (a.in[i]) b.in[i] = static_cast<const char*>(a.in[i]) + static_cast<size_t>(off) * esz;
+    for (int i = 0; i < 2; ++i)
+      if (a.out[i]) b.out[i] = static_cast<char*>(a.out[i]) + static_cast<size_t>(off) * esz;
+    launch(b, tile_grid(b.n / V, U), st);
+  }
+}
+
+// Streaming (non-temporal) access when the call moves `operands` arrays of n elements totalling at
+// least kStreamBytes.
+template <int DT>
+bool streams(const EwArgs& a, int operands) {
+  return static_cast<size_t>(operands) * a.n * (DT == GSVK_F32 ? 4 : 2) >= kStreamBytes;
+}
+
+template <int DT, int NB, bool NT>
+void launch_branch_mean_nb(const EwArgs& a, hipStream_t st) {
+  launch_flat<DT>(a, 1, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
+    hipLaunchKernelGGL((branch_mean_tile<DT, NB, NT>), dim3(g), dim3(kBlock), 0, s, b);
+  });
+}
+
+template <int DT, bool NT>
+void launch_branch_mean_nt(const EwArgs& a, hipStream_t st) {
+  switch (a.nbranch) {
+    case 1: launch_branch_mean_nb<DT, 1, NT>(a, st); break;
+    case 2: launch_branch_mean_nb<DT, 2, NT>(a, st); break;
+    case 3: launch_branch_mean_nb<DT, 3, NT>(a, st); break;
+    default: launch_branch_mean_nb<DT, 4, NT>(a, st); break;
+  }
+}
+
 template <int DT>
 void launch_branch_mean(const EwArgs& a, hipStream_t st) {
-  const unsigned g = flat_grid(a.n / Store<DT>::VEC);
-  switch (a.nbranch) {
-    case 1: hipLaunchKernelGGL((branch_mean_vec<DT, 1>), dim3(g), dim3(kBlock), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((branch_mean_vec<DT, 2>), dim3(g), dim3(kBlock), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((branch_mean_vec<DT, 3>), dim3(g), dim3(kBlock), 0, st, a); break;
-    default: hipLaunchKernelGGL((branch_mean_vec<DT, 4>), dim3(g), dim3(kBlock), 0, st, a); break;
-  }
+  int ops = 1;
+  for (int j = 0; j < a.nbranch; ++j) ops += 1 + (a.in[4 + j] != nullptr);
+  if (streams<DT>(a, ops)) launch_branch_mean_nt<DT, true>(a, st);
+  else launch_branch_mean_nt<DT, false>(a, st);
+}
+
+template <int DT, bool NT>
+void launch_lrelu_nt(const EwArgs& a, hipStream_t st) {
+  launch_flat<DT>(a, kLreluU, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
+    hipLaunchKernelGGL((lrelu_tile<DT, kLreluU, NT>), dim3(g), dim3(kBlock), 0, s, b);
+  });
+}
+
+template <int DT>
+void launch_lrelu(const EwArgs& a, hipStream_t st) {
+  if (streams<DT>(a, 2)) launch_lrelu_nt<DT, true>(a, st);
+  else launch_lrelu_nt<DT, false>(a, st);
+}
+
+template <int DT, bool NT>
+void launch_res_add_nt(const EwArgs& a, hipStream_t st) {
+  launch_flat<DT>(a, kResU, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
+    hipLaunchKernelGGL((res_add_lrelu_tile<DT, kResU, NT>), dim3(g), dim3(kBlock), 0, s, b);
+  });
+}
+
+template <int DT>
+void launch_res_add(const EwArgs& a, hipStream_t st) {
+  if (streams<DT>(a, a.flag ? 4 : 3)) launch_res_add_nt<DT, true>(a, st);
+  else launch_res_add_nt<DT, false>(a, st);
+}
+
+template <int DT, bool NT>
+void launch_scaled_add_nt(const EwArgs& a, hipStream_t st) {
+  launch_flat<DT>(a, kScaledU, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
+    hipLaunchKernelGGL((scaled_add_tile<DT, kScaledU, NT>), dim3(g), dim3(kBlock), 0, s, b);
+  });
+}
+
+template <int DT>
+void launch_scaled_add(const EwArgs& a, hipStream_t st) {
+  if (streams<DT>(a, a.in[0] ? 3 : 2)) launch_scaled_add_nt<DT, true>(a, st);
+  else launch_scaled_add_nt<DT, false>(a, st);
 }
 
 }  // namespace
@@ -369,7 +496,9 @@ extern "C" int gsvk_bias_act(int dtype, int act, const void* x, const float* bia
   if (!valid_dtype(dtype)) return GSVK_E_DTYPE;
   if (act < GSVK_ACT_NONE || act > GSVK_ACT_LEAKY_RELU) return GSVK_E_DTYPE;
   if (!x || !y) return GSVK_E_NULL;
-  if (rows == 0 || n == 0 || ld < n || rows > (1ul << 40) || n > (1ul << 40)) return GSVK_E_SIZE;
+  if (rows == 0 || n == 0 || ld < n || rows > (1ul << 40) || n > (1ul << 30) || ld > (1ul << 40) ||
+      rows * ld > (1ul << 42))
+    return GSVK_E_SIZE;
   const size_t esz = dtype_size(dtype);
   const size_t span = span_bytes(rows, n, ld, esz);
   if (y != x && overlaps(y, span, x, span)) return GSVK_E_ALIAS;
@@ -378,7 +507,8 @@ extern "C" int gsvk_bias_act(int dtype, int act, const void* x, const float* bia
   const int V = dtype == GSVK_F32 ? 4 : 8;
   const bool vec_ok = n % V == 0 && ld % V == 0 && aligned16(x) && aligned16(y) &&
                       (!bias || aligned16(bias));
-  BaArgs a{x, bias, y, static_cast<long>(rows), static_cast<long>(n), static_cast<long>(ld), slope};
+  BaArgs a{x, bias, y, static_cast<long>(rows), static_cast<long>(n), static_cast<long>(ld), 0, 8,
+           slope};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (act) {
     case GSVK_ACT_NONE: return launch_bias_act<GSVK_ACT_NONE>(dtype, a, vec_ok, st);
@@ -403,11 +533,10 @@ extern "C" int gsvk_leaky_relu(int dtype, const void* x, void* y, size_t n, floa
   a.slope = slope;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (aligned16(x) && aligned16(y)) {
-    const unsigned g = flat_grid(a.n / (dtype == GSVK_F32 ? 4 : 8));
     switch (dtype) {
-      case GSVK_F32: hipLaunchKernelGGL((lrelu_vec<GSVK_F32>), dim3(g), dim3(kBlock), 0, st, a); break;
-      case GSVK_F16: hipLaunchKernelGGL((lrelu_vec<GSVK_F16>), dim3(g), dim3(kBlock), 0, st, a); break;
-      default: hipLaunchKernelGGL((lrelu_vec<GSVK_BF16>), dim3(g), dim3(kBlock), 0, st, a); break;
+      case GSVK_F32: launch_lrelu<GSVK_F32>(a, st); break;
+      case GSVK_F16: launch_lrelu<GSVK_F16>(a, st); break;
+      default: launch_lrelu<GSVK_BF16>(a, st); break;
     }
   } else {
     launch_scalar_dt(dtype, a, 0, st);
@@ -436,11 +565,10 @@ extern "C" int gsvk_resblock_add_lrelu(int dtype, void* cur, const void* t_b, vo
   a.flag = t_in != nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (aligned16(cur) && aligned16(t_b) && (!t_in || aligned16(t_in))) {
-    const unsigned g = flat_grid(a.n / (dtype == GSVK_F32 ? 4 : 8));
     switch (dtype) {
-      case GSVK_F32: hipLaunchKernelGGL((res_add_lrelu_vec<GSVK_F32>), dim3(g), dim3(kBlock), 0, st, a); break;
-      case GSVK_F16: hipLaunchKernelGGL((res_add_lrelu_vec<GSVK_F16>), dim3(g), dim3(kBlock), 0, st, a); break;
-      default: hipLaunchKernelGGL((res_add_lrelu_vec<GSVK_BF16>), dim3(g), dim3(kBlock), 0, st, a); break;
+      case GSVK_F32: launch_res_add<GSVK_F32>(a, st); break;
+      case GSVK_F16: launch_res_add<GSVK_F16>(a, st); break;
+      default: launch_res_add<GSVK_BF16>(a, st); break;
     }
   } else {
     launch_scalar_dt(dtype, a, 1, st);
@@ -508,11 +636,10 @@ extern "C" int gsvk_scaled_add(int dtype, const void* acc, const void* src, void
   a.slope = scale;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (aligned16(src) && aligned16(out) && (!acc || aligned16(acc))) {
-    const unsigned g = flat_grid(a.n / (dtype == GSVK_F32 ? 4 : 8));
     switch (dtype) {
-      case GSVK_F32: hipLaunchKernelGGL((scaled_add_vec<GSVK_F32>), dim3(g), dim3(kBlock), 0, st, a); break;
-      case GSVK_F16: hipLaunchKernelGGL((scaled_add_vec<GSVK_F16>), dim3(g), dim3(kBlock), 0, st, a); break;
-      default: hipLaunchKernelGGL((scaled_add_vec<GSVK_BF16>), dim3(g), dim3(kBlock), 0, st, a); break;
+      case GSVK_F32: launch_scaled_add<GSVK_F32>(a, st); break;
+      case GSVK_F16: launch_scaled_add<GSVK_F16>(a, st); break;
+      default: launch_scaled_add<GSVK_BF16>(a, st); break;
     }
   } else {
     launch_scalar_dt(dtype, a, 3, st);

@@ -1,10 +1,10 @@
 // gsvk_norm.hip — residual-add + LayerNorm over rows and per-channel GroupNorm + GELU for gfx950.
 //
-// LayerNorm: one wave64 per row. Each lane owns the 16-byte chunks lane, lane+64, ... of its row
-// (so every load/store instruction of the wave covers 1 KiB contiguously), keeps them in VGPRs,
-// and the row statistics are an exact two-pass mean / centred second moment over those registers,
-// reduced with DPP + ds_swizzle. gamma / beta / bias chunks for the lane's columns stay in VGPRs
-// across all rows the wave visits (waves stride over rows), so per-row traffic is the row itself.
+// LayerNorm: one wave64 per row, R consecutive rows per wave, one-shot grid. Each lane owns the
+// 16-byte chunks lane, lane+64, ... of its rows (so every load/store instruction of the wave covers
+// 1 KiB contiguously), keeps them in VGPRs, and the row statistics are an exact two-pass mean /
+// centred second moment over those registers, reduced with DPP + ds_swizzle. gamma / beta / bias
+// chunks for the lane's columns are loaded once per wave and reused for its R rows.
 //
 // GroupNorm(groups = channels): one 1024-thread workgroup per channel row of length T, the whole
 // row held in VGPRs (up to 8 chunks of 16 bytes per thread: T <= 32768 fp32 / 65536 fp16),
@@ -28,28 +28,36 @@ struct LnArgs {
   int n;
   long ld;
   double eps;
+  double inv_n;  // 1.0 / n, computed on the host
 };
 
-constexpr int kLnBlock = 256;  // 4 waves -> 4 rows in flight per workgroup
+// Workgroup size of the generic path; the tiled path takes it as a template parameter (one wave
+// per workgroup for latency-bound calls, four for large ones).
+constexpr int kLnBlock = 256;
 
 __device__ __forceinline__ float finish_rstd(float var, double eps) {
   return static_cast<float>(1.0 / sqrt(static_cast<double>(var) + eps));
 }
 
 // Vector path: n % VEC == 0, every row start 16-byte aligned, n <= 64 * CPL * VEC.
-template <int DT, int CPL>
-__global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
+// Wave w of workgroup b owns rows (WG*b + w)*R ... (WG*b + w)*R + R - 1 (WG waves per workgroup),
+// so a workgroup's WG*R rows are consecutive: one contiguous tile for row-major data, visited once
+// (one-shot grid). All x / residual chunks of the wave's R rows are loaded (packed) before any
+// arithmetic. The statistics are finalized with the host's 1/n and v_rsq_f32 (1 ulp): the latency
+// of a double-precision divide and square root sits on the critical path of every small call.
+template <int DT, int CPL, int R, bool NT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
-  constexpr bool kCache = CPL * V <= 16;  // keep per-column parameters in VGPRs across rows
+  constexpr bool kCache = CPL * V <= 16;  // keep per-column parameters in VGPRs for all R rows
+  constexpr size_t kEsz = DT == GSVK_F32 ? 4 : 2;
   const int lane = threadIdx.x & (kWave - 1);
-  const long wave = static_cast<long>(blockIdx.x) * (kLnBlock / kWave) + (threadIdx.x / kWave);
-  const long nwaves = static_cast<long>(gridDim.x) * (kLnBlock / kWave);
+  const long row0 = (static_cast<long>(blockIdx.x) * (BLOCK / kWave) + threadIdx.x / kWave) * R;
+  if (row0 >= a.rows) return;  // wave-uniform; this kernel has no workgroup barriers
   const int nch = a.n / V;
   const bool has_bias = a.bias != nullptr, has_res = a.res != nullptr;
   const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
 
-  float pg[kCache ? CPL : 1][V], pb[kCache ? CPL : 1][V], pbias[kCache ? CPL : 1][V];
   auto load_params = [&](int idx, float (&g)[V], float (&b)[V], float (&bi)[V]) {
 #pragma unroll
     for (int k = 0; k < V; k += 4) {
@@ -61,6 +69,22 @@ __global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
       else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
     }
   };
+
+  u32x4 xq[R][CPL], rq[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const size_t base = static_cast<size_t>(row0 + r) * static_cast<size_t>(a.ld);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int idx = lane + c * kWave;
+      if (row0 + r < a.rows && idx < nch) {
+        const size_t off = (base + static_cast<size_t>(idx) * V) * kEsz;
+        xq[r][c] = ld16<NT>(static_cast<const char*>(a.x) + off);
+        if (has_res) rq[r][c] = ld16<NT>(static_cast<const char*>(a.res) + off);
+      }
+    }
+  }
+  float pg[kCache ? CPL : 1][V], pb[kCache ? CPL : 1][V], pbias[kCache ? CPL : 1][V];
   if constexpr (kCache) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -69,7 +93,10 @@ __global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
     }
   }
 
-  for (long row = wave; row < a.rows; row += nwaves) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long row = row0 + r;
+    if (row >= a.rows) break;  // wave-uniform
     const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.ld);
     float h[CPL][V];
     float s = 0.f;
@@ -77,27 +104,24 @@ __global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
     for (int c = 0; c < CPL; ++c) {
       const int idx = lane + c * kWave;
       if (idx < nch) {
-        S::load(a.x, base + static_cast<size_t>(idx) * V, h[c]);
-        float bi[V];
-        if constexpr (kCache) {
-#pragma unroll
-          for (int k = 0; k < V; ++k) bi[k] = pbias[c][k];
-        } else {
-#pragma unroll
-          for (int k = 0; k < V; k += 4) {
-            if (has_bias) load_f32x4(a.bias, static_cast<size_t>(idx) * V + k, &bi[k]);
-            else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
-          }
-        }
+        S::unpack(xq[r][c], h[c]);
         if (has_bias) {
+          float bi[V];
+          if constexpr (kCache) {
+#pragma unroll
+            for (int k = 0; k < V; ++k) bi[k] = pbias[c][k];
+          } else {
+#pragma unroll
+            for (int k = 0; k < V; k += 4) load_f32x4(a.bias, static_cast<size_t>(idx) * V + k, &bi[k]);
+          }
 #pragma unroll
           for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + bi[k];
         }
         if (has_res) {
-          float r[V];
-          S::load(a.res, base + static_cast<size_t>(idx) * V, r);
+          float rv[V];
+          S::unpack(rq[r][c], rv);
 #pragma unroll
-          for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + r[k];
+          for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + rv[k];
         }
 #pragma unroll
         for (int k = 0; k < V; ++k) s += h[c][k];
@@ -107,7 +131,7 @@ __global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
       }
     }
     const float sum = wave_sum(s);
-    const float mean = static_cast<float>(static_cast<double>(sum) / static_cast<double>(a.n));
+    const float mean = static_cast<float>(static_cast<double>(sum) * a.inv_n);
     float q = 0.f;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -121,8 +145,8 @@ __global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
       }
     }
     const float sq = wave_sum(q);
-    const float var = static_cast<float>(static_cast<double>(sq) / static_cast<double>(a.n));
-    const float rstd = finish_rstd(var, a.eps);
+    const float var = static_cast<float>(static_cast<double>(sq) * a.inv_n);
+    const float rstd = __builtin_amdgcn_rsqf(var + static_cast<float>(a.eps));
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int idx = lane + c * kWave;
@@ -140,7 +164,7 @@ __global__ __launch_bounds__(kLnBlock) void ln_rows_vec(LnArgs a) {
         float o[V];
 #pragma unroll
         for (int k = 0; k < V; ++k) o[k] = __builtin_fmaf((h[c][k] - mean) * rstd, g[k], b[k]);
-        S::store(a.y, base + static_cast<size_t>(idx) * V, o);
+        S::template store<NT>(a.y, base + static_cast<size_t>(idx) * V, o);
       }
     }
   }
@@ -198,9 +222,6 @@ struct GnArgs {
 constexpr int kGnBlock = 1024;
 constexpr int kGnWaves = kGnBlock / kWave;
 
-__device__ __forceinline__ float gelu_erf(float v) {
-  return 0.5f * v * (1.f + erff(v * 0.70710678118654752440f));
-}
 
 // Sum of one double per thread over the 1024-thread block; every thread gets the same value.
 __device__ __forceinline__ double block_sum(double v, double* red) {
@@ -217,25 +238,9 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 
 // Row held in VGPRs as raw 16-byte chunks (packed halves stay packed: 4 VGPRs per chunk for every
 // dtype): head elements up to the first 16-byte boundary, CPT chunks per thread, then tail
-// elements. x and y rows share their 16-byte phase (checked on the host).
-template <int DT>
-__device__ __forceinline__ void unpack(const uint4& q, float (&v)[Store<DT>::VEC]) {
-  if constexpr (DT == GSVK_F32) {
-    v[0] = __builtin_bit_cast(float, q.x);
-    v[1] = __builtin_bit_cast(float, q.y);
-    v[2] = __builtin_bit_cast(float, q.z);
-    v[3] = __builtin_bit_cast(float, q.w);
-  } else {
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      v[2 * k] = Store<DT>::up(w[k] & 0xffffu);
-      v[2 * k + 1] = Store<DT>::up(w[k] >> 16);
-    }
-  }
-}
-
-template <int DT, int CPT>
+// elements. x and y rows share their 16-byte phase (checked on the host). The row is read and
+// written once (non-temporally for calls beyond kStreamBytes).
+template <int DT, int CPT, bool NT>
 __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
@@ -250,9 +255,9 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
   const long nbody = (a.T - head) / V;
   const long tail = a.T - head - nbody * V;
   const size_t body0 = base + head;  // element index of the first aligned chunk
-  const uint4* xb = reinterpret_cast<const uint4*>(static_cast<const char*>(a.x) + body0 * ESZ);
+  const char* xb = static_cast<const char*>(a.x) + body0 * ESZ;
 
-  uint4 raw[CPT];
+  u32x4 raw[CPT];
   float e = 0.f;  // this thread's head/tail element, if any
   long e_idx = -1;
   if (t < head) e_idx = t;
@@ -261,15 +266,15 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     const long k = t + static_cast<long>(c) * kGnBlock;
-    if (k < nbody) raw[c] = xb[k];
-    else raw[c] = make_uint4(0, 0, 0, 0);  // zero bits are 0.0 in every dtype
+    if (k < nbody) raw[c] = ld16<NT>(xb + static_cast<size_t>(k) * 16);
+    else raw[c] = u32x4{0u, 0u, 0u, 0u};  // zero bits are 0.0 in every dtype
   }
   if (e_idx >= 0) e = S::load1(a.x, base + e_idx);
   float s = e;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     float v[V];
-    unpack<DT>(raw[c], v);
+    S::unpack(raw[c], v);
 #pragma unroll
     for (int i = 0; i < V; ++i) s += v[i];
   }
@@ -281,7 +286,7 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
     const long k = t + static_cast<long>(c) * kGnBlock;
     if (k < nbody) {
       float v[V];
-      unpack<DT>(raw[c], v);
+      S::unpack(raw[c], v);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float d = v[i] - mean;
@@ -304,13 +309,13 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
     const long k = t + static_cast<long>(c) * kGnBlock;
     if (k < nbody) {
       float v[V], o[V];
-      unpack<DT>(raw[c], v);
+      S::unpack(raw[c], v);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float y = __builtin_fmaf((v[i] - mean) * rstd, g, b);
         o[i] = a.gelu ? gelu_erf(y) : y;
       }
-      S::store(a.y, body0 + static_cast<size_t>(k) * V, o);
+      S::template store<NT>(a.y, body0 + static_cast<size_t>(k) * V, o);
     }
   }
   if (e_idx >= 0) {
@@ -350,40 +355,91 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_generic(GnArgs a) {
 // ---- launchers ----------------------------------------------------------------------------------
 
 int ln_grid(long rows) {
-  // 2048 workgroups (8 per CU on 256 CUs) is enough to keep HBM busy; waves stride over the rest.
+  // generic path: 2048 workgroups (8 per CU on 256 CUs); waves stride over the rest
   const long need = (rows + (kLnBlock / kWave) - 1) / (kLnBlock / kWave);
   return static_cast<int>(need < 2048 ? need : 2048);
+}
+
+// Workgroups per launch of the tiled path (a dispatch holds at most 2^32 - 1 work-items).
+constexpr long kLnMaxGrid = 1L << 22;
+
+template <int DT, int CPL, int R, bool NT, int BLOCK>
+void launch_ln_tile(LnArgs a, hipStream_t st) {
+  constexpr size_t esz = DT == GSVK_F32 ? 4 : 2;
+  const long rows_per_block = (BLOCK / kWave) * R;
+  const long rows_per_launch = kLnMaxGrid * rows_per_block;
+  const long total = a.rows;
+  const void* x0 = a.x;
+  const void* r0p = a.res;
+  void* y0 = a.y;
+  for (long r0 = 0; r0 < total; r0 += rows_per_launch) {
+    const size_t off = static_cast<size_t>(r0) * a.ld * esz;
+    a.rows = total - r0 < rows_per_launch ? total - r0 : rows_per_launch;
+    a.x = static_cast<const char*>(x0) + off;
+    a.res = r0p ? static_cast<const char*>(r0p) + off : nullptr;
+    a.y = static_cast<char*>(y0) + off;
+    const unsigned grid = static_cast<unsigned>((a.rows + rows_per_block - 1) / rows_per_block);
+    hipLaunchKernelGGL((ln_rows_tile<DT, CPL, R, NT, BLOCK>), dim3(grid), dim3(BLOCK), 0, st, a);
+  }
+}
+
+// Short jobs (latency-bound, e.g. one decode step's [64, 512]): one row per wave, one wave per
+// workgroup (measured on MI355X: 2.35 us per launch against 2.59 with four-wave workgroups and a
+// double-precision finalize). Long jobs: four-wave workgroups, two rows per wave up to 1024 f16 /
+// 512 f32 columns (f16 rows of 512: 77% of 8 TB/s with two rows per wave, 61% with four).
+constexpr long kLnManyRows = 8192;
+
+template <int DT, bool NT>
+void launch_ln_vec(const LnArgs& a, int nch, hipStream_t st) {
+  const bool many = a.rows >= kLnManyRows;
+  if (nch <= 1 * kWave) {
+    if (many) launch_ln_tile<DT, 1, 2, NT, 256>(a, st);
+    else launch_ln_tile<DT, 1, 1, NT, 64>(a, st);
+  } else if (nch <= 2 * kWave) {
+    if (many) launch_ln_tile<DT, 2, 2, NT, 256>(a, st);
+    else launch_ln_tile<DT, 2, 1, NT, 64>(a, st);
+  } else if (nch <= 4 * kWave) {
+    if (many) launch_ln_tile<DT, 4, 1, NT, 256>(a, st);
+    else launch_ln_tile<DT, 4, 1, NT, 64>(a, st);
+  } else {
+    if (many) launch_ln_tile<DT, 8, 1, NT, 256>(a, st);
+    else launch_ln_tile<DT, 8, 1, NT, 64>(a, st);
+  }
 }
 
 template <int DT>
 int launch_ln(const LnArgs& a, bool vec_ok, hipStream_t st) {
   constexpr int V = Store<DT>::VEC;
-  const int grid = ln_grid(a.rows);
   const int nch = a.n / V;
-  if (vec_ok) {
-    if (nch <= 1 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 1>), dim3(grid), dim3(kLnBlock), 0, st, a);
-    else if (nch <= 2 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 2>), dim3(grid), dim3(kLnBlock), 0, st, a);
-    else if (nch <= 4 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 4>), dim3(grid), dim3(kLnBlock), 0, st, a);
-    else if (nch <= 8 * kWave) hipLaunchKernelGGL((ln_rows_vec<DT, 8>), dim3(grid), dim3(kLnBlock), 0, st, a);
-    else vec_ok = false;
+  if (vec_ok && nch <= 8 * kWave) {
+    const size_t bytes = static_cast<size_t>(a.rows) * a.n * (DT == GSVK_F32 ? 4 : 2) * (a.res ? 3 : 2);
+    if (bytes >= kStreamBytes) launch_ln_vec<DT, true>(a, nch, st);
+    else launch_ln_vec<DT, false>(a, nch, st);
+  } else {
+    hipLaunchKernelGGL((ln_rows_generic<DT>), dim3(ln_grid(a.rows)), dim3(kLnBlock), 0, st, a);
   }
-  if (!vec_ok) hipLaunchKernelGGL((ln_rows_generic<DT>), dim3(grid), dim3(kLnBlock), 0, st, a);
   return launch_status();
+}
+
+template <int DT, bool NT>
+bool launch_gn_vec(const GnArgs& a, hipStream_t st) {
+  constexpr int V = Store<DT>::VEC;
+  const dim3 grid(static_cast<unsigned>(a.channels));
+  const long nb = a.T / V + 1;  // upper bound on body chunks
+  if (nb <= 1L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 1, NT>), grid, dim3(kGnBlock), 0, st, a);
+  else if (nb <= 2L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 2, NT>), grid, dim3(kGnBlock), 0, st, a);
+  else if (nb <= 4L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 4, NT>), grid, dim3(kGnBlock), 0, st, a);
+  else if (nb <= 8L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 8, NT>), grid, dim3(kGnBlock), 0, st, a);
+  else return false;
+  return true;
 }
 
 template <int DT>
 int launch_gn(const GnArgs& a, bool vec_ok, hipStream_t st) {
-  constexpr int V = Store<DT>::VEC;
-  const dim3 grid(static_cast<unsigned>(a.channels));
-  const long nb = a.T / V + 1;  // upper bound on body chunks
-  if (vec_ok) {
-    if (nb <= 1L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 1>), grid, dim3(kGnBlock), 0, st, a);
-    else if (nb <= 2L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 2>), grid, dim3(kGnBlock), 0, st, a);
-    else if (nb <= 4L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 4>), grid, dim3(kGnBlock), 0, st, a);
-    else if (nb <= 8L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 8>), grid, dim3(kGnBlock), 0, st, a);
-    else vec_ok = false;
-  }
-  if (!vec_ok) hipLaunchKernelGGL((gn_gelu_generic<DT>), grid, dim3(kGnBlock), 0, st, a);
+  const size_t bytes = 2 * static_cast<size_t>(a.channels) * a.T * (DT == GSVK_F32 ? 4 : 2);
+  if (vec_ok) vec_ok = bytes >= kStreamBytes ? launch_gn_vec<DT, true>(a, st) : launch_gn_vec<DT, false>(a, st);
+  if (!vec_ok)
+    hipLaunchKernelGGL((gn_gelu_generic<DT>), dim3(static_cast<unsigned>(a.channels)), dim3(kGnBlock), 0, st, a);
   return launch_status();
 }
 
@@ -408,7 +464,7 @@ extern "C" int gsvk_add_layernorm(int dtype, const void* x, const float* bias, c
     if (p && overlaps(y, span, p, n * sizeof(float))) return GSVK_E_ALIAS;
 
   LnArgs a{x, bias, residual, gamma, beta, y, static_cast<long>(rows), static_cast<int>(n),
-           static_cast<long>(ld), eps};
+           static_cast<long>(ld), eps, 1.0 / static_cast<double>(n)};
   const int V = dtype == GSVK_F32 ? 4 : 8;
   bool vec_ok = (n % V == 0) && (ld % V == 0) && aligned16(x) && aligned16(y) &&
                 (!residual || aligned16(residual));
@@ -426,7 +482,8 @@ extern "C" int gsvk_groupnorm_gelu(int dtype, const void* x, const float* gamma,
                                    int apply_gelu, void* stream) {
   if (!valid_dtype(dtype)) return GSVK_E_DTYPE;
   if (!x || !y) return GSVK_E_NULL;
-  if (channels == 0 || T == 0 || ld < T || channels > 0x7fffffffu || T > (1ul << 40))
+  // one 1024-thread workgroup per channel: a dispatch holds at most 2^32 - 1 work-items
+  if (channels == 0 || T == 0 || ld < T || channels >= (1ul << 22) || T > (1ul << 40))
     return GSVK_E_SIZE;
   if (!(eps >= 0.0) || !std::isfinite(eps)) return GSVK_E_ARG;
   const size_t esz = dtype_size(dtype);

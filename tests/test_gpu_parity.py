@@ -181,6 +181,23 @@ def test_gelu_special_values():
     fin = np.isfinite(want)
     assert_close(F32, got[fin], want[fin], "gelu special")
     assert got[0, 0] == 0 and got[0, 6] == 30.0 and got[0, 7] == 0
+    assert got[0, 8] == np.inf and np.isnan(got[0, 9])  # 0.5f*x*(1+erff(x)) at +-inf
+
+
+@pytest.mark.parametrize("dt", [F32, F16])
+def test_gelu_dense_sweep(dt):
+    """The device GELU (erfc form, see gsvk_common.hpp) against the oracle's libm erff on every
+    value of a dense grid over [-14, 14] plus the tiny / subnormal range, at the stated tolerance."""
+    grid = np.linspace(-14, 14, 2 ** 20 + 1).astype(np.float32)
+    tiny = np.float32(10.0) ** -np.linspace(5, 40, 4096).astype(np.float32)
+    x32 = np.concatenate([grid, tiny, -tiny]).astype(np.float32)
+    x32 = np.concatenate([x32, np.zeros((-x32.size) % 4096, np.float32)]).reshape(-1, 4096)
+    x = st(dt, x32)
+    want = O.bias_act(dt, gsvk.ACT_GELU_ERF, x)
+    X = dev(x, dt)
+    gsvk.bias_act(gsvk.ACT_GELU_ERF, X, X)
+    sync()
+    assert_close(dt, host(X, dt), want, "gelu sweep")
 
 
 # ---- GroupNorm + GELU --------------------------------------------------------------------------
