@@ -143,6 +143,20 @@ struct Store<GSVK_F16> : Store16<GSVK_F16> {};
 template <>
 struct Store<GSVK_BF16> : Store16<GSVK_BF16> {};
 
+// Loads stay outside branches. A load under `if (in_bounds)` or `if (ptr)` ends a basic block, and
+// the compiler then waits for it (s_waitcnt vmcnt(0)) before the next load is issued: a thread
+// keeps one request in flight instead of all of them. So out-of-range indices are clamped to a
+// valid element (the value is discarded) and only stores are guarded, and an absent parameter
+// vector reads one of these constant rows instead of being skipped.
+static __device__ const float kZeros8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+static __device__ const float kOnes8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+
+// Address of the 8-float parameter chunk starting at element i, or of a constant row when the
+// vector is absent.
+__device__ __forceinline__ const float* param_or(const float* p, size_t i, const float* fill) {
+  return p ? p + i : fill;
+}
+
 // fp32 parameter vectors (gamma / beta / bias): 4 floats per 16 bytes.
 __device__ __forceinline__ void load_f32x4(const float* p, size_t i, float* v) {
   const float4 q = *reinterpret_cast<const float4*>(p + i);

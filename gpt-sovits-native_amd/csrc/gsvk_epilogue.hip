@@ -72,17 +72,16 @@ __global__ __launch_bounds__(kBlock) void bias_act_tile(BaArgs a) {
   const long c = (bx << a.wshift) + tc;
   if (c >= a.nch) return;  // no barriers below: idle lanes of a partial tile just leave
   float bi[V];
+  const float* bp = param_or(a.bias, static_cast<size_t>(c) * V, kZeros8);
 #pragma unroll
-  for (int k = 0; k < V; k += 4) {
-    if (a.bias) load_f32x4(a.bias, static_cast<size_t>(c) * V + k, &bi[k]);
-    else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
-  }
+  for (int k = 0; k < V; k += 4) load_f32x4(bp, k, &bi[k]);
   const long r0 = by * static_cast<long>(P) * U + tr;
   float v[U][V];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const long r = r0 + static_cast<long>(u) * P;
-    if (r < a.rows) S::template load<NT>(a.x, static_cast<size_t>(r) * a.ld + c * V, v[u]);
+  for (int u = 0; u < U; ++u) {  // rows past the end re-read the last row (discarded)
+    long r = r0 + static_cast<long>(u) * P;
+    r = r < a.rows ? r : a.rows - 1;
+    S::template load<NT>(a.x, static_cast<size_t>(r) * a.ld + c * V, v[u]);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -125,6 +124,13 @@ template <int U>
 __device__ __forceinline__ long tile_chunk(int u) {
   return static_cast<long>(blockIdx.x) * (kBlock * U) + u * kBlock + threadIdx.x;
 }
+// Chunk to load for tile_chunk(u): clamped to the last whole chunk (nch > 0), so loads need no
+// branch; the value loaded for an out-of-range chunk is discarded.
+template <int U>
+__device__ __forceinline__ long load_chunk(int u, long nch) {
+  const long c = tile_chunk<U>(u);
+  return c < nch ? c : nch - 1;
+}
 // The n % VEC trailing elements are handled one per thread by the last workgroup.
 template <int V>
 __device__ __forceinline__ long tail_elem(long n) {
@@ -139,17 +145,18 @@ __global__ __launch_bounds__(kBlock) void lrelu_tile(EwArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   const long nch = a.n / V;
-  float v[U][V];
+  if (nch > 0) {
+    float v[U][V];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (tile_chunk<U>(u) < nch) S::template load<NT>(a.in[0], tile_chunk<U>(u) * V, v[u]);
+    for (int u = 0; u < U; ++u) S::template load<NT>(a.in[0], load_chunk<U>(u, nch) * V, v[u]);
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (tile_chunk<U>(u) < nch) {
+    for (int u = 0; u < U; ++u)
+      if (tile_chunk<U>(u) < nch) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) v[u][k] = lrelu_ref(v[u][k], a.slope);
-      S::template store<NT>(a.out[0], tile_chunk<U>(u) * V, v[u]);
-    }
+        for (int k = 0; k < V; ++k) v[u][k] = lrelu_ref(v[u][k], a.slope);
+        S::template store<NT>(a.out[0], tile_chunk<U>(u) * V, v[u]);
+      }
+  }
   const long i = tail_elem<V>(a.n);
   if (i >= 0) S::store1(a.out[0], i, lrelu_ref(S::load1(a.in[0], i), a.slope));
 }
@@ -162,25 +169,26 @@ __global__ __launch_bounds__(kBlock) void res_add_lrelu_tile(EwArgs a) {
   const long nch = a.n / V;
   void* cur = a.out[0];
   void* tin = a.out[1];
-  float c[U][V], t[U][V];
+  if (nch > 0) {
+    float c[U][V], t[U][V];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (tile_chunk<U>(u) < nch) {
-      S::template load<NT>(cur, tile_chunk<U>(u) * V, c[u]);
-      S::template load<NT>(a.in[0], tile_chunk<U>(u) * V, t[u]);
+    for (int u = 0; u < U; ++u) {
+      S::template load<NT>(cur, load_chunk<U>(u, nch) * V, c[u]);
+      S::template load<NT>(a.in[0], load_chunk<U>(u, nch) * V, t[u]);
     }
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (tile_chunk<U>(u) < nch) {
+    for (int u = 0; u < U; ++u)
+      if (tile_chunk<U>(u) < nch) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) c[u][k] = c[u][k] + t[u][k];
-      S::template store<NT>(cur, tile_chunk<U>(u) * V, c[u]);
-      if (a.flag) {
+        for (int k = 0; k < V; ++k) c[u][k] = c[u][k] + t[u][k];
+        S::template store<NT>(cur, tile_chunk<U>(u) * V, c[u]);
+        if (a.flag) {
 #pragma unroll
-        for (int k = 0; k < V; ++k) t[u][k] = lrelu_ref(c[u][k], a.slope);
-        S::template store<NT>(tin, tile_chunk<U>(u) * V, t[u]);
+          for (int k = 0; k < V; ++k) t[u][k] = lrelu_ref(c[u][k], a.slope);
+          S::template store<NT>(tin, tile_chunk<U>(u) * V, t[u]);
+        }
       }
-    }
+  }
   const long i = tail_elem<V>(a.n);
   if (i >= 0) {
     const float v = S::load1(cur, i) + S::load1(a.in[0], i);
@@ -192,27 +200,27 @@ __global__ __launch_bounds__(kBlock) void res_add_lrelu_tile(EwArgs a) {
 // out = lrelu( sum_j (cur_j [+ tb_j]) * kinv ), summed left to right with separate roundings.
 // in[0..3] = cur_j, in[4..7] = tb_j (NULL when absent); flag = apply_lrelu. All 2*NB operand
 // chunks are loaded before any arithmetic.
-template <int DT, int NB, bool NT>
+// HAS_T: every branch has its t_b operand (the launcher takes the scalar kernel when only some do).
+template <int DT, int NB, bool NT, bool HAS_T>
 __global__ __launch_bounds__(kBlock) void branch_mean_tile(EwArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   constexpr float kInv = 1.f / static_cast<float>(NB);
   const long nch = a.n / V;
   const long c = tile_chunk<1>(0);
-  if (c < nch) {
+  if (c < nch) {  // one chunk per thread: this branch holds every load of the thread
     float cv[NB][V], tv[NB][V];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       S::template load<NT>(a.in[j], c * V, cv[j]);
-      if (a.in[4 + j]) S::template load<NT>(a.in[4 + j], c * V, tv[j]);
+      if constexpr (HAS_T) S::template load<NT>(a.in[4 + j], c * V, tv[j]);
     }
     float acc[V];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const bool has_t = a.in[4 + j] != nullptr;
 #pragma unroll
       for (int k = 0; k < V; ++k) {
-        const float v = has_t ? cv[j][k] + tv[j][k] : cv[j][k];
+        const float v = HAS_T ? cv[j][k] + tv[j][k] : cv[j][k];
         acc[k] = j == 0 ? v * kInv : acc[k] + v * kInv;
       }
     }
@@ -242,23 +250,26 @@ __global__ __launch_bounds__(kBlock) void scaled_add_tile(EwArgs a) {
   constexpr int V = S::VEC;
   const long nch = a.n / V;
   const bool has_acc = a.in[0] != nullptr;
-  float s[U][V], q[U][V];
+  // Without acc the src chunk is read twice instead of branching around the acc load.
+  const void* accp = has_acc ? a.in[0] : a.in[1];
+  if (nch > 0) {
+    float s[U][V], q[U][V];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (tile_chunk<U>(u) < nch) {
-      S::template load<NT>(a.in[1], tile_chunk<U>(u) * V, s[u]);
-      if (has_acc) S::template load<NT>(a.in[0], tile_chunk<U>(u) * V, q[u]);
+    for (int u = 0; u < U; ++u) {
+      S::template load<NT>(a.in[1], load_chunk<U>(u, nch) * V, s[u]);
+      S::template load<NT>(accp, load_chunk<U>(u, nch) * V, q[u]);
     }
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (tile_chunk<U>(u) < nch) {
+    for (int u = 0; u < U; ++u)
+      if (tile_chunk<U>(u) < nch) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        const float v = s[u][k] * a.slope;
-        s[u][k] = has_acc ? q[u][k] + v : v;
+        for (int k = 0; k < V; ++k) {
+          const float v = s[u][k] * a.slope;
+          s[u][k] = has_acc ? q[u][k] + v : v;
+        }
+        S::template store<NT>(a.out[0], tile_chunk<U>(u) * V, s[u]);
       }
-      S::template store<NT>(a.out[0], tile_chunk<U>(u) * V, s[u]);
-    }
+  }
   const long i = tail_elem<V>(a.n);
   if (i >= 0) {
     const float v = S::load1(a.in[1], i) * a.slope;
@@ -424,9 +435,15 @@ bool streams(const EwArgs& a, int operands) {
 
 template <int DT, int NB, bool NT>
 void launch_branch_mean_nb(const EwArgs& a, hipStream_t st) {
-  launch_flat<DT>(a, 1, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
-    hipLaunchKernelGGL((branch_mean_tile<DT, NB, NT>), dim3(g), dim3(kBlock), 0, s, b);
-  });
+  if (a.in[4]) {
+    launch_flat<DT>(a, 1, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
+      hipLaunchKernelGGL((branch_mean_tile<DT, NB, NT, true>), dim3(g), dim3(kBlock), 0, s, b);
+    });
+  } else {
+    launch_flat<DT>(a, 1, st, [](const EwArgs& b, unsigned g, hipStream_t s) {
+      hipLaunchKernelGGL((branch_mean_tile<DT, NB, NT, false>), dim3(g), dim3(kBlock), 0, s, b);
+    });
+  }
 }
 
 template <int DT, bool NT>
@@ -599,6 +616,12 @@ extern "C" int gsvk_resblock_branch_mean(int dtype, const void* const* cur, cons
     }
   }
   if (ormask % esz) return GSVK_E_ARG;
+  bool all_t = true, any_t = false;
+  for (int j = 0; j < nbranch; ++j) {
+    all_t = all_t && a.in[4 + j] != nullptr;
+    any_t = any_t || a.in[4 + j] != nullptr;
+  }
+  if (any_t && !all_t) aligned = false;  // mixed presence: the scalar kernel handles it per branch
   a.out[0] = out;
   a.n = static_cast<long>(n);
   a.slope = slope;

@@ -45,7 +45,7 @@ __device__ __forceinline__ float finish_rstd(float var, double eps) {
 // (one-shot grid). All x / residual chunks of the wave's R rows are loaded (packed) before any
 // arithmetic. The statistics are finalized with the host's 1/n and v_rsq_f32 (1 ulp): the latency
 // of a double-precision divide and square root sits on the critical path of every small call.
-template <int DT, int CPL, int R, bool NT, int BLOCK>
+template <int DT, int CPL, int R, bool NT, int BLOCK, bool HAS_RES>
 __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
@@ -55,41 +55,43 @@ __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
   const long row0 = (static_cast<long>(blockIdx.x) * (BLOCK / kWave) + threadIdx.x / kWave) * R;
   if (row0 >= a.rows) return;  // wave-uniform; this kernel has no workgroup barriers
   const int nch = a.n / V;
-  const bool has_bias = a.bias != nullptr, has_res = a.res != nullptr;
-  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
+  const bool has_bias = a.bias != nullptr;
 
+  // Every load is unconditional (see param_or): a lane past the row end (idx >= nch) and a row
+  // past the last one read a clamped, valid chunk whose value is never used; absent parameters
+  // read constant rows.
   auto load_params = [&](int idx, float (&g)[V], float (&b)[V], float (&bi)[V]) {
+    const size_t i = static_cast<size_t>(idx) * V;
+    const float* gp = param_or(a.gamma, i, kOnes8);
+    const float* bp = param_or(a.beta, i, kZeros8);
+    const float* bip = param_or(a.bias, i, kZeros8);
 #pragma unroll
     for (int k = 0; k < V; k += 4) {
-      if (has_g) load_f32x4(a.gamma, static_cast<size_t>(idx) * V + k, &g[k]);
-      else g[k] = g[k + 1] = g[k + 2] = g[k + 3] = 1.f;
-      if (has_b) load_f32x4(a.beta, static_cast<size_t>(idx) * V + k, &b[k]);
-      else b[k] = b[k + 1] = b[k + 2] = b[k + 3] = 0.f;
-      if (has_bias) load_f32x4(a.bias, static_cast<size_t>(idx) * V + k, &bi[k]);
-      else bi[k] = bi[k + 1] = bi[k + 2] = bi[k + 3] = 0.f;
+      load_f32x4(gp, k, &g[k]);
+      load_f32x4(bp, k, &b[k]);
+      load_f32x4(bip, k, &bi[k]);
     }
   };
 
   u32x4 xq[R][CPL], rq[R][CPL];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const size_t base = static_cast<size_t>(row0 + r) * static_cast<size_t>(a.ld);
+    const long row = row0 + r < a.rows ? row0 + r : a.rows - 1;
+    const size_t base = static_cast<size_t>(row) * static_cast<size_t>(a.ld);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      const int idx = lane + c * kWave;
-      if (row0 + r < a.rows && idx < nch) {
-        const size_t off = (base + static_cast<size_t>(idx) * V) * kEsz;
-        xq[r][c] = ld16<NT>(static_cast<const char*>(a.x) + off);
-        if (has_res) rq[r][c] = ld16<NT>(static_cast<const char*>(a.res) + off);
-      }
+      const int idx = lane + c * kWave < nch ? lane + c * kWave : nch - 1;
+      const size_t off = (base + static_cast<size_t>(idx) * V) * kEsz;
+      xq[r][c] = ld16<NT>(static_cast<const char*>(a.x) + off);
+      if constexpr (HAS_RES) rq[r][c] = ld16<NT>(static_cast<const char*>(a.res) + off);
     }
   }
   float pg[kCache ? CPL : 1][V], pb[kCache ? CPL : 1][V], pbias[kCache ? CPL : 1][V];
   if constexpr (kCache) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      const int idx = lane + c * kWave;
-      if (idx < nch) load_params(idx, pg[c], pb[c], pbias[c]);
+      const int idx = lane + c * kWave < nch ? lane + c * kWave : nch - 1;
+      load_params(idx, pg[c], pb[c], pbias[c]);
     }
   }
 
@@ -111,13 +113,14 @@ __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
 #pragma unroll
             for (int k = 0; k < V; ++k) bi[k] = pbias[c][k];
           } else {
+            const float* bip = param_or(a.bias, static_cast<size_t>(idx) * V, kZeros8);
 #pragma unroll
-            for (int k = 0; k < V; k += 4) load_f32x4(a.bias, static_cast<size_t>(idx) * V + k, &bi[k]);
+            for (int k = 0; k < V; k += 4) load_f32x4(bip, k, &bi[k]);
           }
 #pragma unroll
           for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + bi[k];
         }
-        if (has_res) {
+        if constexpr (HAS_RES) {
           float rv[V];
           S::unpack(rq[r][c], rv);
 #pragma unroll
@@ -223,11 +226,14 @@ constexpr int kGnBlock = 1024;
 constexpr int kGnWaves = kGnBlock / kWave;
 
 
-// Sum of one double per thread over the 1024-thread block; every thread gets the same value.
-__device__ __forceinline__ double block_sum(double v, double* red) {
-  v = wave_sum(v);
+// Sum over the 1024-thread block of one float per thread (each a partial over ~T/1024 values):
+// DPP wave sums in fp32, the 16 wave sums accumulated in double. Every thread gets the same value.
+// (A double-precision shuffle reduction costs six LDS permutes per step of latency on the
+// pipeline's critical path between two channels.)
+__device__ __forceinline__ double block_sum(float v, double* red) {
+  const float w_sum = wave_sum(v);
   const int w = threadIdx.x / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = static_cast<double>(w_sum);
   __syncthreads();
   double t = 0.0;
 #pragma unroll
@@ -236,40 +242,57 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
   return t;
 }
 
-// Row held in VGPRs as raw 16-byte chunks (packed halves stay packed: 4 VGPRs per chunk for every
-// dtype): head elements up to the first 16-byte boundary, CPT chunks per thread, then tail
-// elements. x and y rows share their 16-byte phase (checked on the host). The row is read and
-// written once (non-temporally for calls beyond kStreamBytes).
-template <int DT, int CPT, bool NT>
-__global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
-  using S = Store<DT>;
-  constexpr int V = S::VEC;
+// A channel row as this thread sees it: head elements up to the first 16-byte boundary, nbody
+// aligned 16-byte chunks (thread t owns chunks t, t + 1024, ...), then tail elements. Thread t also
+// owns head element t (t < head) or tail element t - head (head <= t < head + tail). x and y rows
+// share their 16-byte phase (checked on the host).
+struct GnRow {
+  size_t base;   // element index of the row start
+  size_t body0;  // element index of the first aligned chunk
+  long nbody;
+  long e_idx;    // this thread's head / tail element within the row, or -1
+};
+
+template <int DT>
+__device__ __forceinline__ GnRow gn_row(const GnArgs& a, long ch) {
   constexpr int ESZ = DT == GSVK_F32 ? 4 : 2;
-  __shared__ double red[kGnWaves];
-  const long ch = blockIdx.x;
-  const int t = threadIdx.x;
-  const size_t base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
-  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x) + base * ESZ;
+  constexpr int V = Store<DT>::VEC;
+  GnRow r;
+  r.base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x) + r.base * ESZ;
   long head = static_cast<long>(((16u - (addr & 15u)) & 15u) / ESZ);
   if (head > a.T) head = a.T;
-  const long nbody = (a.T - head) / V;
-  const long tail = a.T - head - nbody * V;
-  const size_t body0 = base + head;  // element index of the first aligned chunk
-  const char* xb = static_cast<const char*>(a.x) + body0 * ESZ;
+  r.nbody = (a.T - head) / V;
+  const long tail = a.T - head - r.nbody * V;
+  r.body0 = r.base + head;
+  const int t = threadIdx.x;
+  r.e_idx = t < head ? t : (t < head + tail ? head + r.nbody * V + (t - head) : -1);
+  return r;
+}
 
-  u32x4 raw[CPT];
-  float e = 0.f;  // this thread's head/tail element, if any
-  long e_idx = -1;
-  if (t < head) e_idx = t;
-  else if (t < head + tail) e_idx = head + nbody * V + (t - head);
-
+// Issue the loads of one row into registers (raw 16-byte chunks: packed halves stay packed, 4
+// VGPRs per chunk for every dtype).
+template <int DT, int CPT, bool NT>
+__device__ __forceinline__ void gn_load(const GnArgs& a, const GnRow& r, u32x4 (&raw)[CPT],
+                                        float& e) {
+  constexpr int ESZ = DT == GSVK_F32 ? 4 : 2;
+  const char* xb = static_cast<const char*>(a.x) + r.body0 * ESZ;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const long k = t + static_cast<long>(c) * kGnBlock;
-    if (k < nbody) raw[c] = ld16<NT>(xb + static_cast<size_t>(k) * 16);
+    const long k = threadIdx.x + static_cast<long>(c) * kGnBlock;
+    if (k < r.nbody) raw[c] = ld16<NT>(xb + static_cast<size_t>(k) * 16);
     else raw[c] = u32x4{0u, 0u, 0u, 0u};  // zero bits are 0.0 in every dtype
   }
-  if (e_idx >= 0) e = S::load1(a.x, base + e_idx);
+  e = r.e_idx >= 0 ? Store<DT>::load1(a.x, r.base + r.e_idx) : 0.f;
+}
+
+// Mean and rstd of one row held in registers (raw chunks + the head / tail element e). Contains
+// workgroup barriers: every thread of the workgroup calls it for the same channel.
+template <int DT, int CPT>
+__device__ __forceinline__ void gn_stats(const GnArgs& a, const GnRow& r, const u32x4 (&raw)[CPT],
+                                         float e, double* red, float& mean, float& rstd) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
   float s = e;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
@@ -278,13 +301,13 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
 #pragma unroll
     for (int i = 0; i < V; ++i) s += v[i];
   }
-  const double mean_d = block_sum(static_cast<double>(s), red) / static_cast<double>(a.T);
-  const float mean = static_cast<float>(mean_d);
+  const double mean_d = block_sum(s, red) / static_cast<double>(a.T);
+  mean = static_cast<float>(mean_d);
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const long k = t + static_cast<long>(c) * kGnBlock;
-    if (k < nbody) {
+    const long k = threadIdx.x + static_cast<long>(c) * kGnBlock;
+    if (k < r.nbody) {
       float v[V];
       S::unpack(raw[c], v);
 #pragma unroll
@@ -294,33 +317,70 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
       }
     }
   }
-  if (e_idx >= 0) {
+  if (r.e_idx >= 0) {
     const float d = e - mean;
     q = __builtin_fmaf(d, d, q);
   }
   // Centred on the fp32 mean, corrected by (mean_d - mean)^2 so the variance is about mean_d.
   const double dm = mean_d - static_cast<double>(mean);
-  const double var = block_sum(static_cast<double>(q), red) / static_cast<double>(a.T) - dm * dm;
-  const float rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
-  const float g = a.gamma ? a.gamma[ch] : 1.f;
-  const float b = a.beta ? a.beta[ch] : 0.f;
+  const double var = block_sum(q, red) / static_cast<double>(a.T) - dm * dm;
+  rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
+}
+
+// Workgroup b normalizes channels b, b + G, b + 2G, ... (G = gridDim.x, about one workgroup per
+// CU) as a two-stage pipeline. The current channel's chunks are parked in LDS (each thread writes
+// and later reads back only its own 16-byte slots, so no barrier orders them), the registers then
+// take the loads of the next channel, and the current channel is normalized, passed through GELU
+// and stored from LDS while those loads are in flight. HBM keeps streaming during the compute
+// phase; with one channel per workgroup the two co-resident workgroups of a CU load, compute and
+// store in lockstep and HBM idles while the CU computes. No workgroup waits for another.
+template <int DT, int CPT, bool NT>
+__global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  extern __shared__ u32x4 stage[];  // CPT * kGnBlock chunks; thread t owns stage[c * kGnBlock + t]
+  __shared__ double red[kGnWaves];
+  const long G = gridDim.x;
+  long ch = blockIdx.x;  // workgroup-uniform
+  GnRow r = gn_row<DT>(a, ch);
+  u32x4 raw[CPT];
+  float e;
+  gn_load<DT, CPT, NT>(a, r, raw, e);
+  while (ch < a.channels) {
+    float mean, rstd;
+    gn_stats<DT, CPT>(a, r, raw, e, red, mean, rstd);
 #pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const long k = t + static_cast<long>(c) * kGnBlock;
-    if (k < nbody) {
-      float v[V], o[V];
-      S::unpack(raw[c], v);
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float y = __builtin_fmaf((v[i] - mean) * rstd, g, b);
-        o[i] = a.gelu ? gelu_erf(y) : y;
-      }
-      S::template store<NT>(a.y, body0 + static_cast<size_t>(k) * V, o);
+    for (int c = 0; c < CPT; ++c) stage[c * kGnBlock + threadIdx.x] = raw[c];
+    const GnRow cur = r;
+    const float e_cur = e;
+    const long next = ch + G;
+    if (next < a.channels) {
+      r = gn_row<DT>(a, next);
+      gn_load<DT, CPT, NT>(a, r, raw, e);
     }
-  }
-  if (e_idx >= 0) {
-    const float y = __builtin_fmaf((e - mean) * rstd, g, b);
-    S::store1(a.y, base + e_idx, a.gelu ? gelu_erf(y) : y);
+    const float g = a.gamma ? a.gamma[ch] : 1.f;
+    const float b = a.beta ? a.beta[ch] : 0.f;
+    // One chunk per iteration (8 or 4 independent elements): the prefetched channel occupies
+    // CPT chunks of VGPRs meanwhile.
+#pragma unroll 1
+    for (int c = 0; c < CPT; ++c) {
+      const long k = threadIdx.x + static_cast<long>(c) * kGnBlock;
+      if (k < cur.nbody) {
+        float v[V], o[V];
+        S::unpack(stage[c * kGnBlock + threadIdx.x], v);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float y = __builtin_fmaf((v[i] - mean) * rstd, g, b);
+          o[i] = a.gelu ? gelu_erf(y) : y;
+        }
+        S::template store<NT>(a.y, cur.body0 + static_cast<size_t>(k) * V, o);
+      }
+    }
+    if (cur.e_idx >= 0) {
+      const float y = __builtin_fmaf((e_cur - mean) * rstd, g, b);
+      S::store1(a.y, cur.base + cur.e_idx, a.gelu ? gelu_erf(y) : y);
+    }
+    ch = next;
   }
 }
 
@@ -333,7 +393,7 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_generic(GnArgs a) {
   const size_t base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
   float s = 0.f;
   for (long j = threadIdx.x; j < a.T; j += kGnBlock) s += S::load1(a.x, base + j);
-  const double mean_d = block_sum(static_cast<double>(s), red) / static_cast<double>(a.T);
+  const double mean_d = block_sum(s, red) / static_cast<double>(a.T);
   const float mean = static_cast<float>(mean_d);
   float q = 0.f;
   for (long j = threadIdx.x; j < a.T; j += kGnBlock) {
@@ -341,7 +401,7 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_generic(GnArgs a) {
     q = __builtin_fmaf(d, d, q);
   }
   const double dm = mean_d - static_cast<double>(mean);
-  const double var = block_sum(static_cast<double>(q), red) / static_cast<double>(a.T) - dm * dm;
+  const double var = block_sum(q, red) / static_cast<double>(a.T) - dm * dm;
   const float rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
   const float g = a.gamma ? a.gamma[ch] : 1.f;
   const float b = a.beta ? a.beta[ch] : 0.f;
@@ -365,6 +425,7 @@ constexpr long kLnMaxGrid = 1L << 22;
 
 template <int DT, int CPL, int R, bool NT, int BLOCK>
 void launch_ln_tile(LnArgs a, hipStream_t st) {
+  const bool has_res = a.res != nullptr;
   constexpr size_t esz = DT == GSVK_F32 ? 4 : 2;
   const long rows_per_block = (BLOCK / kWave) * R;
   const long rows_per_launch = kLnMaxGrid * rows_per_block;
@@ -379,7 +440,10 @@ void launch_ln_tile(LnArgs a, hipStream_t st) {
     a.res = r0p ? static_cast<const char*>(r0p) + off : nullptr;
     a.y = static_cast<char*>(y0) + off;
     const unsigned grid = static_cast<unsigned>((a.rows + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL((ln_rows_tile<DT, CPL, R, NT, BLOCK>), dim3(grid), dim3(BLOCK), 0, st, a);
+    if (has_res)
+      hipLaunchKernelGGL((ln_rows_tile<DT, CPL, R, NT, BLOCK, true>), dim3(grid), dim3(BLOCK), 0, st, a);
+    else
+      hipLaunchKernelGGL((ln_rows_tile<DT, CPL, R, NT, BLOCK, false>), dim3(grid), dim3(BLOCK), 0, st, a);
   }
 }
 
@@ -421,15 +485,43 @@ int launch_ln(const LnArgs& a, bool vec_ok, hipStream_t st) {
   return launch_status();
 }
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <int DT, int CPT, bool NT>
+void launch_gn_cpt(const GnArgs& a, hipStream_t st) {
+  constexpr size_t lds = static_cast<size_t>(CPT) * kGnBlock * 16;  // 16-128 KiB of the 160 KiB
+  static bool attr_set = false;  // dynamic LDS above 64 KiB must be allowed once per kernel
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gn_gelu_vec<DT, CPT, NT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    attr_set = true;
+  }
+  // one workgroup per CU (two when the staging buffer leaves room for a second one)
+  const long slots = device_cus() * (lds <= 64 * 1024 ? 2 : 1);
+  const dim3 grid(static_cast<unsigned>(a.channels < slots ? a.channels : slots));
+  hipLaunchKernelGGL((gn_gelu_vec<DT, CPT, NT>), grid, dim3(kGnBlock), lds, st, a);
+}
+
 template <int DT, bool NT>
 bool launch_gn_vec(const GnArgs& a, hipStream_t st) {
   constexpr int V = Store<DT>::VEC;
-  const dim3 grid(static_cast<unsigned>(a.channels));
   const long nb = a.T / V + 1;  // upper bound on body chunks
-  if (nb <= 1L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 1, NT>), grid, dim3(kGnBlock), 0, st, a);
-  else if (nb <= 2L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 2, NT>), grid, dim3(kGnBlock), 0, st, a);
-  else if (nb <= 4L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 4, NT>), grid, dim3(kGnBlock), 0, st, a);
-  else if (nb <= 8L * kGnBlock) hipLaunchKernelGGL((gn_gelu_vec<DT, 8, NT>), grid, dim3(kGnBlock), 0, st, a);
+  if (nb <= 1L * kGnBlock) launch_gn_cpt<DT, 1, NT>(a, st);
+  else if (nb <= 2L * kGnBlock) launch_gn_cpt<DT, 2, NT>(a, st);
+  else if (nb <= 4L * kGnBlock) launch_gn_cpt<DT, 4, NT>(a, st);
+  else if (nb <= 8L * kGnBlock) launch_gn_cpt<DT, 8, NT>(a, st);
   else return false;
   return true;
 }
