@@ -242,10 +242,12 @@ __device__ __forceinline__ double block_sum(float v, double* red) {
   return t;
 }
 
-// A channel row as this thread sees it: head elements up to the first 16-byte boundary, nbody
-// aligned 16-byte chunks (thread t owns chunks t, t + 1024, ...), then tail elements. Thread t also
-// owns head element t (t < head) or tail element t - head (head <= t < head + tail). x and y rows
-// share their 16-byte phase (checked on the host).
+// A channel row as this thread sees it: head elements up to the first 128-byte boundary, nbody
+// 16-byte chunks (thread t owns chunks t, t + 1024, ...), then fewer than one chunk of tail
+// elements. Thread t also owns head element t (t < head) or tail element t - head (head <= t <
+// head + tail). Starting the body on a cache line keeps every wave access (1 KiB) on 8 lines
+// instead of 9 when rows are not line-aligned ([512, 31999] fp32 rows are 127,996 bytes apart).
+// x and y rows share their 16-byte phase (checked on the host).
 struct GnRow {
   size_t base;   // element index of the row start
   size_t body0;  // element index of the first aligned chunk
@@ -260,7 +262,7 @@ __device__ __forceinline__ GnRow gn_row(const GnArgs& a, long ch) {
   GnRow r;
   r.base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
   const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x) + r.base * ESZ;
-  long head = static_cast<long>(((16u - (addr & 15u)) & 15u) / ESZ);
+  long head = static_cast<long>(((128u - (addr & 127u)) & 127u) / ESZ);
   if (head > a.T) head = a.T;
   r.nbody = (a.T - head) / V;
   const long tail = a.T - head - r.nbody * V;
@@ -297,7 +299,7 @@ __device__ __forceinline__ void gn_stats(const GnArgs& a, const GnRow& r, const 
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     float v[V];
-    S::unpack(raw[c], v);
+    S::unpack(raw[c], v);  // chunks past the row end hold zeros
 #pragma unroll
     for (int i = 0; i < V; ++i) s += v[i];
   }
@@ -328,12 +330,13 @@ __device__ __forceinline__ void gn_stats(const GnArgs& a, const GnRow& r, const 
 }
 
 // Workgroup b normalizes channels b, b + G, b + 2G, ... (G = gridDim.x, about one workgroup per
-// CU) as a two-stage pipeline. The current channel's chunks are parked in LDS (each thread writes
-// and later reads back only its own 16-byte slots, so no barrier orders them), the registers then
-// take the loads of the next channel, and the current channel is normalized, passed through GELU
-// and stored from LDS while those loads are in flight. HBM keeps streaming during the compute
-// phase; with one channel per workgroup the two co-resident workgroups of a CU load, compute and
-// store in lockstep and HBM idles while the CU computes. No workgroup waits for another.
+// CU) as a two-stage pipeline. Once a channel's statistics are known, its chunks are parked in LDS
+// (each thread writes and later reads back only its own 16-byte slots, so no barrier orders them),
+// the registers take the loads of the next channel, and the parked channel is normalized, passed
+// through GELU and stored from LDS while those loads are in flight, so HBM keeps streaming during
+// the compute phase. (With one channel per workgroup, the two co-resident workgroups of a CU load,
+// compute and store in lockstep and HBM idles while the CU computes.) No workgroup waits for
+// another.
 template <int DT, int CPT, bool NT>
 __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
   using S = Store<DT>;
