@@ -10,6 +10,7 @@
 // row held in VGPRs (up to 8 chunks of 16 bytes per thread: T <= 32768 fp32 / 65536 fp16),
 // double-precision block reduction through LDS, then normalize + GELU(erf) and a single write:
 // one HBM read and one write per element.
+#include <atomic>
 #include <cmath>
 
 #include "gsvk_common.hpp"
@@ -488,28 +489,35 @@ int launch_ln(const LnArgs& a, bool vec_ok, hipStream_t st) {
   return launch_status();
 }
 
-// Compute units of the current device (cached per device; 256 on MI355X).
+constexpr int kMaxDevices = 64;
+
+// Compute units of the current device (cached per device; 256 on MI355X). A racing first call
+// stores the same value twice.
 int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 template <int DT, int CPT, bool NT>
 void launch_gn_cpt(const GnArgs& a, hipStream_t st) {
   constexpr size_t lds = static_cast<size_t>(CPT) * kGnBlock * 16;  // 16-128 KiB of the 160 KiB
-  static bool attr_set = false;  // dynamic LDS above 64 KiB must be allowed once per kernel
-  if (!attr_set) {
+  // Dynamic LDS above 64 KiB must be allowed once per kernel and device (idempotent, so two
+  // threads racing on the first call both just set it).
+  static std::atomic<bool> attr_set[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices &&
+      !attr_set[dev].load(std::memory_order_acquire)) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gn_gelu_vec<DT, CPT, NT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    attr_set = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   // one workgroup per CU (two when the staging buffer leaves room for a second one)
   const long slots = device_cus() * (lds <= 64 * 1024 ? 2 : 1);

@@ -48,7 +48,7 @@ struct gsvk_t2s_step {
 };
 
 extern "C" int gsvk_t2s_step_eager(const gsvk_t2s_step_desc* desc, void* stream) {
-  if (!desc_ok(desc)) return desc ? GSVK_E_NULL : GSVK_E_NULL;
+  if (!desc_ok(desc)) return GSVK_E_NULL;
   return issue(desc, stream);
 }
 
