@@ -17,7 +17,10 @@ Also reported (same JSON line):
                 batch of independent instances (> 0.4 GB moved, the 256 MB MALL cleared between
                 repetitions by reading a 512 MiB buffer), in GB/s and fraction of 8 TB/s;
   copy_GBps     a plain device-to-device copy of 1 GiB measured the same way (achievable-bandwidth
-                reference for the replicated figures).
+                reference for the replicated figures);
+  sovits_decoder  the SoVITS ResBlock epilogues at every decoder stage shape (reference 768-channel
+                geometry and the 512-start geometry), with the per-stage launch counts summed into
+                epilogue microseconds per 10 s of audio.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
        python bench.py --only KERNEL   (one kernel of the suite, for rocprofv3 runs)
@@ -251,6 +254,29 @@ def kernel_suite(torch, gsvk, dev, only=None):
 
     run_emb("embed_pe_prefill_1024x512", 1024, 512)
     run_emb("embed_pe_decode_64x512", 64, 8192)
+
+    def text_case(rows, rep):
+        """Text rows: out = mm + (e + bert_b) + alpha*PE(t) (t2s_engine.cpp:1774-1780)."""
+        def make(k):
+            tab = rn(732, D, std=0.02)
+            ids = torch.randint(0, 732, (rows * k,), device=dev, generator=g)
+            mm = rn(rows * k, D)
+            bb = rn(D, dtype=f32, std=0.02)
+            o = torch.empty(rows * k, D, dtype=f16, device=dev)
+            if k == 1:  # one sequence: positions 0..rows-1 implicit, as the reference passes them
+                return lambda: gsvk.embed_pe(tab, ids, pe, 0.93, o, pos0=0, mm=mm, bias=bb)
+            # k sequences of `rows` each: explicit positions restart at 0 for every sequence
+            pos = torch.arange(rows * k, device=dev, dtype=torch.int64) % rows
+            return lambda: gsvk.embed_pe(tab, ids, pe, 0.93, o, pos=pos, mm=mm, bias=bb)
+        # per row: id, table row, PE row, mm row, out row; bias once. The replicated batch also
+        # reads an explicit position per row, and its floor counts the 732-row table and the
+        # `rows` PE rows once (they stay in cache across sequences).
+        per_row = lambda k: rows * k * (8 + 2 * D + 4 * D + 2 * D + 2 * D) + 4 * D
+        floor = lambda k: rows * k * (16 + 4 * D) + 732 * D * 2 + rows * D * 4 + 4 * D
+        return (lambda: make(1), lambda: (rep, make(rep)), per_row, floor)
+
+    st_, rp_, b_, ub_ = text_case(512, 1024)
+    run("embed_pe_text_rows_512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_)
     run("residual_layernorm_f16_64x512", 2, *ln_case(64, 512, f16, 1e-5, True, True, 8192), 48)
     run("bias_relu_f16_64x2048", 2, *ba_case(64, 2048, gsvk.ACT_RELU, 4096), 24)
     # config 3: bias + GELU [512, 4096], residual + LN(1024, eps 1e-12)
@@ -297,10 +323,72 @@ def kernel_suite(torch, gsvk, dev, only=None):
     return out
 
 
+# ---- SoVITS decoder stage sweep ----------------------------------------------------------------------
+
+DECODER_GEOMETRIES = {
+    # Generator with 768 initial channels, upsample rates 10,8,2,2,2, 500 input frames
+    # (dec.hpp:55-76): the geometry the reference runs
+    "reference_768": [(384, 5000), (192, 40000), (96, 80000), (48, 160000), (24, 320000)],
+    # the configuration text's 512-start geometry, final stage 32 x 320000 as written
+    "literal_512": [(256, 5000), (128, 40000), (64, 80000), (32, 160000), (32, 320000)],
+}
+
+
+def sovits_decoder(torch, gsvk, dev):
+    """Per stage (C, T): graph-timed launches of K1 (LeakyReLU in place), K2 (residual add +
+    LeakyReLU write) and K3 (3-branch mean + next LeakyReLU) at that stage's shape, fp32 and fp16,
+    and the stage's epilogue time with the reference's per-stage counts (9 x K1, 6 x K2, 1 x K3;
+    dec.hpp:283-336). Totals are per 10 s of 32 kHz audio."""
+    out = {}
+    for geo, stages in DECODER_GEOMETRIES.items():
+        for dt, nm in ((torch.float32, "f32"), (torch.float16, "f16")):
+            esz = 4 if dt == torch.float32 else 2
+            rows, total = [], 0.0
+            for C, T in stages:
+                n = C * T
+                t = torch.randn(n, device=dev).to(dt)
+                cur = torch.randn(n, device=dev).to(dt)
+                tb = torch.randn(n, device=dev).to(dt)
+                tin = torch.empty_like(t)
+                curs = [torch.randn(n, device=dev).to(dt) for _ in range(3)]
+                tbs = [torch.randn(n, device=dev).to(dt) for _ in range(3)]
+                o = torch.empty_like(t)
+                k1 = graph_us_per_launch(torch, lambda: gsvk.leaky_relu(t, t, 0.1), 16, 5)
+                k2 = graph_us_per_launch(torch, lambda: gsvk.resblock_add_lrelu(cur, tb, tin, 0.1),
+                                         16, 5)
+                k3 = graph_us_per_launch(torch, lambda: gsvk.resblock_branch_mean(curs, tbs, o, True,
+                                                                                  0.1), 16, 5)
+                stage_us = 9 * k1 + 6 * k2 + k3
+                stage_bytes = (9 * 2 + 6 * 4 + 7) * n * esz
+                total += stage_us
+                rows.append({"C": C, "T": T, "K1_us": round(k1, 2), "K2_us": round(k2, 2),
+                             "K3_us": round(k3, 2), "stage_us": round(stage_us, 1),
+                             "stage_GBps": round(stage_bytes / stage_us / 1e3, 1)})
+                del t, cur, tb, tin, curs, tbs, o
+            torch.cuda.empty_cache()
+            out[f"{geo}_{nm}"] = {"stages": rows, "epilogue_us_per_10s_audio": round(total, 1)}
+            log(f"  sovits decoder {geo} {nm}: {total:.1f} us of epilogues per 10 s of audio")
+    return out
+
+
 # ---- CPU baseline ----------------------------------------------------------------------------------
 
-def cpu_baseline(torch, bufs, budget_s=8.0):
-    """The oracle's restatement of the same decode step on host copies of the same buffers."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, bufs, rep_s=0.3, reps=9):
+    """The oracle's restatement of the same decode step on host copies of the same buffers, with
+    the reference's bench convention (src/kern/bench_harness.hpp:8-13): 2 warm-up steps, then the
+    median of `reps` repetitions (each a batch of steps lasting ~rep_s) and their coefficient of
+    variation. Run on 1 thread and on every thread this process may use (rows split into bands, as
+    rt::parallel_for does)."""
     import numpy as np
 
     import oracle as O
@@ -318,13 +406,20 @@ def cpu_baseline(torch, bufs, budget_s=8.0):
     threads_all = max(1, min(threads_all, 16, B))
     res = {}
     for threads in sorted({1, threads_all}):
-        O.t2s_step(O.F16, hb, threads=threads)  # warm
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget_s / 2:
+        for _ in range(2):
             O.t2s_step(O.F16, hb, threads=threads)
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-        res[threads] = (dt, n)
+        t0 = time.perf_counter()
+        O.t2s_step(O.F16, hb, threads=threads)
+        per_rep = max(1, int(rep_s / max(time.perf_counter() - t0, 1e-6)))
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            for _ in range(per_rep):
+                O.t2s_step(O.F16, hb, threads=threads)
+            times.append((time.perf_counter() - t0) / per_rep)
+        med = statistics.median(times)
+        cv = statistics.pstdev(times) / statistics.mean(times)
+        res[threads] = {"s_per_step": med, "cv": cv, "steps": reps * per_rep, "per_rep": per_rep}
     return res, threads_all
 
 
@@ -501,18 +596,22 @@ def main():
     cpu = None
     if not a.no_cpu:
         res, tall = cpu_baseline(torch, bufs)
-        t_best = res[tall][0]
-        cpu = {"value": round(nbytes / t_best / 1e9, 3), "unit": "GB/s", "cores": tall,
+        best = res[tall]
+        cpu = {"value": round(nbytes / best["s_per_step"] / 1e9, 3), "unit": "GB/s", "cores": tall,
                "kind": "port",
-               "sample": f"{res[tall][1]} decode steps (B={B}, {LAYERS} layers, fp16 storage) of the "
-                         f"oracle's C restatement, rows split over {tall} threads",
-               "us_per_step": round(t_best * 1e6, 1),
-               "single_thread_us_per_step": round(res[1][0] * 1e6, 1)}
+               "sample": f"median of 9 repetitions x {best['per_rep']} decode steps (B={B}, "
+                         f"{LAYERS} layers, fp16 storage) of the oracle's C restatement, rows split "
+                         f"over {tall} threads; 2 warm-up steps",
+               "us_per_step": round(best["s_per_step"] * 1e6, 1), "cv": round(best["cv"], 4),
+               "single_thread_us_per_step": round(res[1]["s_per_step"] * 1e6, 1),
+               "single_thread_cv": round(res[1]["cv"], 4),
+               "cpu_model": cpu_model(), "hardware_threads": os.cpu_count()}
 
-    kernels = copy_gbs = None
+    kernels = copy_gbs = decoder = None
     if not a.no_kernels:
         copy_gbs = copy_bandwidth(torch, dev)
         kernels = kernel_suite(torch, gsvk, dev)
+        decoder = sovits_decoder(torch, gsvk, dev)
 
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
@@ -528,6 +627,7 @@ def main():
         "per_op": per_op,
         "copy_GBps": copy_gbs,
         "kernels": kernels,
+        "sovits_decoder": decoder,
     }
     print(json.dumps(line), flush=True)
     step.close()
