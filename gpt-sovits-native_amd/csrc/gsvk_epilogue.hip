@@ -24,25 +24,6 @@ constexpr int kBlock = 256;
 // are split into several launches on the host.
 constexpr long kMaxGrid = 1L << 22;
 
-// ---- activations (reference semantics) ----------------------------------------------------------
-
-// vmaxq_f32(x, 0): a NaN input comes out as that NaN made quiet, -0 -> +0 (kern.cpp:85-91,
-// vector body).
-__device__ __forceinline__ float relu_ref(float v) {
-  if (v != v) return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) | 0x00400000u);
-  return v > 0.f ? v : 0.f;
-}
-// v < 0 ? v * slope : v — keeps -0 and NaN (nn_ops.hpp:48-74).
-__device__ __forceinline__ float lrelu_ref(float v, float slope) { return v < 0.f ? v * slope : v; }
-
-template <int ACT>
-__device__ __forceinline__ float act_apply(float v, float slope) {
-  if constexpr (ACT == GSVK_ACT_RELU) return relu_ref(v);
-  else if constexpr (ACT == GSVK_ACT_GELU_ERF) return gelu_erf(v);
-  else if constexpr (ACT == GSVK_ACT_LEAKY_RELU) return lrelu_ref(v, slope);
-  else return v;
-}
-
 // ---- bias + activation over [rows, n] ------------------------------------------------------------
 
 struct BaArgs {

@@ -24,6 +24,8 @@ SIGNATURES = {
     "gsvk_status_string": (ctypes.c_char_p, [_i]),
     "gsvk_add_layernorm": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _d, _vp]),
     "gsvk_bias_act": (_i, [_i, _i, _vp, _vp, _vp, _sz, _sz, _sz, _f, _vp]),
+    "gsvk_gemv_f16w": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _i, _vp, _sz, _sz, _sz, _sz,
+                            _vp]),
     "gsvk_groupnorm_gelu": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _d, _i, _vp]),
     "gsvk_leaky_relu": (_i, [_i, _vp, _vp, _sz, _f, _vp]),
     "gsvk_resblock_add_lrelu": (_i, [_i, _vp, _vp, _vp, _sz, _f, _vp]),
@@ -96,8 +98,9 @@ def _rows(t):
     """(rows, n, ld) of a 2-D row-major view (or a 1-D buffer as one row)."""
     if t.dim() == 1:
         return 1, t.shape[0], t.shape[0]
-    assert t.dim() == 2 and t.stride(1) == 1, "rows must be contiguous"
-    return t.shape[0], t.shape[1], t.stride(0)
+    assert t.dim() == 2 and (t.stride(1) == 1 or t.shape[1] == 1), "rows must be contiguous"
+    # a single row has no meaningful row stride (numpy / torch may report 0 for it)
+    return t.shape[0], t.shape[1], t.stride(0) if t.shape[0] > 1 else t.shape[1]
 
 
 def add_layernorm(x, gamma, beta, y, eps, bias=None, residual=None, stream=None, check=True):
@@ -112,6 +115,21 @@ def bias_act(act, x, y, bias=None, slope=0.0, stream=None):
     return _check("gsvk_bias_act", lib().gsvk_bias_act(dtype_code(x), act, _ptr(x), _ptr(bias),
                                                        _ptr(y), rows, n, ld, slope,
                                                        _stream(stream)))
+
+
+def gemv_f16w(x, w, y, bias=None, act=ACT_NONE, slope=0.0, residual=None, round_x=True,
+              stream=None):
+    """y[r] = act(w @ x[r] + bias) (+ residual[r]); x [rows, in] f32/f16, w [out, in] f16,
+    y / residual [rows, out] sharing y's row stride."""
+    rows, n_in, ldx = _rows(x)
+    n_out = w.shape[0]
+    _, _, ldy = _rows(y)
+    assert residual is None or residual.data_ptr() == y.data_ptr() or _rows(residual)[2] == ldy, \
+        "residual shares y's row stride"
+    return _check("gsvk_gemv_f16w",
+                  lib().gsvk_gemv_f16w(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(w),
+                                       _ptr(bias), act, slope, _ptr(residual), dtype_code(y),
+                                       _ptr(y), ldy, rows, n_out, n_in, _stream(stream)))
 
 
 def groupnorm_gelu(x, gamma, beta, y, eps, apply_gelu=True, stream=None):

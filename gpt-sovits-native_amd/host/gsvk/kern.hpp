@@ -3,6 +3,8 @@
 // The functions keep the reference's names, argument order and argument meaning so an engine's
 // call sites compile unchanged after swapping the include:
 //   gsv::kern::layernorm / relu                      (src/kern/kern.hpp:25, 33)
+//   gsv::kern::gemv_f16w_f32acc / gemv_f16x_fmlal / f32_to_f16-free batched forms
+//                                                    (src/kern/gemv.cpp:112, gemv_fmlal.cpp:113)
 //   gsv::sovits::leaky_relu_io / leaky_relu_write / add_inplace / add_scaled_inplace / mul_write
 //                                                    (src/sovits/nn_ops.hpp:48-105)
 //   gsv::bert::gelu_erf over a buffer                (src/bert/bert_ops.hpp:25-27, 394)
@@ -83,6 +85,32 @@ inline void bias_relu(float* ff, const float* b1, size_t rows, size_t n) {
   gsvk::check(gsvk_bias_act(GSVK_F32, GSVK_ACT_RELU, ff, b1, ff, rows, n, n, 0.f,
                             gsvk::current_stream()),
               "gsv::kern::bias_relu");
+}
+
+// y[out] = W16 x, fp32 activations, fp32 accumulation (gemv.cpp:112-127).
+inline void gemv_f16w_f32acc(const uint16_t* w, const float* x, float* y, size_t out, size_t in) {
+  gsvk::check(gsvk_gemv_f16w(GSVK_F32, 0, x, in, w, nullptr, GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32,
+                             y, out, 1, out, in, gsvk::current_stream()),
+              "gsv::kern::gemv_f16w_f32acc");
+}
+
+// y[out] = W16 xh with xh already fp16 bit patterns (gemv_fmlal.cpp:113-132).
+inline void gemv_f16x_fmlal(const uint16_t* w, const uint16_t* xh, float* y, size_t out,
+                            size_t in) {
+  gsvk::check(gsvk_gemv_f16w(GSVK_F16, 1, xh, in, w, nullptr, GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32,
+                             y, out, 1, out, in, gsvk::current_stream()),
+              "gsv::kern::gemv_f16x_fmlal");
+}
+
+// B sequences at once, x rounded to fp16 as T2SEngine::gemv_fmlal does (t2s_engine.cpp:696-700),
+// with the loops after the GEMV fused: y = act(W16 x + bias) (+ residual). x [rows, in],
+// y / residual [rows, out]; residual may be y.
+inline void gemv_fmlal_rows(const uint16_t* w, const float* x, float* y, size_t rows, size_t out,
+                            size_t in, const float* bias = nullptr, int act = GSVK_ACT_NONE,
+                            const float* residual = nullptr) {
+  gsvk::check(gsvk_gemv_f16w(GSVK_F32, 1, x, in, w, bias, act, 0.f, residual, GSVK_F32, y, out,
+                             rows, out, in, gsvk::current_stream()),
+              "gsv::kern::gemv_fmlal_rows");
 }
 
 }  // namespace gsv::kern

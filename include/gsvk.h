@@ -88,6 +88,32 @@ int gsvk_bias_act(int dtype, int act, const void* x, const float* bias, void* y,
                   size_t n, size_t ld, float slope, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Batched decode GEMV with fp16 weights and fp32 accumulation, epilogue fused into the store.
+ *   xr[k]  = x[r, k] as fp32; with x_dtype F32 and round_x != 0 it is first rounded to fp16
+ *   acc    = sum_k float(w[n, k]) * xr[k]                       (fp32 sum of the products)
+ *   v      = act(acc + bias[n])                                 (no add when bias is NULL)
+ *   y[r,n] = residual ? v + residual[r, n] : v                  (rounded once to y_dtype)
+ * for rows r < rows (B sequences, one GEMV each), n < out, k < in.
+ * Replaces kern::gemv_f16w_f32acc(const uint16_t* w, const float* x, float* y, size_t out,
+ * size_t in) (src/kern/gemv.cpp:112-127; x_dtype F32, round_x = 0) and T2SEngine::gemv_fmlal ->
+ * kern::gemv_f16x_fmlal (t2s_engine.cpp:696-700, src/kern/gemv_fmlal.cpp:113-132; x rounded to
+ * fp16: x_dtype F16, or F32 with round_x = 1), each called once per sequence, together with the
+ * loops after them in block_decode_impl: QKV + bias (t2s_engine.cpp:1044-1049), out-proj + bias +
+ * residual (1090-1095), W1 + bias + ReLU (1105-1112), W2 + bias + residual (1113-1116).
+ * act is a gsvk_act (slope for LeakyReLU); bias, residual may be NULL.
+ * Layout: x [rows, in] with row stride ldx (x_dtype F32 or F16); w [out, in] row-major fp16 bit
+ * patterns (the .gsv weight layout); residual and y [rows, out] with row stride ldy (y_dtype).
+ * residual == y is allowed (in-place accumulate); y must not overlap x, w or bias.
+ * The sum is formed in a different order from the reference (matrix-core tiles, then a fixed-order
+ * sum of per-wave partials): results agree within fp32 accumulation noise,
+ * |y - ref| <= 1e-5 * max(1, max_n |ref[r, n]|) (the reference's own NEON-vs-scalar rule,
+ * tests/test_kern.cpp:111-118). Deterministic: the same inputs give the same bits on every call.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const uint16_t* w,
+                   const float* bias, int act, float slope, const void* residual, int y_dtype,
+                   void* y, size_t ldy, size_t rows, size_t out, size_t in, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * GroupNorm with one group per channel, optionally followed by GELU(erf).
  *   mean_c, var_c over the T frames of channel c (biased); y = (x - mean)*rstd*gamma[c] + beta[c];
  *   y = gelu_erf(y) when apply_gelu != 0.

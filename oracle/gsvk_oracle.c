@@ -20,6 +20,9 @@
  *   gelu_erf             float64 math.erf closed form, odd-part identity   (no reference vector)
  *   groupnorm_gelu       float64 closed form, T = 1 -> beta                (no reference vector)
  *   leaky / add / mean   exact-rational closed forms, slope identities     (no reference vector)
+ *   gemv_f16w            reference golden gemv_a / gemv_b (test_kern.cpp:96-120) at its own
+ *                        tolerance, exact small-integer products (sum order free), fp16-rounded x
+ *                        identity between the two modes, epilogue order
  * Functions marked "no reference vector" are pinned by mathematics only: the reference holds no
  * golden data for them.
  */
@@ -245,6 +248,98 @@ int oracle_bias_act(int dtype, int act, const void* x, const float* bias, void* 
     oracle_from_f32(dtype, v, row_ptr_w(y, dtype, row * ld), n);
   }
   free(v);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Decode GEMV with fp16 weights (next-tier row 1) and the bias / activation / residual loops that
+ * follow it in block_decode_impl (t2s_engine.cpp:1044-1049, 1090-1095, 1105-1116).
+ *
+ * x rounded to fp16 (T2SEngine::gemv_fmlal, t2s_engine.cpp:696-700 -> kern::f32_to_f16 then
+ * kern::gemv_f16x_fmlal, gemv_fmlal.cpp:23-35 and 40-132): per row, eight 4-lane fp32 accumulators
+ * a0..a7; each 64-element block adds, into lane l of a_j, w*x of elements 8j+l (vfmlalq_low) then
+ * 8j+4+l (vfmlalq_high), every fp16 x fp16 product exact and one rounding per accumulate (fma);
+ * s = vaddv(a0) + vaddv(a1) + ... + vaddv(a7) left to right with vaddv = (l0 + l1) + (l2 + l3);
+ * then the tail elements one by one.
+ *
+ * x in fp32 (kern::gemv_f16w_f32acc, gemv.cpp:36-127, the 4-row kernel): two 4-lane accumulators,
+ * acc0 lane l += w[i+l] * x[i+l], acc1 lane l += w[i+4+l] * x[i+4+l] per 8 elements (vfmaq: fma);
+ * s = vaddv(acc0 + acc1), then the tail with the contracted s += w*x (fma). (The reference sums the
+ * last out % 4 rows of each thread's range as vaddv(acc0) + vaddv(acc1) instead; which rows those
+ * are depends on its core count, so the 4-row order is used for every row. The difference is one
+ * fp32 rounding, far inside the comparison tolerance.)
+ * --------------------------------------------------------------------------------------------- */
+static inline float vaddv4q(const float a[4]) { return (a[0] + a[1]) + (a[2] + a[3]); }
+
+static float dot_fmlal(const uint16_t* w, const float* xh, size_t in) {
+  float a[8][4];
+  memset(a, 0, sizeof a);
+  const size_t vec_end = in & ~(size_t)63;
+  size_t i = 0;
+  for (; i < vec_end; i += 64)
+    for (int j = 0; j < 8; ++j)
+      for (int half = 0; half < 2; ++half)
+        for (int l = 0; l < 4; ++l) {
+          const size_t e = i + 8 * (size_t)j + 4 * (size_t)half + (size_t)l;
+          a[j][l] = fmaf(oracle_h2f(w[e]), xh[e], a[j][l]);
+        }
+  float s = vaddv4q(a[0]);
+  for (int j = 1; j < 8; ++j) s = s + vaddv4q(a[j]);
+  for (; i < in; ++i) s = fmaf(oracle_h2f(w[i]), xh[i], s);
+  return s;
+}
+
+static float dot_f32acc(const uint16_t* w, const float* x, size_t in) {
+  float a0[4] = {0, 0, 0, 0}, a1[4] = {0, 0, 0, 0};
+  const size_t vec_end = in & ~(size_t)7;
+  size_t i = 0;
+  for (; i < vec_end; i += 8)
+    for (int l = 0; l < 4; ++l) {
+      a0[l] = fmaf(oracle_h2f(w[i + l]), x[i + l], a0[l]);
+      a1[l] = fmaf(oracle_h2f(w[i + 4 + l]), x[i + 4 + l], a1[l]);
+    }
+  float t[4];
+  for (int l = 0; l < 4; ++l) t[l] = a0[l] + a1[l];
+  float s = vaddv4q(t);
+  for (; i < in; ++i) s = fmaf(oracle_h2f(w[i]), x[i], s);
+  return s;
+}
+
+int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const uint16_t* w,
+                     const float* bias, int act, float slope, const void* residual, int y_dtype,
+                     void* y, size_t ldy, size_t rows, size_t out, size_t in) {
+  float* xr = (float*)malloc(in * 4);
+  float* v = (float*)malloc(out * 4);
+  float* r = (float*)malloc(out * 4);
+  if (!xr || !v || !r) {
+    free(xr);
+    free(v);
+    free(r);
+    return -1;
+  }
+  const int fmlal = x_dtype == 1 || round_x;
+  for (size_t row = 0; row < rows; ++row) {
+    oracle_to_f32(x_dtype, row_ptr(x, x_dtype, row * ldx), xr, in);
+    if (x_dtype == 0 && round_x)
+      for (size_t k = 0; k < in; ++k) xr[k] = oracle_h2f(oracle_f2h(xr[k]));
+    for (size_t n = 0; n < out; ++n) {
+      const uint16_t* wr = w + n * in;
+      float t = fmlal ? dot_fmlal(wr, xr, in) : dot_f32acc(wr, xr, in);
+      if (bias) t = t + bias[n];
+      if (act == 1) t = relu_vec(t);
+      else if (act == 2) t = oracle_gelu_erf(t);
+      else if (act == 3) t = leaky(t, slope);
+      v[n] = t;
+    }
+    if (residual) {
+      oracle_to_f32(y_dtype, row_ptr(residual, y_dtype, row * ldy), r, out);
+      for (size_t n = 0; n < out; ++n) v[n] = v[n] + r[n];
+    }
+    oracle_from_f32(y_dtype, v, row_ptr_w(y, y_dtype, row * ldy), out);
+  }
+  free(xr);
+  free(v);
+  free(r);
   return 0;
 }
 

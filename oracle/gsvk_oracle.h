@@ -65,6 +65,12 @@ int oracle_resblock_branch_mean(int dtype, const void* const* cur, const void* c
 int oracle_scaled_add(int dtype, const void* acc, const void* src, void* out, size_t n,
                       float scale);
 
+/* Decode GEMV: gemv_f16x_fmlal (x rounded to fp16: x_dtype 1, or 0 with round_x) or
+ * gemv_f16w_f32acc (x_dtype 0, round_x 0), then bias, act (gsvk_act), residual, per row. */
+int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const uint16_t* w,
+                     const float* bias, int act, float slope, const void* residual, int y_dtype,
+                     void* y, size_t ldy, size_t rows, size_t out, size_t in);
+
 /* a10: T2SEngine::pe_row (t2s_engine.cpp:711-720) and the gather + alpha*PE loops
  * (t2s_engine.cpp:1774-1786, 1866-1869). index_type 0 = int64, 1 = int32. Returns the number of
  * rows whose id / position was out of range (those rows are NaN, as the GPU writes them). */

@@ -35,6 +35,8 @@ _SIG = {
     "oracle_resblock_branch_mean": (_i, [_i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i, _vp, _sz,
                                          _i, _f]),
     "oracle_scaled_add": (_i, [_i, _vp, _vp, _vp, _sz, _f]),
+    "oracle_gemv_f16w": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _i, _vp, _sz, _sz, _sz,
+                              _sz]),
     "oracle_pe_row": (None, [_vp, _sz, _sz]),
     "oracle_embed_pe": (ctypes.c_long, [_i, _i, _i, _vp, _sz, _vp, _vp, ctypes.c_int64, _vp, _sz,
                                         _f, _vp, _vp, _vp, _sz, _sz]),
@@ -164,6 +166,25 @@ def scaled_add(dt, acc, src, scale):
     out = np.empty_like(src)
     assert lib().oracle_scaled_add(dt, _p(acc), _p(src), _p(out), src.size, scale) == 0
     return out
+
+
+def gemv_f16w(x_dt, x, w, y_dt, bias=None, act=0, slope=0.0, residual=None, round_x=True):
+    """y [rows, out] storage array = act(w @ x[r] + bias) (+ residual[r]) per row.
+    x: [rows, in] storage of x_dt (F32 or F16); w: [out, in] uint16 fp16 bits."""
+    x = np.ascontiguousarray(x)
+    if x.ndim == 1:
+        x = x[None, :]
+    w = np.ascontiguousarray(w).view(np.uint16)
+    rows, n_in = x.shape
+    n_out = w.shape[0]
+    assert w.shape[1] == n_in
+    y = np.empty((rows, n_out), dtype=storage_dtype(y_dt))
+    if residual is not None:
+        residual = np.ascontiguousarray(residual).reshape(rows, n_out)
+    rc = lib().oracle_gemv_f16w(x_dt, int(round_x), _p(x), n_in, _p(w), _p(bias), act, slope,
+                                _p(residual), y_dt, _p(y), n_out, rows, n_out, n_in)
+    assert rc == 0
+    return y
 
 
 def pe_row(pos, D):

@@ -94,6 +94,30 @@ def test_epilogue_validation(gsvk_lib):
     assert L.gsvk_groupnorm_gelu(0, A, None, None, A + 4, 2, 8, 8, 1e-5, 1, None) == gsvk.E_ALIAS
 
 
+def test_gemv_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_gemv_f16w
+
+    def call(xdt=1, rx=1, x=A, ldx=64, w=B, bias=None, act=0, res=None, ydt=0, y=C, ldy=32,
+             rows=4, out=32, n_in=64):
+        return f(xdt, rx, x, ldx, w, bias, act, 0.0, res, ydt, y, ldy, rows, out, n_in, None)
+
+    assert call(xdt=2) == gsvk.E_DTYPE          # bf16 activations are not a reference input
+    assert call(ydt=5) == gsvk.E_DTYPE
+    assert call(act=4) == gsvk.E_DTYPE
+    assert call(x=None) == gsvk.E_NULL
+    assert call(w=None) == gsvk.E_NULL
+    assert call(y=None) == gsvk.E_NULL
+    assert call(rows=0) == gsvk.E_SIZE
+    assert call(n_in=0) == gsvk.E_SIZE
+    assert call(ldx=63) == gsvk.E_SIZE          # ldx < in
+    assert call(ldy=31) == gsvk.E_SIZE          # ldy < out
+    assert call(rows=65535 * 64 + 1) == gsvk.E_SIZE
+    assert call(y=A + 64) == gsvk.E_ALIAS       # over x
+    assert call(y=B + 128) == gsvk.E_ALIAS      # over the weights
+    assert call(bias=C + 16) == gsvk.E_ALIAS    # bias inside y
+    assert call(res=C + 4) == gsvk.E_ALIAS      # residual partly over y (res == y is allowed)
+
+
 def test_embed_validation(gsvk_lib):
     f = gsvk_lib.gsvk_embed_pe
     args = dict(out=0, tab=1, it=0, table=A, vocab=10, ids=B, pos=None, pos0=0, pe=C, max_pos=4,
@@ -138,6 +162,11 @@ void engine_like(float* x, const float* g, const float* b, float* ff, float* cur
   gsv::sovits::add_scaled_inplace(sum, cur, 1000, 1.f / 3);
   gsv::bert::layernorm1d_forward(x, g, b, 4, 1024);
   gsv::encoder::groupnorm_gelu(x, g, b, 512, 31999, 1e-5);
+  gsv::kern::gemv_f16w_f32acc(reinterpret_cast<const uint16_t*>(g), x, ff, 2048, 512);
+  gsv::kern::gemv_f16x_fmlal(reinterpret_cast<const uint16_t*>(g),
+                             reinterpret_cast<const uint16_t*>(b), ff, 2048, 512);
+  gsv::kern::gemv_fmlal_rows(reinterpret_cast<const uint16_t*>(g), x, ff, 64, 2048, 512, b,
+                             GSVK_ACT_RELU);
 }
 '''
     path = str(tmp_path / "compat_probe.cpp")

@@ -1,0 +1,200 @@
+"""GPU parity of gsvk_gemv_f16w (batched decode GEMV, fp16 weights, fused epilogue) against the
+oracle's restatement of kern::gemv_f16w_f32acc / kern::gemv_f16x_fmlal and the bias / act /
+residual loops of block_decode_impl.
+
+Tolerance: the sum is formed in another order than the reference's (matrix-core tiles and per-wave
+partials), so results are compared with the reference's own rule between two summation orders
+(test_kern.cpp:111-118): |got - want| <= 1e-5 * max(1, max |want| over the row). A 16-bit result
+may in addition sit one rounding step away (a pre-rounding difference at the 1e-5 level can cross a
+rounding boundary), and GELU adds its own fp32 tolerance (1e-6 + 1e-5 |v|). The golden vectors of
+the reference are also checked with the reference's gate (max rel 2e-5, cosine 1 - 1e-12).
+"""
+import numpy as np
+import pytest
+import torch
+
+import gsvk
+import oracle as O
+from conftest import check_close, load_bin
+from gpu_util import BF16, F16, F32, dev, devf, host, say
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(k):
+    return np.random.default_rng(20250823 + 9000 + k)
+
+
+def step16(dt, w):
+    w = np.abs(w.astype(np.float64))
+    if dt == F16:
+        return np.spacing(np.minimum(w, 65504).astype(np.float16)).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(w, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def assert_gemv_close(y_dt, got, want, act=gsvk.ACT_NONE, what=""):
+    g = O.to_f32(y_dt, got).astype(np.float64)
+    w = O.to_f32(y_dt, want).astype(np.float64)
+    assert g.shape == w.shape
+    assert np.array_equal(np.isnan(g), np.isnan(w)), f"{what}: NaN positions differ"
+    peak = np.maximum(1.0, np.nanmax(np.abs(w), axis=1, keepdims=True))
+    tol = 1e-5 * peak
+    if y_dt != F32:
+        tol = tol + step16(y_dt, w)
+    if act == gsvk.ACT_GELU_ERF:
+        tol = tol + 1e-6 + 1e-5 * np.abs(w)
+    err = np.abs(g - w)
+    err[np.isnan(w)] = 0
+    bad = np.argwhere(err > tol)
+    assert bad.size == 0, f"{what}: {len(bad)} outside tolerance, worst {np.max(err - tol):.3e} " \
+                          f"at {bad[:3].tolist()}"
+    return float(np.max(err / peak))
+
+
+def weights(r, n_out, n_in, scale=0.05):
+    return (scale * r.standard_normal((n_out, n_in))).astype(np.float16).view(np.uint16)
+
+
+def run_case(rows, n_out, n_in, x_dt, round_x, y_dt, act=gsvk.ACT_NONE, use_bias=True,
+             use_res=False, slope=0.1, seed=0):
+    say(f"gemv rows={rows} out={n_out} in={n_in} x={x_dt} round={round_x} y={y_dt} act={act} "
+        f"bias={use_bias} res={use_res}")
+    r = rng(seed + rows * 7 + n_out * 3 + n_in)
+    x32 = r.standard_normal((rows, n_in)).astype(np.float32)
+    x = O.to_storage(x_dt, x32)
+    w = weights(r, n_out, n_in)
+    bias = (0.02 * r.standard_normal(n_out)).astype(np.float32) if use_bias else None
+    res = O.to_storage(y_dt, r.standard_normal((rows, n_out)).astype(np.float32)) if use_res \
+        else None
+    want = O.gemv_f16w(x_dt, x, w, y_dt, bias=bias, act=act, slope=slope, residual=res,
+                       round_x=round_x)
+    X, W = dev(x, x_dt), dev(w, F16)
+    Y = torch.empty((rows, n_out), dtype=dev(np.zeros(1, O.storage_dtype(y_dt)), y_dt).dtype,
+                    device="cuda")
+    R = dev(res, y_dt) if use_res else None
+    gsvk.gemv_f16w(X, W, Y, bias=devf(bias) if use_bias else None, act=act, slope=slope,
+                   residual=R, round_x=round_x)
+    torch.cuda.synchronize()
+    return host(Y, y_dt), want, (X, W, bias, R, Y)
+
+
+# ---- the reference's golden vectors -------------------------------------------------------------
+
+@pytest.mark.parametrize("tag", ["gemv_a", "gemv_b"])
+def test_gemv_reference_golden(tag):
+    w = load_bin(f"{tag}_w.f16").view(np.uint16)
+    x = load_bin(f"{tag}_x.f32")
+    y = load_bin(f"{tag}_y.f32")
+    say(f"gemv golden {tag} {w.shape}")
+    X = devf(x[None, :])
+    Y = torch.empty((1, w.shape[0]), dtype=torch.float32, device="cuda")
+    gsvk.gemv_f16w(X, dev(w, F16), Y, round_x=False)
+    torch.cuda.synchronize()
+    got = host(Y, F32)[0]
+    ok, worst, cos = check_close(got, y, 2e-5, 1.0 - 1e-12)
+    assert ok, (worst, cos)
+    want = O.gemv_f16w(F32, x, w, F32, round_x=False)
+    assert_gemv_close(F32, got[None, :], want, what=tag)
+
+
+# ---- decode shapes (B = 64, d_model 512, ffn 2048, vocab 1025) -----------------------------------
+
+DECODE = [
+    # (name, out, in, act, bias, residual, y dtype)
+    ("qkv", 1536, 512, gsvk.ACT_NONE, True, False, F32),
+    ("out_proj", 512, 512, gsvk.ACT_NONE, True, True, F16),
+    ("w1_relu", 2048, 512, gsvk.ACT_RELU, True, False, F16),
+    ("w2", 512, 2048, gsvk.ACT_NONE, True, True, F16),
+    ("logits", 1025, 512, gsvk.ACT_NONE, False, False, F32),
+]
+
+
+@pytest.mark.parametrize("name,n_out,n_in,act,use_bias,use_res,y_dt", DECODE)
+@pytest.mark.parametrize("x_dt,round_x", [(F16, True), (F32, True), (F32, False)])
+def test_gemv_decode_shapes(name, n_out, n_in, act, use_bias, use_res, y_dt, x_dt, round_x):
+    got, want, _ = run_case(64, n_out, n_in, x_dt, round_x, y_dt, act, use_bias, use_res)
+    assert_gemv_close(y_dt, got, want, act, name)
+
+
+def test_gemv_split_mode_is_fp32_accurate():
+    """round_x = 0 must track the fp32 activations, not their fp16 rounding: against a float64
+    product it stays at fp32-accumulation level, ~100x below the fp16-rounding error."""
+    r = rng(1)
+    x = r.standard_normal((64, 512)).astype(np.float32)
+    w = weights(r, 512, 512)
+    exact = x.astype(np.float64) @ w.view(np.float16).astype(np.float64).T
+    Y = torch.empty((64, 512), dtype=torch.float32, device="cuda")
+    gsvk.gemv_f16w(devf(x), dev(w, F16), Y, round_x=False)
+    torch.cuda.synchronize()
+    err_split = np.max(np.abs(host(Y, F32) - exact))
+    gsvk.gemv_f16w(devf(x), dev(w, F16), Y, round_x=True)
+    torch.cuda.synchronize()
+    err_round = np.max(np.abs(host(Y, F32) - exact))
+    say(f"split err {err_split:.3e} round err {err_round:.3e}")
+    assert err_split < 1e-5 and err_round > 30 * err_split
+
+
+# ---- shapes off the tile grid, row counts off 64, all output types -------------------------------
+
+@pytest.mark.parametrize("rows,n_out,n_in", [
+    (1, 1, 1), (3, 8, 8), (64, 7, 7), (17, 17, 131),   # generic path (K % 8 != 0)
+    (1, 512, 512), (5, 33, 40), (63, 100, 72), (65, 130, 264), (130, 257, 1000),
+    (200, 48, 2056), (7, 3, 4096),
+])
+@pytest.mark.parametrize("y_dt", [F32, F16, BF16])
+def test_gemv_ragged(rows, n_out, n_in, y_dt):
+    got, want, _ = run_case(rows, n_out, n_in, F16, True, y_dt, gsvk.ACT_NONE, True, True,
+                            seed=11)
+    assert_gemv_close(y_dt, got, want, what=f"{rows}x{n_out}x{n_in}")
+
+
+@pytest.mark.parametrize("act", [gsvk.ACT_GELU_ERF, gsvk.ACT_LEAKY_RELU, gsvk.ACT_RELU])
+def test_gemv_activations(act):
+    got, want, _ = run_case(64, 3072, 768, F16, True, F16, act, True, False, slope=0.01, seed=3)
+    assert_gemv_close(F16, got, want, act, f"act {act}")
+
+
+def test_gemv_many_column_tiles():
+    """N >= 65536 takes the 64-column workgroup tiles."""
+    got, want, _ = run_case(16, 65536 + 40, 512, F16, True, F16, gsvk.ACT_RELU, True, False,
+                            seed=5)
+    assert_gemv_close(F16, got, want, gsvk.ACT_RELU, "wide")
+
+
+def test_gemv_residual_in_place_and_deterministic():
+    r = rng(9)
+    rows, n_out, n_in = 64, 512, 2048
+    x = O.to_storage(F16, r.standard_normal((rows, n_in)).astype(np.float32))
+    w = weights(r, n_out, n_in)
+    bias = (0.02 * r.standard_normal(n_out)).astype(np.float32)
+    h = O.to_storage(F16, r.standard_normal((rows, n_out)).astype(np.float32))
+    want = O.gemv_f16w(F16, x, w, F16, bias=bias, residual=h)
+    X, W, B = dev(x, F16), dev(w, F16), devf(bias)
+    outs = []
+    for _ in range(3):
+        Y = dev(h, F16)
+        gsvk.gemv_f16w(X, W, Y, bias=B, residual=Y)
+        torch.cuda.synchronize()
+        outs.append(host(Y, F16))
+    assert_gemv_close(F16, outs[0], want, what="in place")
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+def test_gemv_rejects_bad_arguments():
+    X = torch.zeros((4, 64), dtype=torch.float16, device="cuda")
+    W = torch.zeros((32, 64), dtype=torch.float16, device="cuda")
+    Y = torch.zeros((4, 32), dtype=torch.float32, device="cuda")
+    L = gsvk.lib()
+    assert L.gsvk_gemv_f16w(F16, 1, X.data_ptr(), 64, W.data_ptr(), None, 0, 0.0, None, F32,
+                            Y.data_ptr(), 32, 4, 32, 0, None) == gsvk.E_SIZE
+    assert L.gsvk_gemv_f16w(BF16, 1, X.data_ptr(), 64, W.data_ptr(), None, 0, 0.0, None, F32,
+                            Y.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_DTYPE
+    assert L.gsvk_gemv_f16w(F16, 1, X.data_ptr(), 64, W.data_ptr(), None, 9, 0.0, None, F32,
+                            Y.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_DTYPE
+    assert L.gsvk_gemv_f16w(F16, 1, X.data_ptr(), 64, W.data_ptr(), None, 0, 0.0, None, F32,
+                            X.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_ALIAS
+    assert L.gsvk_gemv_f16w(F16, 1, X.data_ptr(), 32, W.data_ptr(), None, 0, 0.0, None, F32,
+                            Y.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_SIZE
+    assert L.gsvk_gemv_f16w(F16, 1, None, 64, W.data_ptr(), None, 0, 0.0, None, F32,
+                            Y.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_NULL
