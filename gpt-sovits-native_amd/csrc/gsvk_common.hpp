@@ -160,8 +160,8 @@ struct Store<GSVK_BF16> : Store16<GSVK_BF16> {};
 // keeps one request in flight instead of all of them. So out-of-range indices are clamped to a
 // valid element (the value is discarded) and only stores are guarded, and an absent parameter
 // vector reads one of these constant rows instead of being skipped.
-static __device__ const float kZeros8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-static __device__ const float kOnes8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+static __device__ float kZeros8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+static __device__ float kOnes8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
 
 // Address of the 8-float parameter chunk starting at element i, or of a constant row when the
 // vector is absent.

@@ -5,18 +5,25 @@
 // (rows) at once. At B = 64 a weight element feeds 64 multiply-adds: 64 flop per weight byte,
 // above the fp32 VALU ridge of MI355X (157 TFLOP/s / 8 TB/s = 20) and far below the fp16 matrix
 // core one (2.5 PFLOP/s / 8 TB/s = 312), so the products go to v_mfma_f32_16x16x32_f16 and the
-// kernel stays bound by the weight stream from HBM.
+// kernel stays bound by memory.
 //
 // Tiles. Operand A of one MFMA is a 16 x 32 slice of W (16 output columns n, 32 k), operand B a
-// 32 x 16 slice of X^T (32 k, 16 rows r): lane l feeds row/column (l & 15) with the 8 k values of
-// its lane group (l >> 4). The accumulator then holds, in lane l, four consecutive outputs
+// 32 x 16 slice of X^T (32 k, 16 rows r): lane l feeds row/column (l & 15) with 8 k values chosen
+// by its lane group (l >> 4). The accumulator then holds, in lane l, four consecutive outputs
 // n = 4 (l >> 4) .. +3 of row (l & 15), stored as one vector. A and B use the same k slots, so
 // which 8 k a lane group holds is free: lane group g holds k = 64 kb + 16 g + 8 h .. +7 for the two
-// MFMAs h = 0, 1 of a 64-wide k block, which makes every wave load 128 contiguous bytes of each
-// weight row per k block.
-// A workgroup covers 64 rows x 16 NF columns; its WK waves split K into contiguous ranges and their
-// partial sums are added in wave order through LDS (a fixed order: results do not depend on
-// timing). Products fp16 x fp16 are exact in fp32; the sum is fp32.
+// MFMAs h = 0, 1 of a 64-wide k block.
+//
+// Staging. Read straight into that fragment layout, every 16-byte load instruction would touch 16
+// rows (one 128-byte line per row, half used), which runs at a fraction of the CU's load rate. So
+// each wave loads its k block as 8 rows x 128 contiguous bytes per instruction, writes it to a
+// private, padded LDS tile and reads the fragments back from there. A wave's LDS accesses execute
+// in issue order; a wavefront fence keeps the compiler from reordering them.
+//
+// Work split. A workgroup covers 16 MF rows x 16 NF columns over all of K; its WK waves split K
+// into contiguous k-block ranges and keep up to D k blocks of global loads in flight each. The
+// per-wave partial sums are added in wave order through LDS (a fixed order: results do not depend
+// on timing). Products fp16 x fp16 are exact in fp32; the sums are fp32.
 //
 // x in fp32: round_x = 1 rounds it to fp16 first (T2SEngine::gemv_fmlal, t2s_engine.cpp:696-700);
 // round_x = 0 keeps the fp32 value (kern::gemv_f16w_f32acc, gemv.cpp:112-127) by feeding
@@ -30,13 +37,13 @@ namespace gsvk {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
-typedef float f8v __attribute__((ext_vector_type(8)));
 
 enum XMode { kXF16 = 0, kXRound = 1, kXSplit = 2 };
 
-constexpr int kRowsPerGroup = 64;  // 4 fragments of 16 rows
 constexpr long kMaxRowGroups = 65535;
+constexpr int kRowHalves = 72;  // LDS row: 64 k + 8 halves of padding (144 bytes)
 
 struct GvArgs {
   const void* x;
@@ -46,45 +53,9 @@ struct GvArgs {
   void* y;
   long M, N, K, ldx, ldy;
   int act;
-  int ydt;
   float slope;
   bool vec_store;
 };
-
-// 8 consecutive k of one weight row; zero when the k block lies past K (the address is clamped to
-// the row's last 8 values, so the load itself stays in bounds and outside any branch).
-__device__ __forceinline__ h8 load_w8(const uint16_t* w, size_t off, bool ok) {
-  u32x4 q = ld16<false>(w + off);
-  if (!ok) q = u32x4{0u, 0u, 0u, 0u};
-  return __builtin_bit_cast(h8, q);
-}
-
-// 8 consecutive k of one activation row as fp16 (hi) and, in split mode, the fp16 remainder (lo).
-template <int XM>
-__device__ __forceinline__ void load_x8(const void* x, size_t off, bool ok, h8& hi, h8& lo) {
-  if constexpr (XM == kXF16) {
-    u32x4 q = ld16<false>(static_cast<const uint16_t*>(x) + off);
-    if (!ok) q = u32x4{0u, 0u, 0u, 0u};
-    hi = __builtin_bit_cast(h8, q);
-  } else {
-    const float* p = static_cast<const float*>(x) + off;
-    const u32x4 q0 = ld16<false>(p), q1 = ld16<false>(p + 4);
-    uint32_t u[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      u[k] = q0[k];
-      u[4 + k] = q1[k];
-    }
-    f8v f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) f[k] = ok ? __builtin_bit_cast(float, u[k]) : 0.f;
-    hi = __builtin_convertvector(f, h8);
-    if constexpr (XM == kXSplit) {
-      const f8v rest = f - __builtin_convertvector(hi, f8v);
-      lo = __builtin_convertvector(rest, h8);
-    }
-  }
-}
 
 __device__ __forceinline__ float act_rt(int act, float v, float slope) {
   switch (act) {
@@ -95,45 +66,67 @@ __device__ __forceinline__ float act_rt(int act, float v, float slope) {
   }
 }
 
-__device__ __forceinline__ float load_y(int dt, const void* p, size_t i) {
-  switch (dt) {
-    case GSVK_F32: return static_cast<const float*>(p)[i];
-    case GSVK_F16: return h2f(static_cast<const uint16_t*>(p)[i]);
-    default: return bf2f(static_cast<const uint16_t*>(p)[i]);
-  }
+template <int YDT>
+__device__ __forceinline__ float load_y(const void* p, size_t i) {
+  if constexpr (YDT == GSVK_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (YDT == GSVK_F16) return h2f(static_cast<const uint16_t*>(p)[i]);
+  else return bf2f(static_cast<const uint16_t*>(p)[i]);
 }
 
-__device__ __forceinline__ void store_y(int dt, void* p, size_t i, float v) {
-  switch (dt) {
-    case GSVK_F32: static_cast<float*>(p)[i] = v; break;
-    case GSVK_F16: static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f2h(v)); break;
-    default: static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f2bf(v)); break;
-  }
+template <int YDT>
+__device__ __forceinline__ void store_y(void* p, size_t i, float v) {
+  if constexpr (YDT == GSVK_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (YDT == GSVK_F16) static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f2h(v));
+  else static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f2bf(v));
 }
 
-// One output: v = act(acc + bias[n]) (+ residual[m, n]). The bias add is skipped, not replaced by
-// + 0, when there is no bias (x + 0 would turn -0 into +0).
-__device__ __forceinline__ float epilogue(const GvArgs& a, long m, long n, float v) {
-  if (a.bias) v = v + a.bias[n];
+// Epilogue operands of four consecutive outputs n .. n+3 of row m: bias[n + q] and
+// residual[m, n + q], read from clamped indices (an in-bounds dummy when absent: the value is then
+// not used) so the loads need no branch.
+struct EpiIn {
+  float b[4];
+  float r[4];
+};
+
+template <int YDT>
+__device__ __forceinline__ EpiIn epi_load(const GvArgs& a, long m, long n) {
+  EpiIn e;
+  const size_t mr = static_cast<size_t>(min(m, a.M - 1)) * a.ldy;
+  const float* bp = a.bias ? a.bias : kZeros8;
+  const void* rp = a.res ? a.res : static_cast<const void*>(kZeros8);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const long nq = min(n + q, a.N - 1);
+    e.b[q] = bp[a.bias ? nq : 0];
+    e.r[q] = load_y<YDT>(rp, a.res ? mr + nq : 0);
+  }
+  return e;
+}
+
+// v = act(acc + bias[n]) (+ residual[m, n]). The bias add is skipped, not replaced by + 0, when
+// there is no bias (x + 0 would turn -0 into +0); likewise the residual add.
+__device__ __forceinline__ float epilogue(const GvArgs& a, float v, float b, float r) {
+  if (a.bias) v = v + b;
   v = act_rt(a.act, v, a.slope);
-  if (a.res) v = v + load_y(a.ydt, a.res, static_cast<size_t>(m) * a.ldy + n);
+  if (a.res) v = v + r;
   return v;
 }
 
 // Four consecutive outputs n .. n+3 of row m.
-__device__ __forceinline__ void finish4(const GvArgs& a, long m, long n, f4v s) {
+template <int YDT>
+__device__ __forceinline__ void finish4(const GvArgs& a, long m, long n, f4v s, const EpiIn& e) {
   if (m >= a.M) return;
   const size_t off = static_cast<size_t>(m) * a.ldy + n;
-  if (a.vec_store && n + 4 <= a.N) {
-    float v[4];
+  float v[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = epilogue(a, m, n + q, s[q]);
-    if (a.ydt == GSVK_F32) {
+  for (int q = 0; q < 4; ++q) v[q] = epilogue(a, s[q], e.b[q], e.r[q]);
+  if (a.vec_store && n + 4 <= a.N) {
+    if constexpr (YDT == GSVK_F32) {
       *reinterpret_cast<float4*>(static_cast<float*>(a.y) + off) = float4{v[0], v[1], v[2], v[3]};
     } else {
       uint32_t h[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) h[q] = a.ydt == GSVK_F16 ? f2h(v[q]) : f2bf(v[q]);
+      for (int q = 0; q < 4; ++q) h[q] = YDT == GSVK_F16 ? f2h(v[q]) : f2bf(v[q]);
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + off) =
           uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     }
@@ -141,79 +134,234 @@ __device__ __forceinline__ void finish4(const GvArgs& a, long m, long n, f4v s) 
   }
 #pragma unroll
   for (int q = 0; q < 4; ++q)
-    if (n + q < a.N) store_y(a.ydt, a.y, off + q, epilogue(a, m, n + q, s[q]));
+    if (n + q < a.N) store_y<YDT>(a.y, off + q, v[q]);
 }
 
-template <int XM, int NF, int WK>
+// One k block as loaded from global memory. 16-bit rows: 128 bytes per row, instruction q covers
+// rows 8q .. 8q+7 (lane l: row l / 8, bytes 16 (l % 8)). fp32 rows: 256 bytes per row,
+// instruction q covers rows 4q .. 4q+3 (lane l: row l / 16, bytes 16 (l % 16)).
+template <int XM>
+constexpr int x_insts() { return XM == kXF16 ? 2 : 4; }
+
+// The in-range flags travel with the data: zeroing a value right after its load would make the
+// wave wait for that load there, so k blocks past K are zeroed only when they are staged (and only
+// in the TAIL instantiation, for K % 64 != 0).
+template <int XM, int MF, int NF>
+struct Raw {
+  u32x4 w[NF][2];
+  u32x4 x[MF][x_insts<XM>()];
+  bool okw, okx;
+};
+
+// Per-wave LDS tile of one k block: NF weight fragments, MF activation fragments (and MF
+// remainders in split mode), 16 rows of kRowHalves each.
+template <int XM, int MF, int NF>
+constexpr int stage_halves() {
+  return (NF + MF * (XM == kXSplit ? 2 : 1)) * 16 * kRowHalves;
+}
+
+template <int XM, int YDT, int MF, int NF, int WK, int D, bool TAIL>
 __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
-  __shared__ f4v red[WK > 1 ? WK : 1][4 * NF][kWave];
+  constexpr int T = MF * NF;  // 16 x 16 output tiles of the workgroup
+  constexpr int SH = stage_halves<XM, MF, NF>();
+  constexpr int kStageBytes = WK * SH * 2;
+  constexpr int kRedBytes = WK > 1 ? WK * T * kWave * 16 : 16;
+  __shared__ __attribute__((aligned(16))) char smem[kStageBytes > kRedBytes ? kStageBytes
+                                                                              : kRedBytes];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int r16 = lane & 15, grp = lane >> 4;
-  const long m0 = static_cast<long>(blockIdx.y) * kRowsPerGroup;
+  const long m0 = static_cast<long>(blockIdx.y) * (16 * MF);
   const long n0 = static_cast<long>(blockIdx.x) * (16 * NF);
   const long nkb = (a.K + 63) >> 6;
   const long per = (nkb + WK - 1) / WK;
   const long kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
 
-  size_t xoff[4], woff[NF];
+  // Each wave finishes tiles wave, wave + WK, ... (TPW of them at most). With few enough tiles it
+  // fetches their epilogue operands first, so that latency hides under the main loads.
+  constexpr int TPW = (T + WK - 1) / WK;
+  constexpr bool kPrefetch = TPW <= 4;
+  EpiIn pre[kPrefetch ? TPW : 1];
+  if constexpr (kPrefetch) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xoff[i] = static_cast<size_t>(min(m0 + 16 * i + r16, a.M - 1)) * a.ldx;
-#pragma unroll
-  for (int j = 0; j < NF; ++j) woff[j] = static_cast<size_t>(min(n0 + 16 * j + r16, a.N - 1)) * a.K;
+    for (int u = 0; u < TPW; ++u) {
+      const int t = min(wave + u * WK, T - 1);
+      pre[u] = epi_load<YDT>(a, m0 + 16 * (t / NF) + r16, n0 + 16 * (t % NF) + 4 * grp);
+    }
+  }
 
-  f4v acc[4][NF];
+  // Global rows this lane loads (clamped: rows past M or N load a valid row that is never stored).
+  constexpr int XQ = x_insts<XM>();
+  constexpr int XLPR = XQ == 2 ? 8 : 16;  // lanes per x row in one instruction
+  size_t wrow[NF][2], xrow[MF][XQ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < NF; ++j)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      wrow[j][q] = static_cast<size_t>(min(n0 + 16 * j + 8 * q + lane / 8, a.N - 1)) * a.K;
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int q = 0; q < XQ; ++q)
+      xrow[i][q] =
+          static_cast<size_t>(min(m0 + 16 * i + (16 / XQ) * q + lane / XLPR, a.M - 1)) * a.ldx;
+
+  auto load = [&](Raw<XM, MF, NF>& r, long kb) {
+    const long kw = kb * 64 + (lane % 8) * 8;  // 8 halves per lane
+    r.okw = !TAIL || kw < a.K;
+    const size_t kcw = static_cast<size_t>(r.okw ? kw : a.K - 8);
+#pragma unroll
+    for (int j = 0; j < NF; ++j)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) r.w[j][q] = ld16<false>(a.w + wrow[j][q] + kcw);
+    if constexpr (XM == kXF16) {
+      r.okx = r.okw;
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          r.x[i][q] = ld16<false>(static_cast<const uint16_t*>(a.x) + xrow[i][q] + kcw);
+    } else {
+      const long kx = kb * 64 + (lane % 16) * 4;  // 4 floats per lane
+      r.okx = !TAIL || kx < a.K;
+      const size_t kcx = static_cast<size_t>(r.okx ? kx : a.K - 4);
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          r.x[i][q] = ld16<false>(static_cast<const float*>(a.x) + xrow[i][q] + kcx);
+    }
+  };
+
+  _Float16* st_w = reinterpret_cast<_Float16*>(smem) + wave * SH;
+  _Float16* st_x = st_w + NF * 16 * kRowHalves;
+  _Float16* st_l = st_x + MF * 16 * kRowHalves;  // split mode: remainders
+
+  auto stage = [&](const Raw<XM, MF, NF>& r) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < NF; ++j)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        *reinterpret_cast<u32x4*>(st_w + (j * 16 + 8 * q + lane / 8) * kRowHalves +
+                                  (lane % 8) * 8) = r.okw ? r.w[j][q] : zero;
+    if constexpr (XM == kXF16) {
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          *reinterpret_cast<u32x4*>(st_x + (i * 16 + 8 * q + lane / 8) * kRowHalves +
+                                    (lane % 8) * 8) = r.okx ? r.x[i][q] : zero;
+    } else {
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4v f = __builtin_bit_cast(f4v, r.okx ? r.x[i][q] : zero);
+          const h4 hi = __builtin_convertvector(f, h4);
+          const int off = (i * 16 + 4 * q + lane / 16) * kRowHalves + (lane % 16) * 4;
+          *reinterpret_cast<h4*>(st_x + off) = hi;
+          if constexpr (XM == kXSplit) {
+            const f4v rest = f - __builtin_convertvector(hi, f4v);
+            *reinterpret_cast<h4*>(st_l + off) = __builtin_convertvector(rest, h4);
+          }
+        }
+    }
+  };
+
+  f4v acc[MF][NF];
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
 #pragma unroll
     for (int j = 0; j < NF; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
 
-  // Fragments of one 64-wide k block: [h][j] weights, [h][i] activations.
-  h8 wv[2][NF], xh[2][4], xl[2][4];
-  auto load = [&](long kb) {
+  auto compute = [&]() {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const long k = kb * 64 + grp * 16 + h * 8;
-      const bool ok = k < a.K;
-      const size_t kc = static_cast<size_t>(ok ? k : a.K - 8);
-#pragma unroll
-      for (int j = 0; j < NF; ++j) wv[h][j] = load_w8(a.w, woff[j] + kc, ok);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) load_x8<XM>(a.x, xoff[i] + kc, ok, xh[h][i], xl[h][i]);
-    }
-  };
-  for (long kb = kb0; kb < kb1; ++kb) {
-    load(kb);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NF; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[h][j], xh[h][i], acc[i][j], 0, 0, 0);
-          if constexpr (XM == kXSplit)
-            acc[i][j] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[h][j], xl[h][i], acc[i][j], 0, 0, 0);
-        }
-  }
-
-  if constexpr (WK == 1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+      const int col = grp * 16 + h * 8;
+      h8 wv[NF], xh[MF], xl[MF];
 #pragma unroll
       for (int j = 0; j < NF; ++j)
-        finish4(a, m0 + 16 * i + r16, n0 + 16 * j + 4 * grp, acc[i][j]);
-  } else {
+        wv[j] = *reinterpret_cast<const h8*>(st_w + (j * 16 + r16) * kRowHalves + col);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MF; ++i) {
+        xh[i] = *reinterpret_cast<const h8*>(st_x + (i * 16 + r16) * kRowHalves + col);
+        if constexpr (XM == kXSplit)
+          xl[i] = *reinterpret_cast<const h8*>(st_l + (i * 16 + r16) * kRowHalves + col);
+      }
 #pragma unroll
-      for (int j = 0; j < NF; ++j) red[wave][i * NF + j][lane] = acc[i][j];
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[j], xh[i], acc[i][j], 0, 0, 0);
+          if constexpr (XM == kXSplit)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[j], xl[i], acc[i][j], 0, 0, 0);
+        }
+    }
+  };
+  // Stage a block, read its fragments, multiply. The fences keep this wave's LDS writes and reads
+  // in program order (the LDS executes one wave's accesses in issue order).
+  auto process = [&](const Raw<XM, MF, NF>& r) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    stage(r);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    compute();
+  };
+
+  // Rolling prefetch: D k blocks of global loads in flight. Block indices past the wave's range
+  // are clamped to its last block (an in-bounds reload whose result is not used), so no load sits
+  // under a branch.
+  if (kb0 < kb1) {
+    Raw<XM, MF, NF> f[D];
+    const long nr = (kb1 - kb0 + D - 1) / D;
+#pragma unroll
+    for (int s = 0; s < D; ++s) load(f[s], min(kb0 + s, kb1 - 1));
+    for (long r = 0; r + 1 < nr; ++r) {
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        process(f[s]);
+        load(f[s], min(kb0 + (r + 1) * D + s, kb1 - 1));
+      }
+    }
+    const long kl = kb0 + (nr - 1) * D;
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+      if (kl + s < kb1) process(f[s]);
+  }
+
+  // Workgroup sum of the wave partials, tile t by wave t % WK, waves added in order. The reduction
+  // area reuses the staging LDS, so every wave must be done with it first.
+  f4v* red = reinterpret_cast<f4v*>(smem);
+  if constexpr (WK > 1) {
     __syncthreads();
-    for (int t = wave; t < 4 * NF; t += WK) {
-      f4v s = red[0][t][lane];
 #pragma unroll
-      for (int w = 1; w < WK; ++w) s = s + red[w][t][lane];
-      const int i = t / NF, j = t % NF;
-      finish4(a, m0 + 16 * i + r16, n0 + 16 * j + 4 * grp, s);
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < NF; ++j) red[(wave * T + i * NF + j) * kWave + lane] = acc[i][j];
+    __syncthreads();
+  }
+  for (int t = wave; t < T; t += WK) {
+    f4v s;
+    if constexpr (WK > 1) {
+      s = red[t * kWave + lane];
+#pragma unroll
+      for (int w = 1; w < WK; ++w) s = s + red[(w * T + t) * kWave + lane];
+    } else {
+      s = acc[0][0];
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NF; ++j)
+          if (i * NF + j == t) s = acc[i][j];
+    }
+    const long m = m0 + 16 * (t / NF) + r16, n = n0 + 16 * (t % NF) + 4 * grp;
+    if constexpr (kPrefetch) {
+      EpiIn e = pre[0];
+#pragma unroll
+      for (int u = 1; u < TPW; ++u)
+        if (wave + u * WK == t) e = pre[u];
+      finish4<YDT>(a, m, n, s, e);
+    } else {
+      finish4<YDT>(a, m, n, s, epi_load<YDT>(a, m, n));
     }
   }
 }
@@ -221,7 +369,7 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
 // Any shape or alignment: one thread per output, k in order with fmaf (the product of an fp16
 // weight and an fp16 or fp32 activation is formed exactly or rounded once, then added: the
 // reference's vfmaq / fmlal step). Used when K % 8 != 0 or a row is not 16-byte aligned.
-template <int XM>
+template <int XM, int YDT>
 __global__ __launch_bounds__(256) void gemv_generic(GvArgs a) {
   const long total = a.M * a.N;
   for (long t = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
@@ -240,37 +388,55 @@ __global__ __launch_bounds__(256) void gemv_generic(GvArgs a) {
       }
       s = __builtin_fmaf(h2f(wr[k]), xv, s);
     }
-    store_y(a.ydt, a.y, static_cast<size_t>(m) * a.ldy + n, epilogue(a, m, n, s));
+    const size_t off = static_cast<size_t>(m) * a.ldy + n;
+    const float b = a.bias ? a.bias[n] : 0.f;
+    const float r = a.res ? load_y<YDT>(a.res, off) : 0.f;
+    store_y<YDT>(a.y, off, epilogue(a, s, b, r));
   }
 }
 
-template <int XM, int NF, int WK>
+// ---- launch plan ---------------------------------------------------------------------------------
+
+template <int XM, int YDT, int MF, int NF, int WK, int D>
 void launch_tiles(const GvArgs& a, hipStream_t st) {
   const long gx = (a.N + 16 * NF - 1) / (16 * NF);
-  const long gy = (a.M + kRowsPerGroup - 1) / kRowsPerGroup;
-  hipLaunchKernelGGL((gemv_mfma<XM, NF, WK>), dim3(static_cast<unsigned>(gx),
-                                                   static_cast<unsigned>(gy)),
-                     dim3(kWave * WK), 0, st, a);
+  const long gy = (a.M + 16 * MF - 1) / (16 * MF);
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  // K a multiple of 64 (every decode shape) needs no zeroing of a partial last k block.
+  if (a.K % 64 == 0)
+    hipLaunchKernelGGL((gemv_mfma<XM, YDT, MF, NF, WK, D, false>), grid, dim3(kWave * WK), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemv_mfma<XM, YDT, MF, NF, WK, D, true>), grid, dim3(kWave * WK), 0, st, a);
+}
+
+template <int XM, int YDT>
+void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
+  if (!tiled) {
+    const long blocks = std::min<long>((a.M * a.N + 255) / 256, 4096);
+    hipLaunchKernelGGL((gemv_generic<XM, YDT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       st, a);
+    return;
+  }
+  const long nkb = (a.K + 63) / 64;
+  const long tiles = (a.N + 15) / 16 * ((a.M + 15) / 16);
+  // A long weight stream (many 16 x 16 tiles): 64 x 64 tiles, so activations and weights are each
+  // re-read from L2 once per 64 columns / rows. Decode shapes: 16 x 16 tiles (the most workgroups)
+  // and K over up to 8 waves.
+  if (tiles >= 16384) return launch_tiles<XM, YDT, 4, 4, 2, 2>(a, st);
+  if (nkb >= 16) return launch_tiles<XM, YDT, 1, 1, 8, 2>(a, st);
+  if (nkb >= 8) return launch_tiles<XM, YDT, 1, 1, 8, 1>(a, st);
+  if (nkb >= 4) return launch_tiles<XM, YDT, 1, 1, 4, 1>(a, st);
+  if (nkb >= 2) return launch_tiles<XM, YDT, 1, 1, 2, 1>(a, st);
+  launch_tiles<XM, YDT, 1, 1, 1, 1>(a, st);
 }
 
 template <int XM>
-void launch_xm(const GvArgs& a, bool tiled, hipStream_t st) {
-  if (!tiled) {
-    const long blocks = std::min<long>((a.M * a.N + 255) / 256, 4096);
-    hipLaunchKernelGGL((gemv_generic<XM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
-                       a);
-    return;
+void launch_xm(int ydt, const GvArgs& a, bool tiled, hipStream_t st) {
+  switch (ydt) {
+    case GSVK_F32: return launch_plan<XM, GSVK_F32>(a, tiled, st);
+    case GSVK_F16: return launch_plan<XM, GSVK_F16>(a, tiled, st);
+    default: return launch_plan<XM, GSVK_BF16>(a, tiled, st);
   }
-  const long tiles16 = (a.N + 15) / 16 * ((a.M + kRowsPerGroup - 1) / kRowsPerGroup);
-  const long nkb = (a.K + 63) >> 6;
-  // Many column tiles (a long weight stream): 64 columns per workgroup so the activations are
-  // re-read once per 64 columns instead of once per 16. Few tiles (decode shapes): 16 columns per
-  // workgroup and K split over up to 8 waves to put more requests in flight per CU.
-  if (tiles16 >= 4096) return launch_tiles<XM, 4, 4>(a, st);
-  if (nkb >= 8) return launch_tiles<XM, 1, 8>(a, st);
-  if (nkb >= 4) return launch_tiles<XM, 1, 4>(a, st);
-  if (nkb >= 2) return launch_tiles<XM, 1, 2>(a, st);
-  launch_tiles<XM, 1, 1>(a, st);
 }
 
 }  // namespace
@@ -287,8 +453,8 @@ extern "C" int gsvk_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ld
   if (act < GSVK_ACT_NONE || act > GSVK_ACT_LEAKY_RELU) return GSVK_E_DTYPE;
   if (!x || !w || !y) return GSVK_E_NULL;
   if (rows == 0 || out == 0 || in == 0 || ldx < in || ldy < out) return GSVK_E_SIZE;
-  if (rows > static_cast<size_t>(kMaxRowGroups) * kRowsPerGroup || out > (1ul << 31) ||
-      in > (1ul << 31) || ldx > (1ul << 40) || ldy > (1ul << 40))
+  if (rows > static_cast<size_t>(kMaxRowGroups) * 16 || out > (1ul << 31) || in > (1ul << 31) ||
+      ldx > (1ul << 40) || ldy > (1ul << 40))
     return GSVK_E_SIZE;
   const size_t xsz = dtype_size(x_dtype), ysz = dtype_size(y_dtype);
   const size_t ybytes = span_bytes(rows, out, ldy, ysz);
@@ -298,18 +464,18 @@ extern "C" int gsvk_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ld
   if (residual && residual != y && overlaps(y, ybytes, residual, ybytes)) return GSVK_E_ALIAS;
 
   GvArgs a{x, w, bias, residual, y, static_cast<long>(rows), static_cast<long>(out),
-           static_cast<long>(in), static_cast<long>(ldx), static_cast<long>(ldy), act, y_dtype,
-           slope, false};
+           static_cast<long>(in), static_cast<long>(ldx), static_cast<long>(ldy), act, slope,
+           false};
   const size_t yalign = y_dtype == GSVK_F32 ? 16 : 8;
   a.vec_store = ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % yalign == 0;
-  // Matrix-core tiles need 16-byte rows: K % 8 == 0, and aligned x rows and weights.
+  // Matrix-core tiles need 16-byte rows: K % 8 == 0, aligned x rows and weights.
   const bool tiled = in % 8 == 0 && aligned16(w) && aligned16(x) && (ldx * xsz) % 16 == 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int xm = x_dtype == GSVK_F16 ? kXF16 : (round_x ? kXRound : kXSplit);
   switch (xm) {
-    case kXF16: launch_xm<kXF16>(a, tiled, st); break;
-    case kXRound: launch_xm<kXRound>(a, tiled, st); break;
-    default: launch_xm<kXSplit>(a, tiled, st); break;
+    case kXF16: launch_xm<kXF16>(y_dtype, a, tiled, st); break;
+    case kXRound: launch_xm<kXRound>(y_dtype, a, tiled, st); break;
+    default: launch_xm<kXSplit>(y_dtype, a, tiled, st); break;
   }
   return launch_status();
 }

@@ -111,7 +111,7 @@ def test_gemv_validation(gsvk_lib):
     assert call(n_in=0) == gsvk.E_SIZE
     assert call(ldx=63) == gsvk.E_SIZE          # ldx < in
     assert call(ldy=31) == gsvk.E_SIZE          # ldy < out
-    assert call(rows=65535 * 64 + 1) == gsvk.E_SIZE
+    assert call(rows=65535 * 16 + 1) == gsvk.E_SIZE
     assert call(y=A + 64) == gsvk.E_ALIAS       # over x
     assert call(y=B + 128) == gsvk.E_ALIAS      # over the weights
     assert call(bias=C + 16) == gsvk.E_ALIAS    # bias inside y
@@ -167,6 +167,8 @@ void engine_like(float* x, const float* g, const float* b, float* ff, float* cur
                              reinterpret_cast<const uint16_t*>(b), ff, 2048, 512);
   gsv::kern::gemv_fmlal_rows(reinterpret_cast<const uint16_t*>(g), x, ff, 64, 2048, 512, b,
                              GSVK_ACT_RELU);
+  gsv::kern::gemv_fmlal_rows(reinterpret_cast<const uint16_t*>(g), x, ff, 64, 2048, 512, b,
+                             GSVK_ACT_RELU, x);
 }
 '''
     path = str(tmp_path / "compat_probe.cpp")
