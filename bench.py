@@ -320,6 +320,42 @@ def kernel_suite(torch, gsvk, dev, only=None):
     for kind, count in (("K3", 1), ("K2", 6), ("K1", 9)):
         for dt, nm, rep in ((f32, "f32", 8), (f16, "f16", 16)):
             run(f"sovits_{kind}_{nm}_24x320000", 5, *sv_case(kind, dt, rep), count)
+
+    # T2S decode GEMVs with their fused epilogues, B = 64 rows (t2s_engine.cpp:1044-1116): the
+    # stated shape cycles through 24 distinct weight matrices (one per layer, as a decode step
+    # does); the replicated case is one weight stream of `rep` such matrices stacked along N.
+    def gemv_case(N, K, act, use_bias, use_res, ydt, rep, layers=24):
+        yesz = 4 if ydt == f32 else 2
+
+        def make(k):
+            n = N * k
+            nw = layers if k == 1 else 1
+            Ws = [rn(n, K, std=0.05) for _ in range(nw)]
+            x = rn(B, K)
+            bi = rn(n, dtype=f32, std=0.02) if use_bias else None
+            y = torch.empty(B, n, dtype=ydt, device=dev)
+            res = rn(B, n, dtype=ydt) if use_res else None
+            it = [0]
+
+            def call():
+                w = Ws[it[0] % nw]
+                it[0] += 1
+                gsvk.gemv_f16w(x, w, y, bias=bi, act=act, residual=res)
+            return call
+
+        def nbytes(k):
+            n = N * k
+            return (n * K * 2 + B * K * 2 + B * n * yesz + (n * 4 if use_bias else 0) +
+                    (B * n * yesz if use_res else 0))
+        return (lambda: make(1), lambda: (rep, make(rep)), nbytes)
+
+    for name, N, K, act, ub, ur, ydt, rep, count in (
+            ("qkv_bias_f32out", 1536, 512, gsvk.ACT_NONE, True, False, f32, 128, 24),
+            ("outproj_bias_residual", 512, 512, gsvk.ACT_NONE, True, True, f16, 256, 24),
+            ("w1_bias_relu", 2048, 512, gsvk.ACT_RELU, True, False, f16, 64, 24),
+            ("w2_bias_residual", 512, 2048, gsvk.ACT_NONE, True, True, f16, 128, 24),
+            ("logits_f32out", 1025, 512, gsvk.ACT_NONE, False, False, f32, 128, 1)):
+        run(f"gemv_{name}_64x{N}x{K}", 2, *gemv_case(N, K, act, ub, ur, ydt, rep), count)
     return out
 
 

@@ -419,12 +419,16 @@ void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
   }
   const long nkb = (a.K + 63) / 64;
   const long tiles = (a.N + 15) / 16 * ((a.M + 15) / 16);
-  // A long weight stream (many 16 x 16 tiles): 64 x 64 tiles, so activations and weights are each
-  // re-read from L2 once per 64 columns / rows. Decode shapes: 16 x 16 tiles (the most workgroups)
-  // and K over up to 8 waves.
-  if (tiles >= 16384) return launch_tiles<XM, YDT, 4, 4, 2, 2>(a, st);
+  // A long weight stream (many 16 x 16 tiles): 64-row tiles, so the weights are re-read from L2
+  // once per 64 rows, and 32 or 64 columns. Decode shapes: 16 x 16 tiles (the most workgroups),
+  // K over 4 or 8 waves with two k blocks each in flight (measured best on MI355X at B = 64 for
+  // K = 512 and 2048).
+  if (tiles >= 16384) {
+    if (nkb > 16) return launch_tiles<XM, YDT, 4, 4, 2, 2>(a, st);
+    return launch_tiles<XM, YDT, 4, 2, 4, 2>(a, st);
+  }
   if (nkb >= 16) return launch_tiles<XM, YDT, 1, 1, 8, 2>(a, st);
-  if (nkb >= 8) return launch_tiles<XM, YDT, 1, 1, 8, 1>(a, st);
+  if (nkb >= 8) return launch_tiles<XM, YDT, 1, 1, 4, 2>(a, st);
   if (nkb >= 4) return launch_tiles<XM, YDT, 1, 1, 4, 1>(a, st);
   if (nkb >= 2) return launch_tiles<XM, YDT, 1, 1, 2, 1>(a, st);
   launch_tiles<XM, YDT, 1, 1, 1, 1>(a, st);
