@@ -26,6 +26,9 @@ SIGNATURES = {
     "gsvk_bias_act": (_i, [_i, _i, _vp, _vp, _vp, _sz, _sz, _sz, _f, _vp]),
     "gsvk_gemv_f16w": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _i, _vp, _sz, _sz, _sz, _sz,
                             _vp]),
+    "gsvk_decode_attention": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz,
+                                   _sz, _vp, _sz, _vp, _vp]),
+    "gsvk_decode_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
     "gsvk_groupnorm_gelu": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _d, _i, _vp]),
     "gsvk_leaky_relu": (_i, [_i, _vp, _vp, _sz, _f, _vp]),
     "gsvk_resblock_add_lrelu": (_i, [_i, _vp, _vp, _vp, _sz, _f, _vp]),
@@ -130,6 +133,44 @@ def gemv_f16w(x, w, y, bias=None, act=ACT_NONE, slope=0.0, residual=None, round_
                   lib().gsvk_gemv_f16w(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(w),
                                        _ptr(bias), act, slope, _ptr(residual), dtype_code(y),
                                        _ptr(y), ldy, rows, n_out, n_in, _stream(stream)))
+
+
+_WS = {}
+
+
+def workspace(device, nbytes):
+    """A device scratch tensor of at least nbytes, kept per device for the process. Grow it before
+    any graph capture (allocation is not allowed while capturing)."""
+    import torch
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", key))
+        _WS[key] = ws
+    return ws
+
+
+def decode_attention(qkv, k_cache, v_cache, pos, out, heads, len_bound=0, err=None, stream=None,
+                     use_workspace=True):
+    """Append k / v at pos and attend. qkv [B, >=3D] fp32; caches [B, max_len, D]; pos [B] int64;
+    out [B, D]."""
+    B = qkv.shape[0]
+    D = out.shape[-1]
+    max_len = k_cache.shape[1]
+    hd = D // heads
+    ws, wsb = None, 0
+    if use_workspace:
+        need = lib().gsvk_decode_attention_workspace_bytes(B, heads, hd, len_bound or max_len)
+        if need:
+            w = workspace(out.device, need)
+            ws, wsb = w.data_ptr(), w.numel()
+    return _check("gsvk_decode_attention",
+                  lib().gsvk_decode_attention(dtype_code(k_cache), dtype_code(out), _ptr(qkv),
+                                              _rows(qkv)[2], _ptr(k_cache), _ptr(v_cache),
+                                              max_len, _ptr(pos), _ptr(out), _rows(out)[2], B,
+                                              heads, hd, len_bound, ws, wsb, _ptr(err),
+                                              _stream(stream)))
 
 
 def groupnorm_gelu(x, gamma, beta, y, eps, apply_gelu=True, stream=None):

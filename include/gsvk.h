@@ -114,6 +114,38 @@ int gsvk_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const ui
                    void* y, size_t ldy, size_t rows, size_t out, size_t in, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * T2S decode attention with the KV append, B sequences at once.
+ *   for each sequence b, p = pos[b]:
+ *     k_cache[b, p, :] = k, v_cache[b, p, :] = v      (k, v = qkv[b, D:2D], qkv[b, 2D:3D], rounded
+ *                                                       once to kv_dtype)
+ *     for each head h:  s_j = (q_h . K[b, j, h]) * (1 / sqrtf(head_dim)),  j = 0 .. p
+ *                       out[b, h*HD : (h+1)*HD] = sum_j softmax(s)_j V[b, j, h]
+ * Replaces the append and the single-query SDPA of T2SEngine::block_decode_impl
+ * (t2s_engine.cpp:1051-1087: kern::f32_to_f16 into k16 / v16 or the fp32 memcpy, then per head
+ * ar_neon::dot_f16kv / dot_f32, kern::softmax (kern.cpp:62-74) and ar_neon::accum_f16kv /
+ * accum_f32, t2s_engine.cpp:40-145), for every sequence in one call.
+ * Layout: qkv [batch, ldq >= 3D] fp32 as the QKV GEMV writes it (q | k | v, bias included);
+ * k_cache / v_cache [batch, max_len, D] of kv_dtype, token-major (row j holds every head, as the
+ * reference's k16[j * D + h * HD + e]); out [batch, ldo >= D] of out_dtype. D = heads * head_dim
+ * <= 512, head_dim a multiple of 8 with head_dim / 8 a power of two; rows 16-byte aligned.
+ * len_bound: a host-side upper bound of pos[b] + 1 (e.g. the longest sequence so far) that sets how
+ * many key chunks a sequence is split into (0 = max_len); results do not depend on it. With more
+ * than one chunk the partial states go through `workspace` (gsvk_decode_attention_workspace_bytes
+ * bytes, 16-byte aligned; no initialisation needed); with a NULL or smaller workspace every sequence
+ * runs as one chunk. A position outside [0, max_len) (undefined in the reference) writes a NaN row,
+ * leaves the caches untouched and stores 1 into *err when err != NULL.
+ * The softmax is formed online (running maximum, rescaled sums) in another order than the
+ * reference's; results agree within fp32 rounding: |out - ref| <= 1e-5 * max(1, max |v|).
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* qkv, size_t ldq, void* k_cache,
+                          void* v_cache, size_t max_len, const int64_t* pos, void* out, size_t ldo,
+                          size_t batch, size_t heads, size_t head_dim, size_t len_bound,
+                          void* workspace, size_t workspace_bytes, int32_t* err, void* stream);
+/* Workspace bytes gsvk_decode_attention uses for these sizes (0: none). Host only. */
+size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t head_dim,
+                                             size_t len_bound);
+
+/* ------------------------------------------------------------------------------------------------
  * GroupNorm with one group per channel, optionally followed by GELU(erf).
  *   mean_c, var_c over the T frames of channel c (biased); y = (x - mean)*rstd*gamma[c] + beta[c];
  *   y = gelu_erf(y) when apply_gelu != 0.

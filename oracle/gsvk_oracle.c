@@ -20,6 +20,8 @@
  *   gelu_erf             float64 math.erf closed form, odd-part identity   (no reference vector)
  *   groupnorm_gelu       float64 closed form, T = 1 -> beta                (no reference vector)
  *   leaky / add / mean   exact-rational closed forms, slope identities     (no reference vector)
+ *   decode_attention     reference softmax golden sm_x / sm_y (test_kern.cpp:219-229) for the
+ *                        softmax step, float64 closed form, one-key and equal-key identities
  *   gemv_f16w            reference golden gemv_a / gemv_b (test_kern.cpp:96-120) at its own
  *                        tolerance, exact small-integer products (sum order free), fp16-rounded x
  *                        identity between the two modes, epilogue order
@@ -340,6 +342,111 @@ int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const 
   free(xr);
   free(v);
   free(r);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * Decode attention (next-tier row 2): block_decode_impl's KV append and single-query SDPA per head
+ * (t2s_engine.cpp:1051-1087), per sequence b at position pos[b]:
+ *   K[pos] = k, V[pos] = v (rounded to the cache type: kern::f32_to_f16 for fp16 caches, 1051-1058)
+ *   for each head h, keys k < len = pos + 1:
+ *     s_k = dot(q_h, K[k, h]) * scale        ar_neon::dot_f16kv / dot_f32 (t2s_engine.cpp:40-103)
+ *     p = kern::softmax(s)                    (kern.cpp:62-74)
+ *     o_h = sum_k p_k V[k, h]                 ar_neon::accum_f16kv / accum_f32 (105-145)
+ * dot: four 4-lane accumulators over 16-element groups (fma), (a0 + a1) + (a2 + a3) lane-wise,
+ * then (l0 + l2) + (l1 + l3); tail elements with the contracted dot += q*k. softmax: sequential max,
+ * e = expf(x - max), sequential sum, then x * (1 / sum). accum: ov[e] = ov[e] + p * v[e] with the
+ * product rounded first (vmulq then vaddq) in 16-element groups, tail contracted (fma).
+ * --------------------------------------------------------------------------------------------- */
+static float attn_dot(const float* q, const float* k, size_t HD) {
+  float a[4][4];
+  memset(a, 0, sizeof a);
+  size_t e = 0;
+  for (; e + 16 <= HD; e += 16)
+    for (int j = 0; j < 4; ++j)
+      for (int l = 0; l < 4; ++l) a[j][l] = fmaf(q[e + 4 * j + l], k[e + 4 * j + l], a[j][l]);
+  float t[4];
+  for (int l = 0; l < 4; ++l) t[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
+  float dot = (t[0] + t[2]) + (t[1] + t[3]);
+  for (; e < HD; ++e) dot = fmaf(q[e], k[e], dot);
+  return dot;
+}
+
+static void attn_accum(float* o, const float* v, float p, size_t HD) {
+  size_t e = 0;
+  for (; e + 16 <= HD; e += 16)
+    for (int i = 0; i < 16; ++i) o[e + i] = o[e + i] + p * v[e + i];
+  for (; e < HD; ++e) o[e] = fmaf(p, v[e], o[e]);
+}
+
+void oracle_softmax(const float* x, float* y, size_t n) {
+  float m = x[0];
+  for (size_t i = 1; i < n; ++i) m = m < x[i] ? x[i] : m;
+  float sum = 0.f;
+  for (size_t i = 0; i < n; ++i) {
+    const float e = expf(x[i] - m);
+    y[i] = e;
+    sum += e;
+  }
+  const float inv = 1.0f / sum;
+  for (size_t i = 0; i < n; ++i) y[i] *= inv;
+}
+
+int oracle_decode_attention(int kv_dtype, const float* qkv, size_t ldq, void* kcache, void* vcache,
+                            size_t max_len, const int64_t* pos, float* out, size_t ldo, size_t B,
+                            size_t H, size_t HD) {
+  const size_t D = H * HD;
+  const float scale = 1.0f / sqrtf((float)HD);
+  float* sc = (float*)malloc((max_len ? max_len : 1) * 4);
+  float* kr = (float*)malloc(D * 4);
+  float* vr = (float*)malloc(D * 4);
+  if (!sc || !kr || !vr) {
+    free(sc);
+    free(kr);
+    free(vr);
+    return -1;
+  }
+  const size_t esz = esize(kv_dtype);
+  for (size_t b = 0; b < B; ++b) {
+    float* ob = out + b * ldo;
+    const int64_t p = pos[b];
+    if (p < 0 || (size_t)p >= max_len) {
+      for (size_t i = 0; i < D; ++i) ob[i] = bits_f(0x7fc00000u);
+      continue;
+    }
+    const float* qb = qkv + b * ldq;
+    char* kb = (char*)kcache + b * max_len * D * esz;
+    char* vb = (char*)vcache + b * max_len * D * esz;
+    oracle_from_f32(kv_dtype, qb + D, kb + (size_t)p * D * esz, D);
+    oracle_from_f32(kv_dtype, qb + 2 * D, vb + (size_t)p * D * esz, D);
+    const size_t len = (size_t)p + 1;
+    for (size_t h = 0; h < H; ++h) {
+      const float* qh = qb + h * HD;
+      for (size_t k = 0; k < len; ++k) {
+        oracle_to_f32(kv_dtype, kb + (k * D + h * HD) * esz, kr, HD);
+        sc[k] = attn_dot(qh, kr, HD) * scale;
+      }
+      float m = sc[0];
+      for (size_t k = 1; k < len; ++k) m = m < sc[k] ? sc[k] : m;
+      float sum = 0.f;
+      for (size_t k = 0; k < len; ++k) {
+        const float e = expf(sc[k] - m);
+        sc[k] = e;
+        sum += e;
+      }
+      const float inv = 1.0f / sum;
+      for (size_t k = 0; k < len; ++k) sc[k] *= inv;
+      float* oh = ob + h * HD;
+      for (size_t e = 0; e < HD; ++e) oh[e] = 0.f;
+      for (size_t k = 0; k < len; ++k) {
+        oracle_to_f32(kv_dtype, vb + (k * D + h * HD) * esz, vr, HD);
+        attn_accum(oh, vr, sc[k], HD);
+      }
+    }
+  }
+  free(sc);
+  free(kr);
+  free(vr);
   return 0;
 }
 

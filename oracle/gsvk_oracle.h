@@ -71,6 +71,16 @@ int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const 
                      const float* bias, int act, float slope, const void* residual, int y_dtype,
                      void* y, size_t ldy, size_t rows, size_t out, size_t in);
 
+/* Decode attention: KV append at pos[b] and single-query SDPA over keys 0..pos[b] per head
+ * (t2s_engine.cpp:1051-1087). kv_dtype 0 = fp32 cache, 1 = fp16 cache. Caches [B][max_len][H*HD];
+ * qkv rows [q | k | v] fp32 with stride ldq; out [B][H*HD] fp32 with stride ldo (NaN rows for a
+ * position outside [0, max_len)). scale = 1 / sqrtf(HD). */
+int oracle_decode_attention(int kv_dtype, const float* qkv, size_t ldq, void* kcache, void* vcache,
+                            size_t max_len, const int64_t* pos, float* out, size_t ldo, size_t B,
+                            size_t H, size_t HD);
+/* kern::softmax on one row (kern.cpp:62-74) */
+void oracle_softmax(const float* x, float* y, size_t n);
+
 /* a10: T2SEngine::pe_row (t2s_engine.cpp:711-720) and the gather + alpha*PE loops
  * (t2s_engine.cpp:1774-1786, 1866-1869). index_type 0 = int64, 1 = int32. Returns the number of
  * rows whose id / position was out of range (those rows are NaN, as the GPU writes them). */

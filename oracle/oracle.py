@@ -37,6 +37,8 @@ _SIG = {
     "oracle_scaled_add": (_i, [_i, _vp, _vp, _vp, _sz, _f]),
     "oracle_gemv_f16w": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _i, _vp, _sz, _sz, _sz,
                               _sz]),
+    "oracle_decode_attention": (_i, [_i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz]),
+    "oracle_softmax": (None, [_vp, _vp, _sz]),
     "oracle_pe_row": (None, [_vp, _sz, _sz]),
     "oracle_embed_pe": (ctypes.c_long, [_i, _i, _i, _vp, _sz, _vp, _vp, ctypes.c_int64, _vp, _sz,
                                         _f, _vp, _vp, _vp, _sz, _sz]),
@@ -185,6 +187,29 @@ def gemv_f16w(x_dt, x, w, y_dt, bias=None, act=0, slope=0.0, residual=None, roun
                                 _p(residual), y_dt, _p(y), n_out, rows, n_out, n_in)
     assert rc == 0
     return y
+
+
+def softmax(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().oracle_softmax(_p(x), _p(y), x.size)
+    return y
+
+
+def decode_attention(kv_dt, qkv, kcache, vcache, pos, H, HD):
+    """KV append + single-query attention. qkv [B, 3D] float32; kcache / vcache [B, max_len, D]
+    storage arrays of kv_dt (F32 or F16), updated in place at pos; returns out [B, D] float32."""
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    B = qkv.shape[0]
+    D = H * HD
+    assert kcache.flags.c_contiguous and vcache.flags.c_contiguous
+    max_len = kcache.shape[1]
+    pos = np.ascontiguousarray(pos, dtype=np.int64)
+    out = np.empty((B, D), dtype=np.float32)
+    rc = lib().oracle_decode_attention(kv_dt, _p(qkv), qkv.shape[1], _p(kcache), _p(vcache),
+                                       max_len, _p(pos), _p(out), D, B, H, HD)
+    assert rc == 0
+    return out
 
 
 def pe_row(pos, D):

@@ -118,6 +118,28 @@ def test_gemv_validation(gsvk_lib):
     assert call(res=C + 4) == gsvk.E_ALIAS      # residual partly over y (res == y is allowed)
 
 
+def test_attention_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_decode_attention
+
+    def call(kv=1, out=0, q=A, ldq=1536, k=B, v=C, max_len=8, pos=0x700000, y=0x800000, ldo=512,
+             batch=2, H=16, HD=32, ws=None, wsb=0):
+        return f(kv, out, q, ldq, k, v, max_len, pos, y, ldo, batch, H, HD, 0, ws, wsb, None, None)
+
+    assert call(kv=9) == gsvk.E_DTYPE
+    assert call(out=9) == gsvk.E_DTYPE
+    assert call(pos=None) == gsvk.E_NULL
+    assert call(max_len=0) == gsvk.E_SIZE
+    assert call(ldq=1535) == gsvk.E_SIZE
+    assert call(ldo=511) == gsvk.E_SIZE
+    assert call(H=16, HD=40) == gsvk.E_ARG       # head_dim / 8 not a power of two
+    assert call(H=32, HD=32) == gsvk.E_ARG       # D > 512
+    assert call(q=A + 4) == gsvk.E_ARG           # rows not 16-byte aligned
+    assert call(y=B + 64) == gsvk.E_ALIAS        # output over the key cache
+    assert call(v=B + 1024) == gsvk.E_ALIAS      # caches overlap
+    assert gsvk_lib.gsvk_decode_attention_workspace_bytes(64, 16, 32, 100) == 0
+    assert gsvk_lib.gsvk_decode_attention_workspace_bytes(64, 16, 32, 1024) > 0
+
+
 def test_embed_validation(gsvk_lib):
     f = gsvk_lib.gsvk_embed_pe
     args = dict(out=0, tab=1, it=0, table=A, vocab=10, ids=B, pos=None, pos0=0, pe=C, max_pos=4,
