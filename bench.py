@@ -356,6 +356,22 @@ def kernel_suite(torch, gsvk, dev, only=None):
             ("w2_bias_residual", 512, 2048, gsvk.ACT_NONE, True, True, f16, 128, 24),
             ("logits_f32out", 1025, 512, gsvk.ACT_NONE, False, False, f32, 128, 1)):
         run(f"gemv_{name}_64x{N}x{K}", 2, *gemv_case(N, K, act, ub, ur, ydt, rep), count)
+
+    # T2S decode attention with the KV append (t2s_engine.cpp:1051-1087): B = 64 sequences, 16 heads
+    # of 32, fp16 caches, every sequence at position L - 1. One call already streams 2 B L D cache
+    # elements, so the replicated case is the same call at twice the length.
+    def attn_case(Ln, rep):
+        def make(k):
+            n = Ln * k
+            kc, vc = rn(B, n, D), rn(B, n, D)
+            q = rn(B, 3 * D, dtype=f32)
+            pos = torch.full((B,), n - 1, dtype=torch.int64, device=dev)
+            o = torch.empty(B, D, dtype=f16, device=dev)
+            return lambda: gsvk.decode_attention(q, kc, vc, pos, o, 16, len_bound=n)
+        nbytes = lambda k: 2 * B * Ln * k * D * 2 + B * 3 * D * 4 + B * D * 2
+        return (lambda: make(1), lambda: (rep, make(rep)), nbytes)
+
+    run("decode_attention_f16kv_64x1024x512", 2, *attn_case(1024, 2), 24)
     return out
 
 
