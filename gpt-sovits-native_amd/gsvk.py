@@ -43,6 +43,8 @@ SIGNATURES = {
     "gsvk_t2s_step_run": (_i, [_vp, _vp]),
     "gsvk_t2s_step_launches": (_i, [_vp]),
     "gsvk_t2s_step_destroy": (None, [_vp]),
+    "gsvk_t2s_decode_eager": (_i, [_vp, _vp]),
+    "gsvk_t2s_decode_create": (_i, [_vp, ctypes.POINTER(_vp)]),
 }
 
 
@@ -296,6 +298,98 @@ class T2SStep:
                                                                        _stream(stream)))
         return _check("gsvk_t2s_step_eager", lib().gsvk_t2s_step_eager(ctypes.byref(self.desc),
                                                                        _stream(stream)))
+
+    def close(self):
+        if self.handle:
+            lib().gsvk_t2s_step_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- whole T2S decode step (gsvk_t2s_decode_*) -------------------------------------------------
+
+class T2SLayer(ctypes.Structure):
+    _fields_ = [(n, _vp) for n in ("wqkv", "bqkv", "wout", "bout", "n1g", "n1b", "w1", "b1", "w2",
+                                   "b2", "n2g", "n2b", "k_cache", "v_cache")]
+
+
+class T2SDecodeDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int), ("kv_dtype", ctypes.c_int), ("batch", _sz), ("d_model", _sz),
+        ("heads", _sz), ("ffn", _sz), ("layers", _sz), ("max_len", _sz), ("len_bound", _sz),
+        ("eps", _d), ("audio_table", _vp), ("table_dtype", ctypes.c_int), ("vocab", _sz),
+        ("ids", _vp), ("index_type", ctypes.c_int), ("pos", _vp), ("kv_pos", _vp), ("pe", _vp),
+        ("max_pos", _sz), ("alpha", _f), ("err", _vp), ("layer", ctypes.POINTER(T2SLayer)),
+        ("w_logits", _vp), ("logits", _vp), ("x", _vp), ("h", _vp), ("z", _vp), ("attn", _vp),
+        ("ff", _vp), ("qkv", _vp), ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class T2SDecode:
+    """One whole decode step (embedding, every layer's GEMVs / attention / LayerNorms, logits)
+    over torch buffers; recorded into a graph unless graph=False. `m` holds the model tensors:
+    table, pe, alpha, heads, layers (list of dicts with the gsvk_t2s_layer names), w_logits (or
+    None); `io` holds ids, pos, kv_pos, err and the activations x, h, z, attn, ff, qkv, logits."""
+
+    def __init__(self, m, io, eps=1e-5, len_bound=0, graph=True):
+        import torch
+        self.m, self.io = m, io
+        layers = m["layers"]
+        L = len(layers)
+        self._layers = (T2SLayer * L)()
+        for i, ly in enumerate(layers):
+            for name, _ in T2SLayer._fields_:
+                setattr(self._layers[i], name, _ptr(ly.get(name)))
+        B, D = io["x"].shape
+        k0 = layers[0]["k_cache"]
+        d = T2SDecodeDesc()
+        d.dtype = dtype_code(io["x"])
+        d.kv_dtype = dtype_code(k0)
+        d.batch, d.d_model, d.heads, d.ffn, d.layers = B, D, m["heads"], io["ff"].shape[1], L
+        d.max_len = k0.shape[1]
+        d.len_bound = len_bound
+        d.eps = eps
+        d.audio_table = _ptr(m["table"])
+        d.table_dtype = dtype_code(m["table"])
+        d.vocab = m["table"].shape[0]
+        d.ids = _ptr(io["ids"])
+        d.index_type = I32 if io["ids"].dtype == torch.int32 else I64
+        d.pos, d.kv_pos = _ptr(io["pos"]), _ptr(io["kv_pos"])
+        d.pe, d.max_pos, d.alpha = _ptr(m["pe"]), m["pe"].shape[0], m["alpha"]
+        d.err = _ptr(io.get("err"))
+        d.layer = ctypes.cast(self._layers, ctypes.POINTER(T2SLayer))
+        d.w_logits = _ptr(m.get("w_logits"))
+        d.logits = _ptr(io.get("logits"))
+        for name in ("x", "h", "z", "attn", "ff", "qkv"):
+            setattr(d, name, _ptr(io[name]))
+        need = lib().gsvk_decode_attention_workspace_bytes(B, m["heads"], D // m["heads"],
+                                                           len_bound or d.max_len)
+        if need:
+            ws = workspace(io["x"].device, need)
+            d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+        self.desc = d
+        self.handle = None
+        if graph:
+            h = _vp()
+            _check("gsvk_t2s_decode_create",
+                   lib().gsvk_t2s_decode_create(ctypes.byref(d), ctypes.byref(h)))
+            self.handle = h
+
+    @property
+    def launches(self):
+        return lib().gsvk_t2s_step_launches(self.handle) if self.handle else 0
+
+    def run(self, stream=None):
+        if self.handle:
+            return _check("gsvk_t2s_step_run", lib().gsvk_t2s_step_run(self.handle,
+                                                                       _stream(stream)))
+        return _check("gsvk_t2s_decode_eager",
+                      lib().gsvk_t2s_decode_eager(ctypes.byref(self.desc), _stream(stream)))
 
     def close(self):
         if self.handle:

@@ -1,5 +1,6 @@
-// t2s_decode_step.cpp — the epilogue chain of one T2S decode step over B sequences, issued through
-// the C ABI and recorded into a HIP graph (one graph launch per step instead of 73 API launches).
+// t2s_decode_step.cpp — one T2S decode step over B sequences, issued through the C ABI and recorded
+// into a HIP graph (one graph launch per step): the epilogue chain alone (gsvk_t2s_step_*) and the
+// whole step with its GEMVs and attention (gsvk_t2s_decode_*).
 #include <hip/hip_runtime.h>
 
 #include <new>
@@ -39,6 +40,68 @@ int issue(const gsvk_t2s_step_desc* d, void* st) {
   return GSVK_OK;
 }
 
+bool decode_ok(const gsvk_t2s_decode_desc* d) {
+  if (!d || !d->layer || !d->x || !d->h || !d->z || !d->attn || !d->ff || !d->qkv || !d->kv_pos)
+    return false;
+  if (d->batch == 0 || d->d_model == 0 || d->heads == 0 || d->ffn == 0 || d->layers == 0)
+    return false;
+  if (d->w_logits && !d->logits) return false;
+  for (size_t l = 0; l < d->layers; ++l) {
+    const gsvk_t2s_layer& L = d->layer[l];
+    if (!L.wqkv || !L.wout || !L.w1 || !L.w2 || !L.k_cache || !L.v_cache) return false;
+  }
+  return true;
+}
+
+// One decode step, launch by launch, in block_decode_impl's order.
+int issue_decode(const gsvk_t2s_decode_desc* d, void* st) {
+  const size_t B = d->batch, D = d->d_model, FF = d->ffn, H = d->heads;
+  const int dt = d->dtype;
+  int rc = gsvk_embed_pe(dt, d->table_dtype, d->index_type, d->audio_table, d->vocab, d->ids,
+                         d->pos, 0, d->pe, d->max_pos, d->alpha, nullptr, nullptr, d->x, B, D,
+                         d->err, st);
+  if (rc) return rc;
+  for (size_t l = 0; l < d->layers; ++l) {
+    const gsvk_t2s_layer& L = d->layer[l];
+    if ((rc = gsvk_gemv_f16w(dt, 1, d->x, D, L.wqkv, L.bqkv, GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32,
+                             d->qkv, 3 * D, B, 3 * D, D, st)))
+      return rc;
+    if ((rc = gsvk_decode_attention(d->kv_dtype, dt, d->qkv, 3 * D, L.k_cache, L.v_cache,
+                                    d->max_len, d->kv_pos, d->attn, D, B, H, D / H, d->len_bound,
+                                    d->workspace, d->workspace_bytes, d->err, st)))
+      return rc;
+    if ((rc = gsvk_gemv_f16w(dt, 1, d->attn, D, L.wout, L.bout, GSVK_ACT_NONE, 0.f, d->x, dt, d->z,
+                             D, B, D, D, st)))
+      return rc;
+    if ((rc = gsvk_add_layernorm(dt, d->z, nullptr, nullptr, L.n1g, L.n1b, d->h, B, D, D, d->eps,
+                                 st)))
+      return rc;
+    if ((rc = gsvk_gemv_f16w(dt, 1, d->h, D, L.w1, L.b1, GSVK_ACT_RELU, 0.f, nullptr, dt, d->ff, FF,
+                             B, FF, D, st)))
+      return rc;
+    if ((rc = gsvk_gemv_f16w(dt, 1, d->ff, FF, L.w2, L.b2, GSVK_ACT_NONE, 0.f, d->h, dt, d->z, D, B,
+                             D, FF, st)))
+      return rc;
+    if ((rc = gsvk_add_layernorm(dt, d->z, nullptr, nullptr, L.n2g, L.n2b, d->x, B, D, D, d->eps,
+                                 st)))
+      return rc;
+  }
+  if (d->w_logits)
+    return gsvk_gemv_f16w(dt, 1, d->x, D, d->w_logits, nullptr, GSVK_ACT_NONE, 0.f, nullptr,
+                          GSVK_F32, d->logits, d->vocab, B, d->vocab, D, st);
+  return GSVK_OK;
+}
+
+int count_decode_launches(const gsvk_t2s_decode_desc* d) {
+  const size_t lb = d->len_bound ? d->len_bound : d->max_len;
+  const bool merge = gsvk_decode_attention_workspace_bytes(d->batch, d->heads,
+                                                           d->d_model / d->heads, lb) > 0 &&
+                     d->workspace &&
+                     d->workspace_bytes >= gsvk_decode_attention_workspace_bytes(
+                                               d->batch, d->heads, d->d_model / d->heads, lb);
+  return static_cast<int>(1 + d->layers * (merge ? 8 : 7) + (d->w_logits ? 1 : 0));
+}
+
 }  // namespace
 
 struct gsvk_t2s_step {
@@ -52,10 +115,9 @@ extern "C" int gsvk_t2s_step_eager(const gsvk_t2s_step_desc* desc, void* stream)
   return issue(desc, stream);
 }
 
-extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_step** out) {
-  if (!out) return GSVK_E_NULL;
-  *out = nullptr;
-  if (!desc_ok(desc)) return GSVK_E_NULL;
+// Record the launches `issue` makes into a graph on a private stream and instantiate it.
+template <class Issue>
+int record(Issue issue, int launches, gsvk_t2s_step** out) {
   hipStream_t cap = nullptr;
   if (hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return GSVK_E_HIP;
   auto* s = new (std::nothrow) gsvk_t2s_step;
@@ -67,7 +129,7 @@ extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_ste
   if (hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal) != hipSuccess) {
     rc = GSVK_E_HIP;
   } else {
-    rc = issue(desc, cap);
+    rc = issue(cap);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(cap, &g);
     if (rc == GSVK_OK && e != hipSuccess) rc = GSVK_E_HIP;
@@ -80,9 +142,30 @@ extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_ste
     gsvk_t2s_step_destroy(s);
     return rc;
   }
-  s->launches = static_cast<int>(1 + 3 * desc->layers);
+  s->launches = launches;
   *out = s;
   return GSVK_OK;
+}
+
+extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_step** out) {
+  if (!out) return GSVK_E_NULL;
+  *out = nullptr;
+  if (!desc_ok(desc)) return GSVK_E_NULL;
+  return record([desc](hipStream_t st) { return issue(desc, st); },
+                static_cast<int>(1 + 3 * desc->layers), out);
+}
+
+extern "C" int gsvk_t2s_decode_eager(const gsvk_t2s_decode_desc* desc, void* stream) {
+  if (!decode_ok(desc)) return GSVK_E_NULL;
+  return issue_decode(desc, stream);
+}
+
+extern "C" int gsvk_t2s_decode_create(const gsvk_t2s_decode_desc* desc, gsvk_t2s_step** out) {
+  if (!out) return GSVK_E_NULL;
+  *out = nullptr;
+  if (!decode_ok(desc)) return GSVK_E_NULL;
+  return record(
+      [desc](hipStream_t st) { return issue_decode(desc, st); }, count_decode_launches(desc), out);
 }
 
 extern "C" int gsvk_t2s_step_run(gsvk_t2s_step* step, void* stream) {

@@ -71,6 +71,77 @@ int gsvk_t2s_step_run(gsvk_t2s_step* step, void* stream);
 int gsvk_t2s_step_launches(const gsvk_t2s_step* step);
 void gsvk_t2s_step_destroy(gsvk_t2s_step* step);
 
+/* ------------------------------------------------------------------------------------------------
+ * The whole T2S decode step for B sequences: the same epilogue chain with the GEMVs and the
+ * attention that feed it, as T2SEngine::generate runs one token (t2s_engine.cpp:1864-1885:
+ * x = audio_emb[id] + alpha * PE, block_decode_impl for every layer, predict_layer_fp):
+ *   x = embed_pe(ids, pos)                                          (1866-1869)
+ *   for each layer l (block_decode_impl, 1035-1120):
+ *     qkv  = Wqkv x + bqkv                           fp32           (1044-1049)
+ *     attn = attention(qkv, K_l, V_l, kv_pos)        + KV append    (1051-1087)
+ *     z    = (Wout attn + bout) + x;   h = LN1(z)                   (1090-1098)
+ *     ff   = relu(W1 h + b1)                                        (1105-1112)
+ *     z    = (W2 ff + b2) + h;         x = LN2(z)                   (1113-1119)
+ *   logits = Wp x                                    fp32, no bias  (predict_layer_fp, 704-707)
+ * Activations x, h, z, attn, ff are stored in `dtype`; GEMVs round x to fp16 (gemv_fmlal) and
+ * accumulate in fp32; the epilogues add in fp32 before the single rounding to `dtype`.
+ * pos[b] is the PE position of the new token (P + idx), kv_pos[b] its cache slot (cur_len); the
+ * step attends over kv_pos[b] + 1 keys. Per layer: 3 GEMV launches + 2 LayerNorms + the attention
+ * (+ 1 chunk merge when len_bound > 256), plus the embedding and the logits GEMV.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct gsvk_t2s_layer {
+  const uint16_t* wqkv; /* [3D, D] fp16 */
+  const float* bqkv;    /* [3D]          */
+  const uint16_t* wout; /* [D, D]        */
+  const float* bout;    /* [D]           */
+  const float* n1g;     /* [D]           */
+  const float* n1b;
+  const uint16_t* w1;   /* [FF, D]       */
+  const float* b1;      /* [FF]          */
+  const uint16_t* w2;   /* [D, FF]       */
+  const float* b2;      /* [D]           */
+  const float* n2g;
+  const float* n2b;
+  void* k_cache;        /* [B, max_len, D] kv_dtype */
+  void* v_cache;
+} gsvk_t2s_layer;
+
+typedef struct gsvk_t2s_decode_desc {
+  int dtype;            /* activation storage                                      */
+  int kv_dtype;         /* cache storage                                           */
+  size_t batch, d_model, heads, ffn, layers;
+  size_t max_len;       /* cache rows per sequence                                 */
+  size_t len_bound;     /* upper bound of kv_pos[b] + 1 (0 = max_len)              */
+  double eps;
+  const void* audio_table; /* [vocab, D] */
+  int table_dtype;
+  size_t vocab;
+  const void* ids;         /* [B] */
+  int index_type;
+  const int64_t* pos;      /* [B] PE positions */
+  const int64_t* kv_pos;   /* [B] cache slots  */
+  const float* pe;         /* [max_pos, D] */
+  size_t max_pos;
+  float alpha;
+  int32_t* err;            /* optional: bad id / position / cache slot */
+  const gsvk_t2s_layer* layer; /* [layers], host memory, read by eager / create only */
+  const uint16_t* w_logits;    /* [vocab, D] fp16 or NULL */
+  float* logits;               /* [B, vocab] */
+  /* scratch activations, all [B, ...] in dtype except qkv (fp32) */
+  void* x;   /* [B, D]  */
+  void* h;   /* [B, D]  */
+  void* z;   /* [B, D]  */
+  void* attn;/* [B, D]  */
+  void* ff;  /* [B, FF] */
+  float* qkv;/* [B, 3D] */
+  void* workspace;         /* gsvk_decode_attention_workspace_bytes(batch, heads, D/heads, len) */
+  size_t workspace_bytes;
+} gsvk_t2s_decode_desc;
+
+int gsvk_t2s_decode_eager(const gsvk_t2s_decode_desc* desc, void* stream);
+/* Records one step into a HIP graph; run / launches / destroy with the gsvk_t2s_step calls. */
+int gsvk_t2s_decode_create(const gsvk_t2s_decode_desc* desc, gsvk_t2s_step** out);
+
 #ifdef __cplusplus
 }
 #endif
