@@ -20,7 +20,10 @@ Also reported (same JSON line):
                 reference for the replicated figures);
   sovits_decoder  the SoVITS ResBlock epilogues at every decoder stage shape (reference 768-channel
                 geometry and the 512-start geometry), with the per-stage launch counts summed into
-                epilogue microseconds per 10 s of audio.
+                epilogue microseconds per 10 s of audio;
+  t2s_whole_decode_step  the whole decode step (GEMVs, attention with KV append, epilogues, logits)
+                for 64 sequences at KV lengths 1024 and 2048, as one graph: microseconds per step,
+                tokens/s and algorithmic GB/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
        python bench.py --only KERNEL   (one kernel of the suite, for rocprofv3 runs)
@@ -423,6 +426,68 @@ def sovits_decoder(torch, gsvk, dev):
     return out
 
 
+# ---- whole T2S decode step ---------------------------------------------------------------------------
+
+def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
+    """One whole decode step (gsvk_t2s_decode: embedding, 24 x [QKV GEMV, attention with KV append,
+    out-proj GEMV + bias + residual, LN1, W1 GEMV + bias + ReLU, W2 GEMV + bias + residual, LN2],
+    logits GEMV) for B = 64 sequences whose caches hold kv_len tokens, replayed as one graph.
+    Random-init weights of the T2S shapes (fp16), fp16 caches and activations."""
+    g = torch.Generator(device=dev).manual_seed(SEED + 7)
+    f16, f32 = torch.float16, torch.float32
+    H, V, max_len = 16, VOCAB, kv_len + 64
+
+    def rn(*shape, std=1.0, mean=0.0, dtype=f16):
+        return torch.empty(*shape, dtype=f32, device=dev).normal_(mean, std, generator=g).to(dtype)
+
+    layers = []
+    for _ in range(LAYERS):
+        layers.append(dict(
+            wqkv=rn(3 * D, D, std=0.05), bqkv=rn(3 * D, std=0.02, dtype=f32),
+            wout=rn(D, D, std=0.05), bout=rn(D, std=0.02, dtype=f32),
+            n1g=rn(D, std=0.1, mean=1.0, dtype=f32), n1b=rn(D, std=0.1, dtype=f32),
+            w1=rn(FF, D, std=0.05), b1=rn(FF, std=0.02, dtype=f32),
+            w2=rn(D, FF, std=0.05), b2=rn(D, std=0.02, dtype=f32),
+            n2g=rn(D, std=0.1, mean=1.0, dtype=f32), n2b=rn(D, std=0.1, dtype=f32),
+            k_cache=rn(B, max_len, D), v_cache=rn(B, max_len, D)))
+    m = dict(table=rn(V, D, std=0.02), pe=torch.from_numpy(gsvk.pe_table(MAX_POS, D)).to(dev),
+             alpha=0.93, heads=H, layers=layers, w_logits=rn(V, D, std=0.05))
+    io = dict(ids=torch.randint(0, V, (B,), device=dev, generator=g),
+              pos=torch.full((B,), 512, dtype=torch.int64, device=dev),
+              kv_pos=torch.full((B,), kv_len - 1, dtype=torch.int64, device=dev),
+              err=torch.zeros(1, dtype=torch.int32, device=dev),
+              x=torch.empty(B, D, dtype=f16, device=dev), h=torch.empty(B, D, dtype=f16, device=dev),
+              z=torch.empty(B, D, dtype=f16, device=dev),
+              attn=torch.empty(B, D, dtype=f16, device=dev),
+              ff=torch.empty(B, FF, dtype=f16, device=dev),
+              qkv=torch.empty(B, 3 * D, dtype=f32, device=dev),
+              logits=torch.empty(B, V, dtype=f32, device=dev))
+    step = gsvk.T2SDecode(m, io, len_bound=max_len, graph=True)
+    for _ in range(warmup):
+        step.run()
+    torch.cuda.synchronize()
+    ms = time_loop(torch, step.run, steps)
+    assert int(io["err"].item()) == 0
+    # algorithmic bytes: every weight and parameter once, the kv_len cached rows of K and V per
+    # layer once, the appended rows, and each activation read / written once
+    w_bytes = LAYERS * ((3 * D * D + D * D + 2 * FF * D) * 2 + (3 * D + 6 * D + FF) * 4) + V * D * 2
+    kv_bytes = LAYERS * (2 * B * kv_len * D * 2)
+    act_bytes = LAYERS * B * (D * 2 + 3 * D * 4 * 2 + D * 2 * 2 + D * 2 * 3 + D * 2 * 2 +
+                              FF * 2 * 2 + D * 2 * 3 + D * 2 * 2) + B * V * 4 + B * D * 2
+    nbytes = w_bytes + kv_bytes + act_bytes
+    out = {"batch": B, "layers": LAYERS, "d_model": D, "ffn": FF, "heads": H, "vocab": V,
+           "kv_len": kv_len, "storage": "f16", "kv_storage": "f16", "launches": step.launches,
+           "us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(B / ms * 1e3, 0),
+           "bytes_per_step": nbytes, "GBps": round(nbytes / ms / 1e6, 1),
+           "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_GBS, 4)}
+    log(f"  whole decode step (B={B}, kv_len={kv_len}, graph of {step.launches} launches): "
+        f"{out['us_per_step']} us, {out['tokens_per_s']:.0f} tokens/s, {out['GBps']} GB/s")
+    step.close()
+    del m, io, layers
+    torch.cuda.empty_cache()
+    return out
+
+
 # ---- CPU baseline ----------------------------------------------------------------------------------
 
 def cpu_model():
@@ -659,11 +724,12 @@ def main():
                "single_thread_cv": round(res[1]["cv"], 4),
                "cpu_model": cpu_model(), "hardware_threads": os.cpu_count()}
 
-    kernels = copy_gbs = decoder = None
+    kernels = copy_gbs = decoder = full = None
     if not a.no_kernels:
         copy_gbs = copy_bandwidth(torch, dev)
         kernels = kernel_suite(torch, gsvk, dev)
         decoder = sovits_decoder(torch, gsvk, dev)
+        full = [full_decode_step(torch, gsvk, dev, kv_len=n) for n in (1024, 2048)]
 
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
@@ -680,6 +746,7 @@ def main():
         "copy_GBps": copy_gbs,
         "kernels": kernels,
         "sovits_decoder": decoder,
+        "t2s_whole_decode_step": full,
     }
     print(json.dumps(line), flush=True)
     step.close()
