@@ -27,6 +27,8 @@ extern "C" const char* gsvk_status_string(int status) {
     case GSVK_E_ALIAS: return "output overlaps an input";
     case GSVK_E_ARG: return "invalid argument";
     case GSVK_E_HIP: return "HIP launch error";
+    case GSVK_E_FORMAT: return "malformed .gsv container";
+    case GSVK_E_IO: return "cannot open or map the file";
     default: return "unknown status";
   }
 }

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libgsvk.so")
 F32, F16, BF16 = 0, 1, 2
 I64, I32 = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_LEAKY_RELU = 0, 1, 2, 3
-OK, E_NULL, E_SIZE, E_DTYPE, E_ALIAS, E_ARG, E_HIP = 0, -1, -2, -3, -4, -5, -6
+OK, E_NULL, E_SIZE, E_DTYPE, E_ALIAS, E_ARG, E_HIP, E_FORMAT, E_IO = 0, -1, -2, -3, -4, -5, -6, -7, -8
 
 # Every exported symbol of the C ABI with (restype, argtypes).
 _vp, _sz, _i, _f, _d = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_double
@@ -44,6 +44,18 @@ SIGNATURES = {
     "gsvk_t2s_step_launches": (_i, [_vp]),
     "gsvk_t2s_step_destroy": (None, [_vp]),
     "gsvk_t2s_decode_eager": (_i, [_vp, _vp]),
+    "gsvk_gsv_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "gsvk_gsv_open_memory": (_i, [_vp, _sz, ctypes.POINTER(_vp)]),
+    "gsvk_gsv_close": (None, [_vp]),
+    "gsvk_gsv_header": (_i, [_vp, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                             ctypes.POINTER(_vp), ctypes.POINTER(_sz), ctypes.POINTER(_vp),
+                             ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_uint32)]),
+    "gsvk_gsv_tensor_at": (_i, [_vp, _sz, _vp]),
+    "gsvk_gsv_find": (ctypes.c_long, [_vp, ctypes.c_char_p]),
+    "gsvk_gsv_arena": (_i, [_vp, _i, ctypes.POINTER(ctypes.c_uint64),
+                            ctypes.POINTER(ctypes.c_uint64)]),
+    "gsvk_gsv_upload": (_i, [_vp, _i, _vp, _sz, _vp]),
+    "gsvk_gsv_device_ptr": (_vp, [_vp, _i, _vp, _sz]),
     "gsvk_t2s_decode_create": (_i, [_vp, ctypes.POINTER(_vp)]),
 }
 
@@ -401,3 +413,119 @@ class T2SDecode:
             self.close()
         except Exception:
             pass
+
+
+# ---- .gsv container (include/gsvk_gsv.h) ------------------------------------------------------
+
+class GsvTensorInfo(ctypes.Structure):
+    _fields_ = [("name", _vp), ("name_len", _sz), ("rank", ctypes.c_uint32),
+                ("dims", ctypes.c_uint32 * 8), ("numel", ctypes.c_uint64),
+                ("src_dtype", ctypes.c_int), ("f32_offset", ctypes.c_uint64),
+                ("f32_nbytes", ctypes.c_uint64), ("f16_offset", ctypes.c_uint64),
+                ("f16_nbytes", ctypes.c_uint64)]
+
+
+class GsvFile:
+    """A validated .gsv file (gsvk_gsv_open). `tensors` maps name -> info dict; `config` is the
+    parsed JSON (a file whose JSON does not parse is rejected, as GsvFile's constructor does,
+    gsv_loader.cpp:145-150); `upload(kind)` copies the fp16 (F16) or fp32 (F32) segments to one
+    device arena and returns {name: tensor view} for the tensors that have that segment."""
+
+    def __init__(self, path=None, data=None):
+        import json
+        h = _vp()
+        if data is not None:
+            self._buf = ctypes.create_string_buffer(bytes(data), len(data))
+            rc = lib().gsvk_gsv_open_memory(ctypes.cast(self._buf, _vp), len(data), ctypes.byref(h))
+        else:
+            rc = lib().gsvk_gsv_open(os.fsencode(path), ctypes.byref(h))
+        _check("gsvk_gsv_open", rc)
+        self.handle = h
+        ver, flags, n = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        nm, nml, cf, cfl = _vp(), _sz(), _vp(), _sz()
+        _check("gsvk_gsv_header", lib().gsvk_gsv_header(h, ctypes.byref(ver), ctypes.byref(flags),
+                                                        ctypes.byref(nm), ctypes.byref(nml),
+                                                        ctypes.byref(cf), ctypes.byref(cfl),
+                                                        ctypes.byref(n)))
+        self.version, self.flags, self.n_tensors = ver.value, flags.value, n.value
+        self.name = ctypes.string_at(nm.value, nml.value).decode() if nml.value else ""
+        raw = ctypes.string_at(cf.value, cfl.value) if cfl.value else b""
+        try:
+            self.config = json.loads(raw.decode()) if raw else None
+        except ValueError as exc:
+            self.close()
+            raise GsvkError("gsvk_gsv_open: config JSON", E_FORMAT) from exc
+        self.tensors = {}
+        self._index = {}
+        for i in range(self.n_tensors):
+            t = GsvTensorInfo()
+            _check("gsvk_gsv_tensor_at", lib().gsvk_gsv_tensor_at(h, i, ctypes.byref(t)))
+            name = ctypes.string_at(t.name, t.name_len).decode()
+            self.tensors[name] = dict(dims=tuple(t.dims[:t.rank]), numel=t.numel,
+                                      src_dtype=t.src_dtype, f32_offset=t.f32_offset,
+                                      f32_nbytes=t.f32_nbytes, f16_offset=t.f16_offset,
+                                      f16_nbytes=t.f16_nbytes)
+            self._index[name] = i
+
+    def arena_bytes(self, kind):
+        base, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        _check("gsvk_gsv_arena", lib().gsvk_gsv_arena(self.handle, kind, ctypes.byref(base),
+                                                      ctypes.byref(nb)))
+        return nb.value
+
+    def upload(self, kind, device="cuda", stream=None):
+        import torch
+        nb = self.arena_bytes(kind)
+        arena = torch.empty(max(nb, 1), dtype=torch.uint8, device=device)
+        _check("gsvk_gsv_upload", lib().gsvk_gsv_upload(self.handle, kind, arena.data_ptr(),
+                                                        arena.numel(), _stream(stream)))
+        tdt = torch.float16 if kind == F16 else torch.float32
+        esz = 2 if kind == F16 else 4
+        views = {}
+        for name, i in self._index.items():
+            ptr = lib().gsvk_gsv_device_ptr(self.handle, kind, arena.data_ptr(), i)
+            if not ptr:
+                continue
+            off = ptr - arena.data_ptr()
+            n = self.tensors[name]["numel"]
+            views[name] = arena[off:off + n * esz].view(tdt).view(*self.tensors[name]["dims"])
+        return arena, views
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().gsvk_gsv_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def t2s_model_from_gsv(g, dev="cuda", stream=None):
+    """The decode step's model tensors (T2SDecode's `m`) from an ar_s1 .gsv, by the names
+    T2SEngine's loader reads (t2s_engine.cpp:575-627): fp16 copies for the GEMV weights and the
+    audio embedding table, fp32 for biases, LayerNorm parameters and alpha. Caches are the
+    caller's. Returns (m, arenas)."""
+    a16, t16 = g.upload(F16, dev, stream)
+    a32, t32 = g.upload(F32, dev, stream)
+    mc = (g.config or {}).get("model_config") or {}
+    mm = mc.get("model", {})
+    n_layer, heads = int(mm["n_layer"]), int(mm["head"])
+    layers = []
+    for l in range(n_layer):
+        p, ps = f"h.layers.{l}.", f"h.layers.{l}.self_attn."
+        layers.append(dict(wqkv=t16[ps + "in_proj_weight"], bqkv=t32[ps + "in_proj_bias"],
+                           wout=t16[ps + "out_proj.weight"], bout=t32[ps + "out_proj.bias"],
+                           n1g=t32[p + "norm1.weight"], n1b=t32[p + "norm1.bias"],
+                           w1=t16[p + "linear1.weight"], b1=t32[p + "linear1.bias"],
+                           w2=t16[p + "linear2.weight"], b2=t32[p + "linear2.bias"],
+                           n2g=t32[p + "norm2.weight"], n2b=t32[p + "norm2.bias"]))
+    import torch
+    alpha = float(t32["ar_audio_position.alpha"].reshape(-1)[0].item())
+    m = dict(table=t16["ar_audio_embedding.word_embeddings.weight"], heads=heads, layers=layers,
+             w_logits=t16["ar_predict_layer.weight"], alpha=alpha,
+             dims=dict(d_model=int(mm["hidden_dim"]), ffn=int(mm["linear_units"]),
+                       vocab=int(mm["vocab_size"]), n_layer=n_layer))
+    return m, (a16, a32)

@@ -53,6 +53,8 @@ typedef enum gsvk_status {
   GSVK_E_ALIAS = -4,  /* output overlaps an input other than the allowed exact alias  */
   GSVK_E_ARG = -5,    /* other invalid argument (negative or non-finite eps, odd D, …) */
   GSVK_E_HIP = -6,    /* the HIP runtime reported an error at launch                  */
+  GSVK_E_FORMAT = -7, /* malformed .gsv container (gsvk_gsv.h)                         */
+  GSVK_E_IO = -8,     /* a file could not be opened or mapped                          */
 } gsvk_status;
 
 /* Library identification and error text (host only, no GPU needed). */

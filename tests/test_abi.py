@@ -16,7 +16,7 @@ import gsvk
 
 def _declared_functions():
     names = []
-    for h in ("gsvk.h", "gsvk_t2s.h"):
+    for h in ("gsvk.h", "gsvk_t2s.h", "gsvk_gsv.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(gsvk_\w+)\s*\(", text, flags=re.M)
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol(gsvk_lib):
 
 def test_version_and_status_strings(gsvk_lib):
     assert b"gfx950" in gsvk_lib.gsvk_version()
-    for code in (0, -1, -2, -3, -4, -5, -6):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8):
         assert gsvk_lib.gsvk_status_string(code)
     assert gsvk_lib.gsvk_status_string(-99) == b"unknown status"
 

@@ -1,0 +1,81 @@
+"""The .gsv upload on the GPU: both segment arenas arrive bit-exact, the per-tensor device views
+equal the file's arrays, and a decode step built from a .gsv (t2s_model_from_gsv, the names
+T2SEngine's loader reads) matches the oracle chain run on the same weights."""
+import numpy as np
+import pytest
+import torch
+
+import gsvk
+import oracle as O
+from gpu_util import F16, F32, host, say
+from gsv_writer import gsv_bytes, t2s_tensors
+from test_gpu_t2s_decode import compare, oracle_step
+
+pytestmark = pytest.mark.gpu
+
+
+def test_upload_arenas_bit_exact(tmp_path):
+    t, cfg = t2s_tensors(seed=4)
+    p = tmp_path / "m.gsv"
+    p.write_bytes(gsv_bytes("ar_s1v3", t, cfg))
+    g = gsvk.GsvFile(str(p))
+    a16, v16 = g.upload(gsvk.F16)
+    a32, v32 = g.upload(gsvk.F32)
+    torch.cuda.synchronize()
+    say(f"gsv arenas: fp16 {a16.numel()} B, fp32 {a32.numel()} B")
+    for name, arr in t.items():
+        np.testing.assert_array_equal(v32[name].cpu().numpy(), arr.astype(np.float32))
+        if arr.size >= 4096:
+            assert np.array_equal(v16[name].cpu().numpy().view(np.uint16),
+                                  arr.astype(np.float16).view(np.uint16))
+        else:
+            assert name not in v16
+
+
+def test_decode_step_from_gsv_matches_oracle(tmp_path):
+    D, H, FF, L, V, B, max_len = 128, 4, 256, 2, 50, 5, 64
+    t, cfg = t2s_tensors(D, H, FF, L, V, seed=5)
+    p = tmp_path / "m.gsv"
+    p.write_bytes(gsv_bytes("ar_s1v3", t, cfg))
+    g = gsvk.GsvFile(str(p))
+    m, arenas = gsvk.t2s_model_from_gsv(g)
+    r = np.random.default_rng(6)
+    caches = [(O.to_storage(F16, r.standard_normal((B, max_len, D)).astype(np.float32)),
+               O.to_storage(F16, r.standard_normal((B, max_len, D)).astype(np.float32)))
+              for _ in range(L)]
+    for ly, (kc, vc) in zip(m["layers"], caches):
+        ly["k_cache"] = torch.from_numpy(kc.view(np.int16)).view(torch.float16).cuda()
+        ly["v_cache"] = torch.from_numpy(vc.view(np.int16)).view(torch.float16).cuda()
+    m["pe"] = torch.from_numpy(gsvk.pe_table(256, D)).cuda()
+    io_h = dict(ids=r.integers(0, V, B).astype(np.int64), pos=r.integers(0, 200, B).astype(np.int64),
+                kv_pos=r.integers(0, max_len, B).astype(np.int64))
+    iod = dict(ids=torch.from_numpy(io_h["ids"]).cuda(), pos=torch.from_numpy(io_h["pos"]).cuda(),
+               kv_pos=torch.from_numpy(io_h["kv_pos"]).cuda(),
+               err=torch.zeros(1, dtype=torch.int32, device="cuda"),
+               x=torch.empty(B, D, dtype=torch.float16, device="cuda"),
+               h=torch.empty(B, D, dtype=torch.float16, device="cuda"),
+               z=torch.empty(B, D, dtype=torch.float16, device="cuda"),
+               attn=torch.empty(B, D, dtype=torch.float16, device="cuda"),
+               ff=torch.empty(B, FF, dtype=torch.float16, device="cuda"),
+               qkv=torch.empty(B, 3 * D, dtype=torch.float32, device="cuda"),
+               logits=torch.empty(B, V, dtype=torch.float32, device="cuda"))
+    step = gsvk.T2SDecode(m, iod, len_bound=max_len)
+    step.run()
+    torch.cuda.synchronize()
+    # the same model on the host, from the same arrays (fp16 weights; fp32 biases / norms / alpha)
+    mh = dict(table=t["ar_audio_embedding.word_embeddings.weight"].view(np.uint16),
+              pe=gsvk.pe_table(256, D), alpha=np.float32(t["ar_audio_position.alpha"][0]),
+              heads=H, w_logits=t["ar_predict_layer.weight"].view(np.uint16), layers=[])
+    for l in range(L):
+        pfx, ps = f"h.layers.{l}.", f"h.layers.{l}.self_attn."
+        f32 = lambda k: t[k].astype(np.float32)
+        mh["layers"].append(dict(
+            wqkv=t[ps + "in_proj_weight"].view(np.uint16), bqkv=f32(ps + "in_proj_bias"),
+            wout=t[ps + "out_proj.weight"].view(np.uint16), bout=f32(ps + "out_proj.bias"),
+            n1g=f32(pfx + "norm1.weight"), n1b=f32(pfx + "norm1.bias"),
+            w1=t[pfx + "linear1.weight"].view(np.uint16), b1=f32(pfx + "linear1.bias"),
+            w2=t[pfx + "linear2.weight"].view(np.uint16), b2=f32(pfx + "linear2.bias"),
+            n2g=f32(pfx + "norm2.weight"), n2b=f32(pfx + "norm2.bias"),
+            k_cache=caches[l][0].copy(), v_cache=caches[l][1].copy()))
+    x_want, lg_want = oracle_step(mh, io_h)
+    compare(host(iod["x"], F16), host(iod["logits"], F32), x_want, lg_want, "from .gsv")
