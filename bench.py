@@ -28,6 +28,7 @@ Also reported (same JSON line):
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
        python bench.py --only KERNEL   (one kernel of the suite, for rocprofv3 runs)
        python bench.py --pmc           (dominant kernel + a 256 MiB copy, for rocprofv3 --pmc runs)
+       python bench.py --whole-step 1024   (the whole decode step alone, for rocprofv3 runs)
 """
 import argparse
 import json
@@ -644,6 +645,8 @@ def main():
                     help="run the dominant kernel and a plain copy only (for rocprofv3 --pmc)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
+    ap.add_argument("--whole-step", type=int, default=0, metavar="KV_LEN",
+                    help="run only the whole T2S decode step at this KV length (rocprofv3 runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every kernel here is row- or element-local, so more "
@@ -659,6 +662,9 @@ def main():
 
     if a.only:
         kernel_suite(torch, gsvk, dev, only=a.only)
+        return
+    if a.whole_step:
+        print(json.dumps(full_decode_step(torch, gsvk, dev, kv_len=a.whole_step)), flush=True)
         return
 
     bufs = make_step_buffers(torch, gsvk, dev)

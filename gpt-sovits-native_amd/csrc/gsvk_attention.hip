@@ -242,31 +242,41 @@ __global__ __launch_bounds__(kWave * kAttnWaves) void attn_chunk(AttnArgs a) {
   p[2 * kWave + lane] = float4{M, L, 0.f, 0.f};
 }
 
-// Merge the C chunk states of one sequence (chunk order) and divide by the softmax sum.
+// Merge the C chunk states of one sequence and divide by the softmax sum. One wave per chunk
+// loads that chunk's (m, l, o) (all C loads in flight at once); wave 0 merges them in chunk order.
 template <int OUTT>
-__global__ __launch_bounds__(kWave) void attn_merge(AttnArgs a, int C) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(kWave * kMaxChunks) void attn_merge(AttnArgs a, int C) {
+  __shared__ float sm[kMaxChunks][kWave], sl[kMaxChunks][kWave];
+  __shared__ float so[kMaxChunks][8][kWave];
+  const int lane = threadIdx.x & (kWave - 1), c = threadIdx.x / kWave;
   const long b = blockIdx.x;
-  if (8 * lane >= a.D) return;
   const float4* p = a.part + static_cast<size_t>(b) * C * 3 * kWave;
+  if (c < C) {
+    const float4 lo = p[(c * 3 + 0) * kWave + lane], hi = p[(c * 3 + 1) * kWave + lane];
+    const float4 ml = p[(c * 3 + 2) * kWave + lane];
+    sm[c][lane] = ml.x;
+    sl[c][lane] = ml.y;
+    so[c][0][lane] = lo.x;
+    so[c][1][lane] = lo.y;
+    so[c][2][lane] = lo.z;
+    so[c][3][lane] = lo.w;
+    so[c][4][lane] = hi.x;
+    so[c][5][lane] = hi.y;
+    so[c][6][lane] = hi.z;
+    so[c][7][lane] = hi.w;
+  }
+  __syncthreads();
+  if (c != 0 || 8 * lane >= a.D) return;
   float M = -INFINITY;
-  for (int c = 0; c < C; ++c) M = fmaxf(M, p[(c * 3 + 2) * kWave + lane].x);
+  for (int k = 0; k < C; ++k) M = fmaxf(M, sm[k][lane]);
   float L = 0.f, O[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) O[i] = 0.f;
-  for (int c = 0; c < C; ++c) {
-    const float4 lo = p[(c * 3 + 0) * kWave + lane], hi = p[(c * 3 + 1) * kWave + lane];
-    const float4 ml = p[(c * 3 + 2) * kWave + lane];
-    const float f = exp_rel(ml.x, M);
-    L = __builtin_fmaf(ml.y, f, L);
-    O[0] = __builtin_fmaf(lo.x, f, O[0]);
-    O[1] = __builtin_fmaf(lo.y, f, O[1]);
-    O[2] = __builtin_fmaf(lo.z, f, O[2]);
-    O[3] = __builtin_fmaf(lo.w, f, O[3]);
-    O[4] = __builtin_fmaf(hi.x, f, O[4]);
-    O[5] = __builtin_fmaf(hi.y, f, O[5]);
-    O[6] = __builtin_fmaf(hi.z, f, O[6]);
-    O[7] = __builtin_fmaf(hi.w, f, O[7]);
+  for (int k = 0; k < C; ++k) {
+    const float f = exp_rel(sm[k][lane], M);
+    L = __builtin_fmaf(sl[k][lane], f, L);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) O[i] = __builtin_fmaf(so[k][i][lane], f, O[i]);
   }
   float y[8];
   const float inv = 1.f / L;
@@ -289,8 +299,8 @@ void launch_attn(const AttnArgs& a, size_t B, int C, hipStream_t st) {
   hipLaunchKernelGGL((attn_chunk<KVT, OUTT>), dim3(C, static_cast<unsigned>(B)),
                      dim3(kWave * kAttnWaves), 0, st, a);
   if (C > 1)
-    hipLaunchKernelGGL((attn_merge<OUTT>), dim3(static_cast<unsigned>(B)), dim3(kWave), 0, st, a,
-                       C);
+    hipLaunchKernelGGL((attn_merge<OUTT>), dim3(static_cast<unsigned>(B)), dim3(kWave * C), 0, st,
+                       a, C);
 }
 
 template <int KVT>
