@@ -20,6 +20,8 @@
  *   gelu_erf             float64 math.erf closed form, odd-part identity   (no reference vector)
  *   groupnorm_gelu       float64 closed form, T = 1 -> beta                (no reference vector)
  *   leaky / add / mean   exact-rational closed forms, slope identities     (no reference vector)
+ *   conv1d               float64 closed form via numpy correlation, k = 1 matmul, delta inputs
+ *                        give the taps, padding / dilation planted mistakes (no reference vector)
  *   decode_attention     reference softmax golden sm_x / sm_y (test_kern.cpp:219-229) for the
  *                        softmax step, float64 closed form, one-key and equal-key identities
  *   gemv_f16w            reference golden gemv_a / gemv_b (test_kern.cpp:96-120) at its own
@@ -342,6 +344,71 @@ int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const 
   free(xr);
   free(v);
   free(r);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * SoVITS Conv1d with the ResBlock epilogues (next-tier row 4): Conv1d::forward's fallback path
+ * (conv1d.hpp:155-196): same padding pad_l = (k-1)*dilation/2, im2col K index = i*k + kk, fp32
+ * weights (the fp16 weights upcast), y = W col + b ("yr[t] += bc" after the GEMM); then, per epi:
+ *   0: y                                   1: leaky_relu_io(y, slope)      (dec.hpp:323-324)
+ *   2: cur += y; y_out = lrelu(cur, slope) (add_inplace then the next leaky_relu_write, 322-326)
+ *   3: cur += y                            (add_inplace only: the branch's last pair)
+ * The GEMM sums over K in order with one rounding per step (fmaf); Accelerate's sgemm order is not
+ * published, so parity with it is tolerance-based in any case.
+ * --------------------------------------------------------------------------------------------- */
+int oracle_conv1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const float* bias, int epi,
+                  float slope, void* cur, size_t ldc, void* y, size_t ldy, size_t cin, size_t cout,
+                  size_t T, size_t k, size_t dil) {
+  float* xr = (float*)malloc(cin * T * 4);
+  float* wf = (float*)malloc(cout * cin * k * 4);
+  float* row = (float*)malloc(T * 4);
+  if (!xr || !wf || !row) {
+    free(xr);
+    free(wf);
+    free(row);
+    return -1;
+  }
+  for (size_t i = 0; i < cin; ++i) oracle_to_f32(dtype, row_ptr(x, dtype, i * ldx), xr + i * T, T);
+  for (size_t e = 0; e < cout * cin * k; ++e) wf[e] = oracle_h2f(w[e]);
+  const long pad = (long)((k - 1) * dil) / 2;
+  for (size_t o = 0; o < cout; ++o) {
+    for (size_t t = 0; t < T; ++t) {
+      float s = 0.f;
+      for (size_t i = 0; i < cin; ++i)
+        for (size_t kk = 0; kk < k; ++kk) {
+          const long src = (long)t + (long)(kk * dil) - pad;
+          const float xv = (src >= 0 && src < (long)T) ? xr[i * T + (size_t)src] : 0.f;
+          s = fmaf(wf[(o * cin + i) * k + kk], xv, s);
+        }
+      row[t] = bias ? s + bias[o] : s;
+    }
+    if (epi == 1) {
+      for (size_t t = 0; t < T; ++t) row[t] = leaky(row[t], slope);
+      oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), T);
+    } else if (epi == 2 || epi == 3) {
+      float* c = (float*)malloc(T * 4);
+      if (!c) {
+        free(xr);
+        free(wf);
+        free(row);
+        return -1;
+      }
+      oracle_to_f32(dtype, row_ptr(cur, dtype, o * ldc), c, T);
+      for (size_t t = 0; t < T; ++t) c[t] = c[t] + row[t];
+      oracle_from_f32(dtype, c, row_ptr_w(cur, dtype, o * ldc), T);
+      if (epi == 2) {
+        for (size_t t = 0; t < T; ++t) row[t] = leaky(c[t], slope);
+        oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), T);
+      }
+      free(c);
+    } else {
+      oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), T);
+    }
+  }
+  free(xr);
+  free(wf);
+  free(row);
   return 0;
 }
 

@@ -71,6 +71,13 @@ int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const 
                      const float* bias, int act, float slope, const void* residual, int y_dtype,
                      void* y, size_t ldy, size_t rows, size_t out, size_t in);
 
+/* SoVITS Conv1d (conv1d.hpp:155-196) + ResBlock epilogue epi (0 bias, 1 + leaky_relu_io,
+ * 2 cur += y then y = lrelu(cur), 3 cur += y). x [cin, T] (stride ldx), w [cout][cin][k] fp16 bits,
+ * bias [cout] fp32 or NULL, cur / y [cout, T] (strides ldc / ldy), storage dtype for x / cur / y. */
+int oracle_conv1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const float* bias, int epi,
+                  float slope, void* cur, size_t ldc, void* y, size_t ldy, size_t cin, size_t cout,
+                  size_t T, size_t k, size_t dil);
+
 /* Decode attention: KV append at pos[b] and single-query SDPA over keys 0..pos[b] per head
  * (t2s_engine.cpp:1051-1087). kv_dtype 0 = fp32 cache, 1 = fp16 cache. Caches [B][max_len][H*HD];
  * qkv rows [q | k | v] fp32 with stride ldq; out [B][H*HD] fp32 with stride ldo (NaN rows for a

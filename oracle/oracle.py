@@ -39,6 +39,8 @@ _SIG = {
                               _sz]),
     "oracle_decode_attention": (_i, [_i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz]),
     "oracle_softmax": (None, [_vp, _vp, _sz]),
+    "oracle_conv1d": (_i, [_i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
+                           _sz]),
     "oracle_pe_row": (None, [_vp, _sz, _sz]),
     "oracle_embed_pe": (ctypes.c_long, [_i, _i, _i, _vp, _sz, _vp, _vp, ctypes.c_int64, _vp, _sz,
                                         _f, _vp, _vp, _vp, _sz, _sz]),
@@ -187,6 +189,21 @@ def gemv_f16w(x_dt, x, w, y_dt, bias=None, act=0, slope=0.0, residual=None, roun
                                 _p(residual), y_dt, _p(y), n_out, rows, n_out, n_in)
     assert rc == 0
     return y
+
+
+def conv1d(dt, x, w, bias=None, dil=1, epi=0, slope=0.1, cur=None):
+    """SoVITS Conv1d + epilogue. x [cin, T] storage of dt; w [cout, cin, k] uint16 fp16 bits.
+    Returns y (and the updated cur for epi 2 / 3)."""
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w).view(np.uint16)
+    cout, cin, k = w.shape
+    T = x.shape[1]
+    y = np.zeros((cout, T), dtype=storage_dtype(dt))
+    c = None if cur is None else np.ascontiguousarray(cur).copy()
+    rc = lib().oracle_conv1d(dt, _p(x), T, _p(w), _p(bias), epi, slope, _p(c), T, _p(y), T, cin,
+                             cout, T, k, dil)
+    assert rc == 0
+    return (y, c) if epi in (2, 3) else y
 
 
 def softmax(x):
