@@ -427,6 +427,72 @@ def sovits_decoder(torch, gsvk, dev):
     return out
 
 
+# ---- SoVITS ResBlock convolutions --------------------------------------------------------------------
+
+RES_KERNELS = (3, 7, 11)      # ResBlock1 kernel sizes (dec.hpp:55-76)
+RES_DILATIONS = (1, 3, 5)     # conv1 dilations; every conv2 has dilation 1
+PEAK_F16_TFLOPS = 2500.0      # MI355X dense fp16 matrix-core peak
+
+
+def conv_us(torch, fn, iters=10):
+    """Device time of one launch: HIP events around `iters` back-to-back launches."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) * 1e3 / iters
+
+
+def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
+    """Per decoder stage (C, T): every distinct ResBlock convolution timed once (conv1: k x
+    dilation 1 / 3 / 5 with the LeakyReLU epilogue; conv2: k, dilation 1, with the residual +
+    LeakyReLU epilogue), and the stage's 18 convolutions (3 ResBlocks x 3 pairs) summed. fp32
+    activations multiplied exactly (the reference's sgemm path) and, as a second figure, rounded to
+    fp16 (its AMX path). Algorithmic flops 2 C^2 k T per convolution."""
+    stages, tot, tot_rx, flops_tot = [], 0.0, 0.0, 0.0
+    for C, T in DECODER_GEOMETRIES[geometry]:
+        x = torch.randn(C, T, device=dev)
+        y = torch.empty(C, T, device=dev)
+        cur = torch.randn(C, T, device=dev)
+        row = {"C": C, "T": T, "convs": []}
+        st, st_rx, st_fl = 0.0, 0.0, 0.0
+        for k in RES_KERNELS:
+            conv = gsvk.Conv1d((torch.randn(C, C, k, device=dev) / (C * k) ** 0.5).half(),
+                               torch.randn(C, device=dev) * 0.05, 1)
+            fl = 2.0 * C * C * k * T
+            for dil, epi, n in [(d, gsvk.CONV_EPI_LRELU, 1) for d in RES_DILATIONS] + \
+                               [(1, gsvk.CONV_EPI_RES_LRELU, 3)]:
+                conv.dilation = dil
+                us = conv_us(torch, lambda: conv.forward(x, y, epi=epi, cur=cur))
+                us_rx = conv_us(torch, lambda: conv.forward(x, y, epi=epi, cur=cur, round_x=True))
+                row["convs"].append({"k": k, "dil": dil, "epi": epi, "count": n,
+                                     "us": round(us, 2), "us_round_x": round(us_rx, 2),
+                                     "TFLOPs": round(fl / us / 1e6, 1)})
+                st += n * us
+                st_rx += n * us_rx
+                st_fl += n * fl
+        row.update({"stage_us": round(st, 1), "stage_us_round_x": round(st_rx, 1),
+                    "stage_TFLOPs": round(st_fl / st / 1e6, 1)})
+        stages.append(row)
+        tot, tot_rx, flops_tot = tot + st, tot_rx + st_rx, flops_tot + st_fl
+        log(f"  conv stage {C}x{T}: {st:.1f} us (round_x {st_rx:.1f} us), "
+            f"{st_fl / st / 1e6:.0f} TFLOP/s")
+        del x, y, cur, conv
+    torch.cuda.empty_cache()
+    ach = flops_tot / tot / 1e6
+    return {"geometry": geometry, "stages": stages, "resblock_conv_us_per_10s_audio": round(tot, 1),
+            "resblock_conv_us_per_10s_audio_round_x": round(tot_rx, 1),
+            "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_F16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ach / PEAK_F16_TFLOPS, 4),
+                         "flops": flops_tot,
+                         "note": "algorithmic flops; exact fp32 runs two fp16 products per term"}}
+
+
 # ---- whole T2S decode step ---------------------------------------------------------------------------
 
 def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
@@ -645,6 +711,8 @@ def main():
                     help="run the dominant kernel and a plain copy only (for rocprofv3 --pmc)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
+    ap.add_argument("--conv", action="store_true",
+                    help="time the SoVITS ResBlock convolutions per decoder stage and exit")
     ap.add_argument("--whole-step", type=int, default=0, metavar="KV_LEN",
                     help="run only the whole T2S decode step at this KV length (rocprofv3 runs)")
     a = ap.parse_args()
@@ -665,6 +733,9 @@ def main():
         return
     if a.whole_step:
         print(json.dumps(full_decode_step(torch, gsvk, dev, kv_len=a.whole_step)), flush=True)
+        return
+    if a.conv:
+        print(json.dumps(sovits_conv(torch, gsvk, dev)), flush=True)
         return
 
     bufs = make_step_buffers(torch, gsvk, dev)
@@ -730,12 +801,13 @@ def main():
                "single_thread_cv": round(res[1]["cv"], 4),
                "cpu_model": cpu_model(), "hardware_threads": os.cpu_count()}
 
-    kernels = copy_gbs = decoder = full = None
+    kernels = copy_gbs = decoder = full = conv = None
     if not a.no_kernels:
         copy_gbs = copy_bandwidth(torch, dev)
         kernels = kernel_suite(torch, gsvk, dev)
         decoder = sovits_decoder(torch, gsvk, dev)
         full = [full_decode_step(torch, gsvk, dev, kv_len=n) for n in (1024, 2048)]
+        conv = sovits_conv(torch, gsvk, dev)
 
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
@@ -753,6 +825,7 @@ def main():
         "kernels": kernels,
         "sovits_decoder": decoder,
         "t2s_whole_decode_step": full,
+        "sovits_resblock_conv": conv,
     }
     print(json.dumps(line), flush=True)
     step.close()

@@ -1,0 +1,466 @@
+// gsvk_conv.hip — SoVITS Conv1d (same padding, dilation) on the gfx950 matrix cores, with the
+// ResBlock element-wise passes that follow a convolution fused into its store.
+//
+// y[o, t] = bias[o] + sum_{i, kk} w[o, i, kk] x[i, t + kk dil - pad], pad = (k - 1) dil / 2, zero
+// outside [0, T) (Conv1d::forward, conv1d.hpp:109-194: im2col col[(i k + kk), t] then
+// y = W[o, i k] col, then add_bias). Channel-major activations [C, T] with rows of stride ld, fp16 weights.
+//
+// Implicit GEMM: M = T, N = C_out, K = C_in x k, never materialised. One MFMA
+// v_mfma_f32_16x16x32_f16 multiplies a 16 t x 32 channel slice of X^T (operand A) by a 32 channel
+// x 16 o slice of W^T for one tap (operand B); lane l feeds row / column (l & 15) with 8 channels
+// chosen by its lane group (l >> 4), and the accumulator holds, in lane l, four consecutive t
+// 4 (l >> 4) .. +3 of output row o = (l & 15): one 16-byte store per fragment.
+//
+// Workgroup: 4 waves side by side along t, NT fragments (16 NT t) each, all on the same 16 NO
+// output rows. Input channels go in chunks of 32. A chunk of x, with the halo of (k - 1) dil
+// columns the taps reach past the tile, is staged once in LDS and read k times, once per tap at
+// shift kk dil: layout [plane][channel group g = 0..3][t][8 channels], so a fragment read is 16
+// consecutive 16-byte rows (no bank conflicts) and the tap shift is a row offset. The weights are
+// packed once (gsvk_conv1d_pack) as [chunk][tap][o][32 channels]: the B fragment of one step is 16
+// rows x 64 contiguous bytes straight from global memory (L1 / L2: the whole filter bank is at most
+// a few MB and every workgroup reads it), loaded two steps ahead of its use. The next chunk of x is
+// loaded into registers while the current one is multiplied.
+//
+// x in fp32: round_x = 1 rounds it to fp16 (the reference's AMX packing, im2col_to_panel_f16);
+// round_x = 0 keeps fp32 (the reference's default sgemm path) by multiplying hi = f16(x) and
+// lo = f16(x - hi) separately: hi + lo equals x to about 2^-22 relative (|x| < 65504), and the
+// products with fp16 weights are exact in fp32. Sums are fp32 in the matrix cores' order.
+#include <algorithm>
+
+#include "gsvk_common.hpp"
+
+namespace gsvk {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+enum XMode { kXF16 = 0, kXRound = 1, kXSplit = 2 };
+
+constexpr int kChunk = 32;  // input channels per LDS chunk: one MFMA k depth
+constexpr int kOPad = 64;   // packed output rows: a multiple of the largest wave tile
+constexpr int kWaves = 4;   // waves per workgroup, side by side along t
+constexpr int kThreads = kWaves * kWave;
+constexpr int kMaxHalo = 256;
+constexpr int kTapGroup = 4;  // taps whose weights share one LDS refill
+constexpr int kWRow = 40;     // LDS halves per weight row: 32 channels + 8 padding
+
+struct ConvArgs {
+  const void* x;
+  const uint16_t* wp;
+  const float* bias;
+  void* cur;
+  void* y;
+  long cin, cout, T, ldx, ldc, ldy;
+  int k, dil, pad, nch, opad;
+  int epi;
+  float slope;
+  bool vec;
+};
+
+template <int XM>
+constexpr int planes() { return XM == kXSplit ? 2 : 1; }
+
+template <int XM>
+constexpr int storage_dt() { return XM == kXF16 ? GSVK_F16 : GSVK_F32; }
+
+// Packed weights: wp[((c k + kk) opad + o) 32 + j] = w[o, 32 c + j, kk], zero past C_out / C_in.
+__global__ __launch_bounds__(256) void conv_pack(const uint16_t* __restrict__ w,
+                                                 uint16_t* __restrict__ wp, long cout, long cin,
+                                                 long k, long opad, long total) {
+  for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<long>(gridDim.x) * blockDim.x) {
+    const long j = e % kChunk, o = (e / kChunk) % opad, s = e / (kChunk * opad);
+    const long c = s / k, kk = s % k, i = c * kChunk + j;
+    wp[e] = (o < cout && i < cin) ? w[(o * cin + i) * k + kk] : uint16_t(0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void* p, size_t i) { return Store<DT>::load1(p, i); }
+
+// cur[o, t .. t+3] for the residual epilogues, read before any result is stored so that all
+// fragments' loads are in flight together: one vector load for a whole group inside T with aligned
+// rows, otherwise element loads at clamped columns (values past T are not used).
+template <int DT>
+__device__ __forceinline__ f4v load_cur(const ConvArgs& a, long o, long t) {
+  const size_t row = static_cast<size_t>(min(o, a.cout - 1)) * a.ldc;
+  f4v c;
+  if (a.vec && t + 4 <= a.T) {
+    if constexpr (DT == GSVK_F32) {
+      c = *reinterpret_cast<const f4v*>(static_cast<const float*>(a.cur) + row + t);
+    } else {
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.cur) + row + t);
+      c = f4v{h2f(q.x & 0xffffu), h2f(q.x >> 16), h2f(q.y & 0xffffu), h2f(q.y >> 16)};
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c[q] = ld1<DT>(a.cur, row + min(t + q, a.T - 1));
+  }
+  return c;
+}
+
+// Four consecutive outputs t .. t+3 of row o: bias, epilogue, stores. Vector stores when the whole
+// group lies inside T and the rows are aligned.
+template <int DT>
+__device__ __forceinline__ void finish4(const ConvArgs& a, long o, long t, f4v s, float b,
+                                        f4v cur) {
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = a.bias ? s[q] + b : s[q];
+  const size_t yo = static_cast<size_t>(o) * a.ldy + t;
+  const size_t co = static_cast<size_t>(o) * a.ldc + t;
+  const bool full = a.vec && t + 4 <= a.T;
+  if (a.epi >= 2) {  // cur += conv (+ b); epi 2 also writes y = lrelu(cur)
+    float c[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c[q] = cur[q] + v[q];
+    if (full) {
+      if constexpr (DT == GSVK_F32)
+        *reinterpret_cast<float4*>(static_cast<float*>(a.cur) + co) = float4{c[0], c[1], c[2], c[3]};
+      else
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.cur) + co) =
+            uint2{f2h2(c[0], c[1]), f2h2(c[2], c[3])};
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (t + q < a.T) Store<DT>::store1(a.cur, co + q, c[q]);
+    }
+    if (a.epi == 3) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = lrelu_ref(c[q], a.slope);
+  } else if (a.epi == 1) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = lrelu_ref(v[q], a.slope);
+  }
+  if (full) {
+    if constexpr (DT == GSVK_F32)
+      *reinterpret_cast<float4*>(static_cast<float*>(a.y) + yo) = float4{v[0], v[1], v[2], v[3]};
+    else
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + yo) =
+          uint2{f2h2(v[0], v[1]), f2h2(v[2], v[3])};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (t + q < a.T) Store<DT>::store1(a.y, yo + q, v[q]);
+  }
+}
+
+// XM: activation mode; NT: 16-t fragments per wave; NO: 16-row output fragments per wave;
+// HMAX: largest halo (k - 1) dil the LDS tile holds.
+template <int XM, int NT, int NO, int HMAX>
+__global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
+  constexpr int DT = storage_dt<XM>();
+  constexpr int P = planes<XM>();
+  constexpr int TT = kWaves * 16 * NT;  // output columns of the workgroup
+  constexpr int TTH = TT + HMAX;        // staged columns (tile + halo)
+  constexpr int NI = TTH / kWave;       // staged columns per lane
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [P][4][TTH][8]
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const long t0 = static_cast<long>(blockIdx.x) * TT;
+  const long o0 = static_cast<long>(blockIdx.y) * (16 * NO);
+
+  // ---- x chunk: global -> registers -> LDS ------------------------------------------------------
+  // Wave g stages channel group g (channels 8 g .. 8 g + 7 of the chunk) over all TTH columns:
+  // lane l holds column tp = l + 64 u (global column t0 - pad + tp, clamped into [0, T)). The row
+  // is wave-uniform, so each load is a buffer load with the column as its 32-bit offset and the
+  // row, clamped to the chunk's last row, as a scalar offset: every load reads inside x. Clamped
+  // values are zeroed when staged (a zero pad, and no 0 * inf from channels past C_in).
+  static_assert(TTH % kWave == 0, "staged columns: whole waves");
+  constexpr int ESZ = DT == GSVK_F32 ? 4 : 2;
+  const int g = __builtin_amdgcn_readfirstlane(wave);
+  const int row_bytes = static_cast<int>(a.ldx) * ESZ;
+  int tcol[NI];
+#pragma unroll
+  for (int u = 0; u < NI; ++u)
+    tcol[u] = static_cast<int>(min(max(t0 - a.pad + lane + kWave * u, 0l), a.T - 1)) * ESZ;
+  uint32_t raw[NI][8];  // bit patterns; converted when staged so the loads stay in flight
+  auto xload = [&](int c) {
+    const long ch0 = static_cast<long>(c) * kChunk;
+    const int last = static_cast<int>(min(a.cin - ch0, static_cast<long>(kChunk))) - 1;
+    const char* base = static_cast<const char*>(a.x) + static_cast<size_t>(ch0) * row_bytes;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(base), 0, last * row_bytes + static_cast<int>(a.T) * ESZ, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int srow = min(8 * g + j, last) * row_bytes;
+#pragma unroll
+      for (int u = 0; u < NI; ++u) {
+        if constexpr (DT == GSVK_F32)
+          raw[u][j] = __builtin_amdgcn_raw_buffer_load_b32(rs, tcol[u], srow, 0);
+        else
+          raw[u][j] = __builtin_amdgcn_raw_buffer_load_b16(rs, tcol[u], srow, 0);
+      }
+    }
+  };
+  auto stage = [&](int c) {
+    const long ch0 = static_cast<long>(c) * kChunk + 8 * g;
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const int tp = lane + kWave * u;
+      const long t = t0 - a.pad + tp;
+      const bool tok = t >= 0 && t < a.T;
+      h8 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv = DT == GSVK_F32 ? __builtin_bit_cast(float, raw[u][j]) : h2f(raw[u][j]);
+        const float v = tok && ch0 + j < a.cin ? xv : 0.f;
+        hi[j] = static_cast<_Float16>(v);
+        if constexpr (P == 2) {  // an infinite x leaves inf - inf: its remainder is 0
+          const float rest = v - static_cast<float>(hi[j]);
+          lo[j] = static_cast<_Float16>(rest == rest ? rest : 0.f);
+        }
+      }
+      *reinterpret_cast<h8*>(xs + (static_cast<size_t>(g) * TTH + tp) * 8) = hi;
+      if constexpr (P == 2)
+        *reinterpret_cast<h8*>(xs + (static_cast<size_t>(4 + g) * TTH + tp) * 8) = lo;
+    }
+  };
+
+  // ---- weights: groups of up to kTapGroup taps of the chunk through LDS ------------------------
+  // Group q covers chunk c = q / ng, taps kk0 = 4 (q % ng) .. +3 (fewer at the end of k). Its
+  // packed rows [s][o0 .. o0 + 16 NO)[32] (s = c k + kk) are 16 NO x 64 contiguous bytes per tap:
+  // item it = tid + 256 u is tap it / (64 NO), row (it % (64 NO)) / 4, 16-byte part it % 4. In LDS
+  // a row holds kWRow halves (32 + 8 padding) so that the 16 rows of a fragment read fall on
+  // distinct banks.
+  _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][16 NO][kWRow]
+  const int ng = (a.k + kTapGroup - 1) / kTapGroup;
+  const int Q = a.nch * ng;
+  u32x4 wraw[NO];
+  auto wload = [&](int q) {
+    const int c = q / ng, kk0 = (q - c * ng) * kTapGroup, nt = min(kTapGroup, a.k - kk0);
+    const size_t s0 = static_cast<size_t>(c) * a.k + kk0;
+#pragma unroll
+    for (int u = 0; u < NO; ++u) {
+      const int it = tid + kThreads * u;
+      const int tap = it / (64 * NO), rem = it - tap * 64 * NO;
+      const size_t row = (s0 + min(tap, nt - 1)) * a.opad + o0 + (rem >> 2);
+      wraw[u] = ld16<false>(a.wp + row * kChunk + (rem & 3) * 8);
+    }
+  };
+  auto wstage = [&]() {
+#pragma unroll
+    for (int u = 0; u < NO; ++u) {
+      const int it = tid + kThreads * u;
+      const int tap = it / (64 * NO), rem = it - tap * 64 * NO;
+      *reinterpret_cast<u32x4*>(ws + (tap * 16 * NO + (rem >> 2)) * kWRow + (rem & 3) * 8) =
+          wraw[u];
+    }
+  };
+
+  float bias[NO];
+#pragma unroll
+  for (int n = 0; n < NO; ++n)
+    bias[n] = a.bias ? a.bias[min(o0 + 16 * n + r16, a.cout - 1)] : 0.f;
+
+  f4v acc[NT][NO];
+#pragma unroll
+  for (int i = 0; i < NT; ++i)
+#pragma unroll
+    for (int n = 0; n < NO; ++n) acc[i][n] = f4v{0.f, 0.f, 0.f, 0.f};
+
+  // One step: tap kk0 + tl (slot tl of the group) of the staged chunk. Only LDS reads feed the
+  // MFMAs.
+  const _Float16* xw = xs + (static_cast<size_t>(grp) * TTH + wave * 16 * NT + r16) * 8;
+  const _Float16* wr = ws + r16 * kWRow + 8 * grp;
+  auto step = [&](int kk, int tl) {
+    const int sh = kk * a.dil;
+    h8 xf[NT][P], wf[NO];
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int i = 0; i < NT; ++i)
+        xf[i][p] = *reinterpret_cast<const h8*>(
+            xw + (static_cast<size_t>(p) * 4 * TTH + 16 * i + sh) * 8);
+#pragma unroll
+    for (int n = 0; n < NO; ++n)
+      wf[n] = *reinterpret_cast<const h8*>(wr + (tl * 16 * NO + 16 * n) * kWRow);
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int n = 0; n < NO; ++n)
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[i][p], wf[n], acc[i][n], 0, 0, 0);
+  };
+
+  // Group g of chunk c: refill LDS from the registers loaded one group earlier (x only at g = 0),
+  // then load ahead: the next group's weights first, then, at g = 0, the next chunk's x. Issued in
+  // that order, each weight load can be waited for without waiting for the x loads, which get the
+  // whole chunk to arrive. The last group reloads in-bounds data that is not used. The groups of a chunk are laid out in straight-line code (at most three
+  // for k <= 12; further groups loop) so the compiler can count the loads in flight exactly.
+  auto group = [&](int c, int g) {
+    const int kk0 = g * kTapGroup, nt = min(kTapGroup, a.k - kk0);
+    if (c > 0 || g > 0) __syncthreads();  // every wave is done with the previous group
+    if (g == 0) stage(c);
+    wstage();
+    __syncthreads();
+    // (Unconditional, with clamped indices past the end: loads under a branch would make the
+    // compiler assume the worst order and wait for the x loads here.)
+    wload(min(c * ng + g + 1, Q - 1));
+    __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the x loads
+    if (g == 0) xload(min(c + 1, a.nch - 1));
+#pragma unroll
+    for (int tl = 0; tl < kTapGroup; ++tl)
+      if (tl < nt) step(kk0 + tl, tl);
+  };
+
+  xload(0);
+  wload(0);
+  for (int c = 0; c < a.nch; ++c) {
+    group(c, 0);
+    if (ng > 1) group(c, 1);
+    if (ng > 2) group(c, 2);
+    for (int g = 3; g < ng; ++g) group(c, g);
+  }
+
+  // ---- epilogue ---------------------------------------------------------------------------------
+  f4v cur[NT][NO];
+  if (a.epi >= 2) {
+#pragma unroll
+    for (int n = 0; n < NO; ++n)
+#pragma unroll
+      for (int i = 0; i < NT; ++i)
+        cur[i][n] = load_cur<DT>(a, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
+  }
+#pragma unroll
+  for (int n = 0; n < NO; ++n) {
+    const long o = o0 + 16 * n + r16;
+    if (o >= a.cout) continue;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const long t = t0 + wave * 16 * NT + 16 * i + 4 * grp;
+      if (t < a.T) finish4<DT>(a, o, t, acc[i][n], bias[n], cur[i][n]);
+    }
+  }
+}
+
+template <int XM, int NT, int NO, int HMAX>
+constexpr size_t lds_bytes() {
+  return static_cast<size_t>(planes<XM>()) * 4 * (kWaves * 16 * NT + HMAX) * 16 +
+         static_cast<size_t>(kTapGroup) * 16 * NO * kWRow * 2;
+}
+
+template <int XM, int NT, int NO, int HMAX>
+int launch_tiles(const ConvArgs& a, hipStream_t st) {
+  constexpr size_t lds = lds_bytes<XM, NT, NO, HMAX>();
+  auto kern = conv1d_mfma<XM, NT, NO, HMAX>;
+  if constexpr (lds > 64 * 1024) {
+    static const bool opted = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  static_cast<int>(lds)) == hipSuccess;
+    if (!opted) return GSVK_E_HIP;
+  }
+  const long gx = (a.T + kWaves * 16 * NT - 1) / (kWaves * 16 * NT);
+  const long gy = (a.cout + 16 * NO - 1) / (16 * NO);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
+                     dim3(kThreads), lds, st, a);
+  return launch_status();
+}
+
+template <int XM, int NT, int HMAX>
+int launch_no(const ConvArgs& a, int no, hipStream_t st) {
+  switch (no) {
+    case 1: return launch_tiles<XM, NT, 1, HMAX>(a, st);
+    case 2: return launch_tiles<XM, NT, 2, HMAX>(a, st);
+    case 3: return launch_tiles<XM, NT, 3, HMAX>(a, st);
+    default: return launch_tiles<XM, NT, 4, HMAX>(a, st);
+  }
+}
+
+// Output rows per wave: the largest fragment count (4..1) that pads at most a sixth of the rows
+// it computes, and whose last tile stays inside the packed rows. Columns per wave: 64, or 32 when
+// that leaves fewer than two workgroups per CU.
+template <int XM>
+int launch_plan(const ConvArgs& a, hipStream_t st) {
+  const long ofr = (a.cout + 15) / 16;
+  int no = 1;
+  for (int c = 4; c > 1; --c) {
+    const long rows = (ofr + c - 1) / c * c;
+    if (6 * (rows - ofr) <= rows && rows * 16 <= a.opad) {
+      no = c;
+      break;
+    }
+  }
+  const long tiles64 = (a.T + 255) / 256 * ((ofr + no - 1) / no);
+  const bool nt2 = tiles64 < 512;
+  const int halo = (a.k - 1) * a.dil;
+  if (halo <= 64)
+    return nt2 ? launch_no<XM, 2, 64>(a, no, st) : launch_no<XM, 4, 64>(a, no, st);
+  return launch_no<XM, 1, kMaxHalo>(a, no, st);
+}
+
+}  // namespace
+}  // namespace gsvk
+
+using namespace gsvk;
+
+extern "C" size_t gsvk_conv1d_packed_elems(size_t c_out, size_t c_in, size_t k) {
+  if (!c_out || !c_in || !k) return 0;
+  return (c_in + kChunk - 1) / kChunk * k * ((c_out + kOPad - 1) / kOPad * kOPad) * kChunk;
+}
+
+extern "C" int gsvk_conv1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k,
+                                uint16_t* w_packed, size_t packed_elems, void* stream) {
+  if (!w || !w_packed) return GSVK_E_NULL;
+  if (!c_out || !c_in || !k || c_out > (1ul << 24) || c_in > (1ul << 24) || k > 4096)
+    return GSVK_E_SIZE;
+  const size_t total = gsvk_conv1d_packed_elems(c_out, c_in, k);
+  if (packed_elems < total) return GSVK_E_SIZE;
+  if (overlaps(w, c_out * c_in * k * 2, w_packed, total * 2)) return GSVK_E_ALIAS;
+  const long opad = static_cast<long>((c_out + kOPad - 1) / kOPad * kOPad);
+  const long blocks = std::min<long>((static_cast<long>(total) + 255) / 256, 16384);
+  hipLaunchKernelGGL(conv_pack, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), w, w_packed, static_cast<long>(c_out),
+                     static_cast<long>(c_in), static_cast<long>(k), opad,
+                     static_cast<long>(total));
+  return launch_status();
+}
+
+extern "C" int gsvk_conv1d(int dtype, int round_x, const void* x, size_t ldx,
+                           const uint16_t* w_packed, const float* bias, int epi, float slope,
+                           void* cur, size_t ldc, void* y, size_t ldy, size_t c_in, size_t c_out,
+                           size_t T, size_t k, size_t dilation, void* stream) {
+  if (dtype != GSVK_F32 && dtype != GSVK_F16) return GSVK_E_DTYPE;
+  if (epi < GSVK_CONV_EPI_BIAS || epi > GSVK_CONV_EPI_RES) return GSVK_E_DTYPE;
+  const bool has_res = epi == GSVK_CONV_EPI_RES_LRELU || epi == GSVK_CONV_EPI_RES;
+  const bool has_y = epi != GSVK_CONV_EPI_RES;
+  if (!x || !w_packed || (has_y && !y) || (has_res && !cur)) return GSVK_E_NULL;
+  if (!c_in || !c_out || !T || !k || !dilation || ldx < T || (has_y && ldy < T) ||
+      (has_res && ldc < T))
+    return GSVK_E_SIZE;
+  if (c_in > (1ul << 24) || c_out > (1ul << 24) || k > 4096 || dilation > 4096 ||
+      T > (1ul << 31) - 512 || ldx > (1ul << 40) || ldy > (1ul << 40) || ldc > (1ul << 40))
+    return GSVK_E_SIZE;
+  if ((k - 1) * dilation > static_cast<size_t>(kMaxHalo)) return GSVK_E_ARG;
+  // a chunk of 32 input rows is addressed with 32-bit byte offsets
+  if (kChunk * ldx * dtype_size(dtype) >= (1ul << 31)) return GSVK_E_SIZE;
+  if (!aligned16(w_packed)) return GSVK_E_ARG;
+  const size_t esz = dtype_size(dtype);
+  const size_t xb = span_bytes(c_in, T, ldx, esz);
+  const size_t wb = gsvk_conv1d_packed_elems(c_out, c_in, k) * 2;
+  const size_t bb = bias ? c_out * 4 : 0;
+  const void* yp = has_y ? y : nullptr;
+  const void* cp = has_res ? cur : nullptr;
+  const size_t yb = has_y ? span_bytes(c_out, T, ldy, esz) : 0;
+  const size_t cb = has_res ? span_bytes(c_out, T, ldc, esz) : 0;
+  if (overlaps(yp, yb, x, xb) || overlaps(yp, yb, w_packed, wb) || overlaps(yp, yb, bias, bb) ||
+      overlaps(yp, yb, cp, cb) || overlaps(cp, cb, x, xb) || overlaps(cp, cb, w_packed, wb) ||
+      overlaps(cp, cb, bias, bb))
+    return GSVK_E_ALIAS;
+
+  ConvArgs a{x, w_packed, bias, cur, y, static_cast<long>(c_in), static_cast<long>(c_out),
+             static_cast<long>(T), static_cast<long>(ldx), static_cast<long>(has_res ? ldc : 0),
+             static_cast<long>(has_y ? ldy : 0), static_cast<int>(k), static_cast<int>(dilation),
+             static_cast<int>((k - 1) * dilation / 2),
+             static_cast<int>((c_in + kChunk - 1) / kChunk),
+             static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad), epi, slope, false};
+  const size_t va = esz * 4;  // one vector: four elements
+  a.vec = T >= 4 && (!has_y || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % va == 0)) &&
+          (!has_res || (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(cur) % va == 0));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == GSVK_F16) return launch_plan<kXF16>(a, st);
+  return round_x ? launch_plan<kXRound>(a, st) : launch_plan<kXSplit>(a, st);
+}

@@ -15,6 +15,7 @@ F32, F16, BF16 = 0, 1, 2
 I64, I32 = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_LEAKY_RELU = 0, 1, 2, 3
 OK, E_NULL, E_SIZE, E_DTYPE, E_ALIAS, E_ARG, E_HIP, E_FORMAT, E_IO = 0, -1, -2, -3, -4, -5, -6, -7, -8
+CONV_EPI_BIAS, CONV_EPI_LRELU, CONV_EPI_RES_LRELU, CONV_EPI_RES = 0, 1, 2, 3
 
 # Every exported symbol of the C ABI with (restype, argtypes).
 _vp, _sz, _i, _f, _d = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_double
@@ -29,6 +30,10 @@ SIGNATURES = {
     "gsvk_decode_attention": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz,
                                    _sz, _vp, _sz, _vp, _vp]),
     "gsvk_decode_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
+    "gsvk_conv1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
+                         _sz, _vp]),
+    "gsvk_conv1d_packed_elems": (_sz, [_sz, _sz, _sz]),
+    "gsvk_conv1d_pack": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
     "gsvk_groupnorm_gelu": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _d, _i, _vp]),
     "gsvk_leaky_relu": (_i, [_i, _vp, _vp, _sz, _f, _vp]),
     "gsvk_resblock_add_lrelu": (_i, [_i, _vp, _vp, _vp, _sz, _f, _vp]),
@@ -147,6 +152,53 @@ def gemv_f16w(x, w, y, bias=None, act=ACT_NONE, slope=0.0, residual=None, round_
                   lib().gsvk_gemv_f16w(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(w),
                                        _ptr(bias), act, slope, _ptr(residual), dtype_code(y),
                                        _ptr(y), ldy, rows, n_out, n_in, _stream(stream)))
+
+
+def conv1d_pack(w, stream=None):
+    """Pack a [c_out, c_in, k] fp16 filter bank on its device; returns the packed uint16 tensor."""
+    import torch
+    c_out, c_in, k = w.shape
+    assert w.dtype in (torch.float16, torch.int16) and w.is_contiguous()
+    n = lib().gsvk_conv1d_packed_elems(c_out, c_in, k)
+    wp = torch.empty(n, dtype=torch.int16, device=w.device)
+    _check("gsvk_conv1d_pack", lib().gsvk_conv1d_pack(_ptr(w), c_out, c_in, k, _ptr(wp), n,
+                                                      _stream(stream)))
+    return wp
+
+
+def conv1d(x, wp, c_out, k, y=None, bias=None, dilation=1, epi=CONV_EPI_BIAS, slope=0.1, cur=None,
+           round_x=False, stream=None, check=True):
+    """SoVITS Conv1d on channel-major x [c_in, T] with packed weights (conv1d_pack) and a fused
+    epilogue (CONV_EPI_*); y / cur [c_out, T] of x's dtype."""
+    c_in, T, ldx = _rows(x)
+    ldy = _rows(y)[2] if y is not None else 0
+    ldc = _rows(cur)[2] if cur is not None else 0
+    rc = lib().gsvk_conv1d(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(wp), _ptr(bias), epi,
+                           slope, _ptr(cur), ldc, _ptr(y), ldy, c_in, c_out, T, k, dilation,
+                           _stream(stream))
+    return _check("gsvk_conv1d", rc) if check else rc
+
+
+class Conv1d:
+    """Mirror of the reference's sovits::Conv1d (conv1d.hpp:56-203): out_c, in_c, k, dilation, the
+    fp16 weights packed once at load, fp32 bias (zeros when absent), forward(x, y)."""
+
+    def __init__(self, w16, bias=None, dilation=1, stream=None):
+        import torch
+        self.out_c, self.in_c, self.k = (int(d) for d in w16.shape)
+        self.dilation = int(dilation)
+        self.wp = conv1d_pack(w16.contiguous(), stream)
+        self.b = bias if bias is not None else torch.zeros(self.out_c, dtype=torch.float32,
+                                                           device=w16.device)
+
+    def forward(self, x, y=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None, round_x=False,
+                stream=None):
+        import torch
+        if y is None and epi != CONV_EPI_RES:
+            y = torch.empty(self.out_c, x.shape[1], dtype=x.dtype, device=x.device)
+        conv1d(x, self.wp, self.out_c, self.k, y, self.b, self.dilation, epi, slope, cur, round_x,
+               stream)
+        return y
 
 
 _WS = {}

@@ -45,6 +45,14 @@ typedef enum gsvk_act {
   GSVK_ACT_LEAKY_RELU = 3, /* sovits::leaky_relu_write semantics (nn_ops.hpp:64-74) */
 } gsvk_act;
 
+typedef enum gsvk_conv_epi {
+  GSVK_CONV_EPI_BIAS = 0,       /* y = conv + bias                           (conv1d.hpp:193-202) */
+  GSVK_CONV_EPI_LRELU = 1,      /* y = lrelu(conv + bias)         conv1 then leaky_relu_io (dec.hpp:323-324) */
+  GSVK_CONV_EPI_RES_LRELU = 2,  /* cur += conv + bias; y = lrelu(cur)  conv2, add_inplace, next
+                                   leaky_relu_write (dec.hpp:325-326, 322) */
+  GSVK_CONV_EPI_RES = 3,        /* cur += conv + bias (y unused)      a branch's last conv2 (dec.hpp:325-326) */
+} gsvk_conv_epi;
+
 typedef enum gsvk_status {
   GSVK_OK = 0,
   GSVK_E_NULL = -1,   /* a required pointer is NULL                                  */
@@ -146,6 +154,38 @@ int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* qkv, size_t 
 /* Workspace bytes gsvk_decode_attention uses for these sizes (0: none). Host only. */
 size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t head_dim,
                                              size_t len_bound);
+
+/* ------------------------------------------------------------------------------------------------
+ * SoVITS Conv1d, same padding with dilation, and the ResBlock passes that follow it.
+ *   v[o, t] = bias[o] + sum_{i < c_in, kk < k} w[o, i, kk] * x[i, t + kk*dilation - pad],
+ *   pad = (k - 1) * dilation / 2, x = 0 outside [0, T); the output has T columns.
+ *   epi (gsvk_conv_epi): BIAS y = v; LRELU y = lrelu(v, slope); RES_LRELU cur += v, y =
+ *   lrelu(cur, slope) (from the fp32 sum); RES cur += v (y may be NULL).
+ * Replaces Conv1d::forward (src/sovits/conv1d.hpp:109-194: im2col, sgemm, add_bias) and, fused
+ * into its store, the ResBlock passes after each convolution in Generator::forward
+ * (src/sovits/dec.hpp:322-326: leaky_relu_io after conv1, add_inplace after conv2 and the next
+ * pair's leaky_relu_write).
+ * Layout: channel-major [channels, T] rows with strides ldx, ldc, ldy >= T; x, cur, y of dtype
+ * (F32 or F16); bias fp32 [c_out] or NULL (conv_post has none, conv1d.hpp:82-88); w_packed from
+ * gsvk_conv1d_pack, 16-byte aligned. dtype F32 multiplies the fp32 activations exactly
+ * (round_x = 0, the reference's sgemm path; |x| < 65504) or rounded to fp16 (round_x = 1, as the
+ * reference's AMX path packs them, conv1d.hpp:130-151); F16 storage rounds each output once.
+ * (k - 1) * dilation <= 256. y and cur must not overlap x, the weights, the bias or each other
+ * (the reference's in-place x == y goes through a copy; here the caller keeps them apart).
+ * The sum is formed in the matrix cores' order: |y - ref| <= 1e-5 * max(1, max_t |ref[o, t]|)
+ * against the fp32 reference (fp32 storage). Deterministic.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_conv1d(int dtype, int round_x, const void* x, size_t ldx, const uint16_t* w_packed,
+                const float* bias, int epi, float slope, void* cur, size_t ldc, void* y, size_t ldy,
+                size_t c_in, size_t c_out, size_t T, size_t k, size_t dilation, void* stream);
+/* Elements (uint16_t) of the packed weights of a [c_out, c_in, k] filter bank (0 for a zero size).
+ * Host only. */
+size_t gsvk_conv1d_packed_elems(size_t c_out, size_t c_in, size_t k);
+/* Pack a torch-layout [c_out, c_in, k] fp16 filter bank (the .gsv layout; Conv1d::load,
+ * conv1d.hpp:74-107, packs its AMX panel once the same way) into the layout gsvk_conv1d reads:
+ * [c_in / 32][k][c_out padded to 64][32], zero padded. Runs on the GPU, once per model load. */
+int gsvk_conv1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k, uint16_t* w_packed,
+                     size_t packed_elems, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * GroupNorm with one group per channel, optionally followed by GELU(erf).

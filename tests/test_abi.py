@@ -140,6 +140,43 @@ def test_attention_validation(gsvk_lib):
     assert gsvk_lib.gsvk_decode_attention_workspace_bytes(64, 16, 32, 1024) > 0
 
 
+def test_conv_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_conv1d
+    n = gsvk_lib.gsvk_conv1d_packed_elems(8, 16, 3)
+    assert n == 1 * 3 * 64 * 32  # one 32-channel chunk, 3 taps, 8 outputs padded to 64
+    assert gsvk_lib.gsvk_conv1d_packed_elems(0, 16, 3) == 0
+    assert gsvk_lib.gsvk_conv1d_packed_elems(65, 33, 1) == 2 * 1 * 128 * 32
+
+    def call(dt=0, x=A, ldx=100, w=B, bias=None, epi=0, cur=None, ldc=0, y=C, ldy=100, cin=16,
+             cout=8, T=100, k=3, dil=1):
+        return f(dt, 0, x, ldx, w, bias, epi, 0.1, cur, ldc, y, ldy, cin, cout, T, k, dil, None)
+
+    assert call(dt=2) == gsvk.E_DTYPE           # bf16 activations are not a reference input
+    assert call(epi=4) == gsvk.E_DTYPE
+    assert call(x=None) == gsvk.E_NULL
+    assert call(w=None) == gsvk.E_NULL
+    assert call(y=None) == gsvk.E_NULL
+    assert call(epi=2, cur=None) == gsvk.E_NULL  # the residual modes need cur
+    assert call(T=0) == gsvk.E_SIZE
+    assert call(dil=0) == gsvk.E_SIZE
+    assert call(ldx=99) == gsvk.E_SIZE
+    assert call(ldy=99) == gsvk.E_SIZE
+    assert call(epi=3, cur=0x700000, ldc=99, y=None) == gsvk.E_SIZE
+    assert call(k=11, dil=26) == gsvk.E_ARG      # halo (k - 1) dil above 256
+    assert call(w=B + 8) == gsvk.E_ARG           # packed weights not 16-byte aligned
+    assert call(ldx=1 << 26, T=100) == gsvk.E_SIZE  # 32 rows beyond 32-bit offsets
+    assert call(y=A + 64) == gsvk.E_ALIAS        # output over x
+    assert call(y=B + 64) == gsvk.E_ALIAS        # output over the weights
+    assert call(bias=C + 16) == gsvk.E_ALIAS     # bias inside y
+    assert call(epi=2, cur=C + 64, ldc=100) == gsvk.E_ALIAS  # cur over y
+    assert call(epi=3, cur=A + 4, ldc=100, y=None) == gsvk.E_ALIAS  # cur over x
+    p = gsvk_lib.gsvk_conv1d_pack
+    assert p(None, 8, 16, 3, B, n, None) == gsvk.E_NULL
+    assert p(A, 8, 16, 3, B, n - 1, None) == gsvk.E_SIZE
+    assert p(A, 8, 16, 0, B, n, None) == gsvk.E_SIZE
+    assert p(A, 8, 16, 3, A + 64, n, None) == gsvk.E_ALIAS
+
+
 def test_embed_validation(gsvk_lib):
     f = gsvk_lib.gsvk_embed_pe
     args = dict(out=0, tab=1, it=0, table=A, vocab=10, ids=B, pos=None, pos0=0, pe=C, max_pos=4,

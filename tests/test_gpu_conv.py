@@ -1,0 +1,207 @@
+"""GPU parity of gsvk_conv1d (SoVITS Conv1d on the matrix cores with the ResBlock epilogues fused)
+against the oracle's restatement of Conv1d::forward (conv1d.hpp:109-194) and the passes after it
+in Generator::forward (dec.hpp:322-326).
+
+Tolerance: the sum is formed in another order than the reference's (matrix-core tiles over 32
+channels x one tap), so results follow the reference's own rule between two summation orders
+(test_kern.cpp:111-118): |got - want| <= 1e-5 * max(1, max_t |conv[o, t]|) per output row o, plus
+one fp32 step of the result (the residual add after it), and one fp16 step for fp16 storage (a
+difference at the 1e-5 level can cross a rounding boundary). NaN / inf positions must agree.
+
+Full reference sizes (the decoder stages at 500 frames, T up to 320,000) are checked through
+column windows: a same-padded convolution restricted to columns [a, b) only reads x columns
+[a - pad, b - pad + halo), so the oracle run on x[:, a - halo : b + halo] (clipped to [0, T), where
+the clip coincides with the zero padding) gives exactly those outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import gsvk
+import oracle as O
+from gpu_util import F16, F32, dev, devf, host, say
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(k):
+    return np.random.default_rng(20250823 + 17000 + k)
+
+
+def step16(w):
+    w = np.abs(w.astype(np.float64))
+    return np.spacing(np.minimum(w, 65504).astype(np.float16)).astype(np.float64)
+
+
+def assert_conv_close(dt, got, want, conv_ref, what=""):
+    g = O.to_f32(dt, got).astype(np.float64)
+    w = O.to_f32(dt, want).astype(np.float64)
+    assert g.shape == w.shape
+    gn, wn = ~np.isfinite(g), ~np.isfinite(w)
+    assert np.array_equal(np.isnan(g), np.isnan(w)), f"{what}: NaN positions differ"
+    assert np.array_equal(np.isinf(g), np.isinf(w)), f"{what}: inf positions differ"
+    assert np.array_equal(g[np.isinf(w)], w[np.isinf(w)]), f"{what}: inf signs differ"
+    c = np.abs(O.to_f32(F32 if conv_ref.dtype == np.float32 else dt, conv_ref).astype(np.float64))
+    c[~np.isfinite(c)] = 0
+    peak = np.maximum(1.0, c.max(axis=1, keepdims=True))
+    tol = 1e-5 * peak + 2.0 ** -23 * np.abs(w)
+    if dt == F16:
+        tol = tol + step16(w)
+    err = np.abs(g - w)
+    err[wn] = 0
+    bad = np.argwhere(err > tol)
+    assert bad.size == 0, f"{what}: {len(bad)} outside tolerance, worst {np.max(err - tol):.3e} " \
+                          f"at {bad[:3].tolist()}"
+    return float(np.max(err / peak))
+
+
+def make(r, cin, cout, T, k, dt=F32, wscale=None, xscale=1.0):
+    wscale = wscale if wscale is not None else 1.0 / np.sqrt(cin * k)
+    x = O.to_storage(dt, (xscale * r.standard_normal((cin, T))).astype(np.float32))
+    w = (wscale * r.standard_normal((cout, cin, k))).astype(np.float16).view(np.uint16)
+    b = (0.05 * r.standard_normal(cout)).astype(np.float32)
+    cur = O.to_storage(dt, r.standard_normal((cout, T)).astype(np.float32))
+    return x, w, b, cur
+
+
+def run_gpu(dt, x, w, b, dil, epi, cur=None, round_x=False, slope=0.1, ld_pad=0, y_offset=0):
+    cin, T = x.shape
+    cout, _, k = w.shape
+    xd = dev(np.pad(x, ((0, 0), (0, ld_pad))), dt)[:, :T] if ld_pad else dev(x, dt)
+    conv = gsvk.Conv1d(dev(w, F16), devf(b) if b is not None else None, dil)
+    if b is None:
+        conv.b = None
+    yd = None
+    if epi != gsvk.CONV_EPI_RES:
+        buf = torch.empty(cout * (T + ld_pad) + y_offset, dtype=xd.dtype, device="cuda")
+        yd = buf[y_offset:].view(cout, T + ld_pad)[:, :T] if ld_pad else \
+            buf[y_offset:].view(cout, T)
+    cd = dev(cur, dt) if cur is not None else None
+    conv.forward(xd, yd, epi=epi, slope=slope, cur=cd, round_x=round_x)
+    torch.cuda.synchronize()
+    y = host(yd, dt) if yd is not None else None
+    c = host(cd, dt) if cd is not None else None
+    return y, c
+
+
+def check_case(dt, cin, cout, T, k, dil, epi=0, round_x=False, use_bias=True, seed=0, ld_pad=0,
+               y_offset=0, what=""):
+    r = rng(seed)
+    x, w, b, cur = make(r, cin, cout, T, k, dt)
+    b = b if use_bias else None
+    xo = O.to_storage(F32, O.to_f32(F16, O.to_storage(F16, x))) if round_x else x
+    ref0 = O.conv1d(dt, xo, w, b, dil)  # the plain convolution: the tolerance scale
+    want = O.conv1d(dt, xo, w, b, dil, epi=epi, slope=0.1, cur=cur if epi >= 2 else None)
+    y, c = run_gpu(dt, x, w, b, dil, epi, cur=cur if epi >= 2 else None, round_x=round_x,
+                   ld_pad=ld_pad, y_offset=y_offset)
+    tag = f"{what} dt={dt} {cin}->{cout} T={T} k={k} dil={dil} epi={epi} rx={round_x}"
+    if epi in (2, 3):
+        want_y, want_c = want
+        e = assert_conv_close(dt, c, want_c, ref0, tag + " cur")
+        if epi == 2:
+            e = max(e, assert_conv_close(dt, y, want_y, ref0, tag + " y"))
+    else:
+        e = assert_conv_close(dt, y, want, ref0, tag)
+    say(f"{tag}: max err / peak {e:.2e}")
+
+
+# The decoder's ResBlock convolutions (ResBlock1: k 3 / 7 / 11, conv1 dilations 1 / 3 / 5, conv2
+# dilation 1) at the stage channel counts 384 .. 24, with T cut to oracle-friendly lengths.
+STAGES = [(384, 600), (192, 1000), (96, 1500), (48, 2000), (24, 3000)]
+
+
+@pytest.mark.parametrize("C,T", STAGES)
+@pytest.mark.parametrize("k,dil", [(3, 1), (7, 3), (11, 5)])
+def test_resblock_conv1_fp32(C, T, k, dil):
+    check_case(F32, C, C, T, k, dil, epi=gsvk.CONV_EPI_LRELU, seed=C + k)
+
+
+@pytest.mark.parametrize("C,T", STAGES[1::2])
+@pytest.mark.parametrize("epi", [gsvk.CONV_EPI_BIAS, gsvk.CONV_EPI_RES_LRELU, gsvk.CONV_EPI_RES])
+def test_resblock_conv2_epilogues_fp32(C, T, epi):
+    check_case(F32, C, C, T, 7, 1, epi=epi, seed=C + 31 * epi)
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_fp16_storage(epi):
+    check_case(F16, 96, 96, 700, 11, 5, epi=epi, seed=40 + epi)
+
+
+@pytest.mark.parametrize("C,k,dil", [(192, 3, 1), (48, 11, 5)])
+def test_round_x_mode(C, k, dil):
+    """round_x = 1: x rounded to fp16 first (the reference's AMX panel packing)."""
+    check_case(F32, C, C, 500, k, dil, epi=0, round_x=True, seed=50 + C)
+
+
+@pytest.mark.parametrize("cin,cout,T,k,dil", [
+    (20, 5, 37, 3, 1),      # C_in and C_out below one chunk / fragment
+    (45, 33, 130, 5, 2),    # ragged chunks and fragments, odd T
+    (64, 17, 1, 7, 1),      # a single column: every tap but the centre reads padding
+    (32, 16, 3, 11, 5),     # the halo spans the whole sequence
+    (70, 100, 257, 4, 3),   # even k: pad (k - 1) dil / 2 rounds down
+    (50, 40, 300, 1, 1),    # k = 1: a matrix product
+    (40, 24, 400, 11, 20),  # halo 200 > 64: the wide-halo tile
+    (192, 768, 50, 7, 1),   # conv_pre (192 -> 768, k 7) at 50 frames
+])
+def test_shapes_and_edges(cin, cout, T, k, dil):
+    check_case(F32, cin, cout, T, k, dil, epi=0, seed=cin + cout + T)
+
+
+def test_conv_post_no_bias():
+    """conv_post: 24 -> 1 channel, k 7, no bias (conv1d.hpp:82-88)."""
+    check_case(F32, 24, 1, 5000, 7, 1, epi=0, use_bias=False, seed=60)
+
+
+@pytest.mark.parametrize("dt", [F32, F16])
+def test_strided_and_unaligned_rows(dt):
+    """x and y rows with ld > T (x, y) and a y base off the vector alignment (scalar stores)."""
+    check_case(dt, 48, 40, 301, 3, 1, epi=1, ld_pad=7, seed=70, what="ld")
+    check_case(dt, 48, 40, 300, 3, 1, epi=1, y_offset=1, seed=71, what="offset")
+
+
+def test_nonfinite_inputs():
+    r = rng(80)
+    cin, cout, T, k, dil = 40, 20, 200, 7, 3
+    x, w, b, _ = make(r, cin, cout, T, k)
+    x[3, 50] = np.inf
+    x[7, 120] = np.nan
+    x[12, 199] = -np.inf
+    want = O.conv1d(F32, x, w, b, dil)
+    y, _ = run_gpu(F32, x, w, b, dil, 0)
+    assert_conv_close(F32, y, want, want, "non-finite")
+
+
+def test_deterministic():
+    r = rng(90)
+    x, w, b, _ = make(r, 96, 96, 3000, 11)
+    y1, _ = run_gpu(F32, x, w, b, 5, 0)
+    y2, _ = run_gpu(F32, x, w, b, 5, 0)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+# Full decoder stage sizes (reference geometry, 500 frames), windowed oracle.
+FULL = [(384, 5000, 11, 5), (192, 40000, 7, 3), (96, 80000, 3, 1), (48, 160000, 11, 1),
+        (24, 320000, 11, 5)]
+
+
+@pytest.mark.parametrize("C,T,k,dil", FULL)
+def test_full_stage_windows(C, T, k, dil):
+    r = rng(100 + C)
+    x, w, b, cur = make(r, C, C, T, k)
+    halo = (k - 1) * dil
+    xd, cd = dev(x, F32), dev(cur, F32)
+    conv = gsvk.Conv1d(dev(w, F16), devf(b), dil)
+    yd = torch.empty(C, T, dtype=torch.float32, device="cuda")
+    conv.forward(xd, yd, epi=gsvk.CONV_EPI_RES_LRELU, slope=0.1, cur=cd)
+    torch.cuda.synchronize()
+    y, c = host(yd, F32), host(cd, F32)
+    width = 96
+    starts = [0, 250, T // 2 - 37, T - 300, T - width]
+    for a in starts:
+        bnd = a + width
+        w0, w1 = max(0, a - halo), min(T, bnd + halo)
+        ref0 = O.conv1d(F32, x[:, w0:w1], w, b, dil)[:, a - w0:bnd - w0]
+        wy, wc = O.conv1d(F32, x[:, w0:w1], w, b, dil, epi=2, slope=0.1, cur=cur[:, w0:w1])
+        assert_conv_close(F32, c[:, a:bnd], wc[:, a - w0:bnd - w0], ref0, f"cur[{a}:{bnd}]")
+        assert_conv_close(F32, y[:, a:bnd], wy[:, a - w0:bnd - w0], ref0, f"y[{a}:{bnd}]")
+    say(f"full stage C={C} T={T} k={k} dil={dil}: {len(starts)} windows ok")
