@@ -430,6 +430,9 @@ def sovits_decoder(torch, gsvk, dev):
 # ---- SoVITS ResBlock convolutions --------------------------------------------------------------------
 
 RES_KERNELS = (3, 7, 11)      # ResBlock1 kernel sizes (dec.hpp:55-76)
+UPS = {"reference_768": [(768, 10, 20), (384, 8, 16), (192, 2, 8), (96, 2, 2), (48, 2, 2)],
+       "literal_512": [(512, 10, 20), (256, 8, 16), (128, 2, 8), (64, 2, 2), (32, 2, 2)]}
+# (input channels, stride u, kernel k) of Generator.ups per stage (dec.hpp:55-76)
 RES_DILATIONS = (1, 3, 5)     # conv1 dilations; every conv2 has dilation 1
 PEAK_F16_TFLOPS = 2500.0      # MI355X dense fp16 matrix-core peak
 
@@ -449,13 +452,23 @@ def conv_us(torch, fn, iters=10):
 
 
 def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
-    """Per decoder stage (C, T): every distinct ResBlock convolution timed once (conv1: k x
-    dilation 1 / 3 / 5 with the LeakyReLU epilogue; conv2: k, dilation 1, with the residual +
-    LeakyReLU epilogue), and the stage's 18 convolutions (3 ResBlocks x 3 pairs) summed. fp32
+    """Per decoder stage (C, T): the upsampler (ConvT1d into the stage) and every distinct ResBlock
+    convolution timed once (conv1: k x dilation 1 / 3 / 5 with the LeakyReLU epilogue; conv2: k,
+    dilation 1, with the residual + LeakyReLU epilogue); the stage total is the upsampler plus its
+    18 convolutions (3 ResBlocks x 3 pairs). fp32
     activations multiplied exactly (the reference's sgemm path) and, as a second figure, rounded to
     fp16 (its AMX path). Algorithmic flops 2 C^2 k T per convolution."""
     stages, tot, tot_rx, flops_tot = [], 0.0, 0.0, 0.0
-    for C, T in DECODER_GEOMETRIES[geometry]:
+    for (C, T), (cin_up, u, k_up) in zip(DECODER_GEOMETRIES[geometry], UPS[geometry]):
+        # the stage's upsampler: ConvT1d cin_up -> C, T / u -> T frames
+        xu = torch.randn(cin_up, T // u, device=dev)
+        yu = torch.empty(C, T, device=dev)
+        up = gsvk.ConvT1d((torch.randn(cin_up, C, k_up, device=dev) / (cin_up * k_up / u) ** 0.5)
+                          .half(), torch.randn(C, device=dev) * 0.05, u)
+        up_us = conv_us(torch, lambda: up.forward(xu, yu))
+        up_us_rx = conv_us(torch, lambda: up.forward(xu, yu, round_x=True))
+        up_fl = 2.0 * cin_up * C * k_up * (T // u)
+        del xu, yu, up
         x = torch.randn(C, T, device=dev)
         y = torch.empty(C, T, device=dev)
         cur = torch.randn(C, T, device=dev)
@@ -476,17 +489,22 @@ def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
                 st += n * us
                 st_rx += n * us_rx
                 st_fl += n * fl
+        row["upsample"] = {"c_in": cin_up, "stride": u, "k": k_up, "us": round(up_us, 2),
+                           "us_round_x": round(up_us_rx, 2),
+                           "TFLOPs": round(up_fl / up_us / 1e6, 1),
+                           "out_GBps": round(C * T * 4 / up_us / 1e3, 1)}
+        st, st_rx, st_fl = st + up_us, st_rx + up_us_rx, st_fl + up_fl
         row.update({"stage_us": round(st, 1), "stage_us_round_x": round(st_rx, 1),
                     "stage_TFLOPs": round(st_fl / st / 1e6, 1)})
         stages.append(row)
         tot, tot_rx, flops_tot = tot + st, tot_rx + st_rx, flops_tot + st_fl
-        log(f"  conv stage {C}x{T}: {st:.1f} us (round_x {st_rx:.1f} us), "
-            f"{st_fl / st / 1e6:.0f} TFLOP/s")
+        log(f"  conv stage {C}x{T}: {st:.1f} us incl. upsampler {up_us:.1f} us (round_x "
+            f"{st_rx:.1f} us), {st_fl / st / 1e6:.0f} TFLOP/s")
         del x, y, cur, conv
     torch.cuda.empty_cache()
     ach = flops_tot / tot / 1e6
-    return {"geometry": geometry, "stages": stages, "resblock_conv_us_per_10s_audio": round(tot, 1),
-            "resblock_conv_us_per_10s_audio_round_x": round(tot_rx, 1),
+    return {"geometry": geometry, "stages": stages, "conv_us_per_10s_audio": round(tot, 1),
+            "conv_us_per_10s_audio_round_x": round(tot_rx, 1),
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_F16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(ach / PEAK_F16_TFLOPS, 4),
                          "flops": flops_tot,
@@ -825,7 +843,7 @@ def main():
         "kernels": kernels,
         "sovits_decoder": decoder,
         "t2s_whole_decode_step": full,
-        "sovits_resblock_conv": conv,
+        "sovits_conv": conv,
     }
     print(json.dumps(line), flush=True)
     step.close()

@@ -51,12 +51,52 @@ struct ConvArgs {
   const float* bias;
   void* cur;
   void* y;
-  long cin, cout, T, ldx, ldc, ldy;
+  long cin, cout, T, ldx, ldc, ldy;  // T: input columns
   int k, dil, pad, nch, opad;
   int epi;
   float slope;
   bool vec;
+  int up;     // 0: Conv1d; u: transposed convolution with stride u (phase r = blockIdx.z)
+  long Tout;  // transposed: output columns T u
+  int pad_t;  // transposed: (k - u) / 2
 };
+
+// What one workgroup computes. Conv1d: output column t reads x columns t - pad + kk dil over the
+// k taps. Transposed convolution, phase r (ConvT1d, conv1d.hpp:250-340; y[j u + d - pad_t] +=
+// W[:, :, d] x[:, j]): the outputs t_out = q u + r - pad_t take the taps d = r + m u < k with
+// x column q - m, i.e. kn = ceil((k - r) / u) taps in reverse order (packed so, slot kk = kn - 1 -
+// m) over x columns q - (kn - 1) + kk. Position t of the phase is q = qlo + t, written to column
+// obase + t ostr.
+struct Map {
+  int kn;       // taps
+  long nq;      // output positions
+  long xoff;    // x column of position 0, tap 0
+  long ostr;    // output column stride
+  long obase;   // output column of position 0
+  const uint16_t* wp;
+};
+
+__device__ __forceinline__ long ceil_div(long a, long b) { return a >= 0 ? (a + b - 1) / b : -((-a) / b); }
+__device__ __forceinline__ long floor_div(long a, long b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+
+__device__ __forceinline__ Map block_map(const ConvArgs& a) {
+  Map m;
+  if (!a.up) {
+    m.kn = a.k, m.nq = a.T, m.xoff = -a.pad, m.ostr = 1, m.obase = 0, m.wp = a.wp;
+    return m;
+  }
+  const int u = a.up, r = blockIdx.z;
+  m.kn = (a.k - r + u - 1) / u;
+  size_t taps_before = 0;
+  for (int r2 = 0; r2 < r; ++r2) taps_before += static_cast<size_t>((a.k - r2 + u - 1) / u);
+  m.wp = a.wp + taps_before * a.nch * a.opad * kChunk;
+  const long qlo = ceil_div(a.pad_t - r, u), qhi = floor_div(a.Tout - 1 + a.pad_t - r, u);
+  m.nq = qhi - qlo + 1;
+  m.xoff = qlo - (m.kn - 1);
+  m.ostr = u;
+  m.obase = qlo * u + r - a.pad_t;
+  return m;
+}
 
 template <int XM>
 constexpr int planes() { return XM == kXSplit ? 2 : 1; }
@@ -76,17 +116,38 @@ __global__ __launch_bounds__(256) void conv_pack(const uint16_t* __restrict__ w,
   }
 }
 
+// Transposed weights, torch layout w[i, o, d] (ConvT1d::load, conv1d.hpp:219-237), packed per
+// phase r = 0 .. u-1 one after another, each like conv_pack with kn_r = ceil((k - r) / u) taps:
+// slot kk holds tap d = r + (kn_r - 1 - kk) u.
+__global__ __launch_bounds__(256) void convt_pack(const uint16_t* __restrict__ w,
+                                                  uint16_t* __restrict__ wp, long cout, long cin,
+                                                  long k, long u, long nch, long opad, long total) {
+  for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<long>(gridDim.x) * blockDim.x) {
+    long rest = e, r = 0, kn = (k + u - 1) / u;
+    while (rest >= nch * kn * opad * kChunk) {  // at most u - 1 steps
+      rest -= nch * kn * opad * kChunk;
+      ++r;
+      kn = (k - r + u - 1) / u;
+    }
+    const long j = rest % kChunk, o = (rest / kChunk) % opad, s = rest / (kChunk * opad);
+    const long c = s / kn, kk = s % kn, i = c * kChunk + j, d = r + (kn - 1 - kk) * u;
+    wp[e] = (o < cout && i < cin) ? w[(i * cout + o) * k + d] : uint16_t(0);
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ float ld1(const void* p, size_t i) { return Store<DT>::load1(p, i); }
 
-// cur[o, t .. t+3] for the residual epilogues, read before any result is stored so that all
-// fragments' loads are in flight together: one vector load for a whole group inside T with aligned
-// rows, otherwise element loads at clamped columns (values past T are not used).
+// cur[o, t .. t+3] for the residual epilogues (positions t .. t+3 of the map), read before any
+// result is stored so that all fragments' loads are in flight together: one vector load for a whole
+// group of contiguous, aligned columns, otherwise element loads at clamped positions (values past
+// the end are not used).
 template <int DT>
-__device__ __forceinline__ f4v load_cur(const ConvArgs& a, long o, long t) {
-  const size_t row = static_cast<size_t>(min(o, a.cout - 1)) * a.ldc;
+__device__ __forceinline__ f4v load_cur(const ConvArgs& a, const Map& m, long o, long t) {
+  const size_t row = static_cast<size_t>(min(o, a.cout - 1)) * a.ldc + m.obase;
   f4v c;
-  if (a.vec && t + 4 <= a.T) {
+  if (a.vec && m.ostr == 1 && t + 4 <= m.nq) {
     if constexpr (DT == GSVK_F32) {
       c = *reinterpret_cast<const f4v*>(static_cast<const float*>(a.cur) + row + t);
     } else {
@@ -95,22 +156,22 @@ __device__ __forceinline__ f4v load_cur(const ConvArgs& a, long o, long t) {
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c[q] = ld1<DT>(a.cur, row + min(t + q, a.T - 1));
+    for (int q = 0; q < 4; ++q) c[q] = ld1<DT>(a.cur, row + min(t + q, m.nq - 1) * m.ostr);
   }
   return c;
 }
 
-// Four consecutive outputs t .. t+3 of row o: bias, epilogue, stores. Vector stores when the whole
-// group lies inside T and the rows are aligned.
+// Positions t .. t+3 of row o: bias, epilogue, stores. Vector stores when the four columns are
+// contiguous, inside the output and aligned.
 template <int DT>
-__device__ __forceinline__ void finish4(const ConvArgs& a, long o, long t, f4v s, float b,
-                                        f4v cur) {
+__device__ __forceinline__ void finish4(const ConvArgs& a, const Map& m, long o, long t, f4v s,
+                                        float b, f4v cur) {
   float v[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) v[q] = a.bias ? s[q] + b : s[q];
-  const size_t yo = static_cast<size_t>(o) * a.ldy + t;
-  const size_t co = static_cast<size_t>(o) * a.ldc + t;
-  const bool full = a.vec && t + 4 <= a.T;
+  const size_t yo = static_cast<size_t>(o) * a.ldy + m.obase + t * m.ostr;
+  const size_t co = static_cast<size_t>(o) * a.ldc + m.obase + t * m.ostr;
+  const bool full = a.vec && m.ostr == 1 && t + 4 <= m.nq;
   if (a.epi >= 2) {  // cur += conv (+ b); epi 2 also writes y = lrelu(cur)
     float c[4];
 #pragma unroll
@@ -124,7 +185,7 @@ __device__ __forceinline__ void finish4(const ConvArgs& a, long o, long t, f4v s
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (t + q < a.T) Store<DT>::store1(a.cur, co + q, c[q]);
+        if (t + q < m.nq) Store<DT>::store1(a.cur, co + q * m.ostr, c[q]);
     }
     if (a.epi == 3) return;
 #pragma unroll
@@ -142,7 +203,7 @@ __device__ __forceinline__ void finish4(const ConvArgs& a, long o, long t, f4v s
   } else {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (t + q < a.T) Store<DT>::store1(a.y, yo + q, v[q]);
+      if (t + q < m.nq) Store<DT>::store1(a.y, yo + q * m.ostr, v[q]);
   }
 }
 
@@ -161,10 +222,12 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   const int r16 = lane & 15, grp = lane >> 4;
   const long t0 = static_cast<long>(blockIdx.x) * TT;
   const long o0 = static_cast<long>(blockIdx.y) * (16 * NO);
+  const Map m = block_map(a);
+  if (t0 >= m.nq) return;  // a phase with fewer positions than the grid covers (whole workgroup)
 
   // ---- x chunk: global -> registers -> LDS ------------------------------------------------------
   // Wave g stages channel group g (channels 8 g .. 8 g + 7 of the chunk) over all TTH columns:
-  // lane l holds column tp = l + 64 u (global column t0 - pad + tp, clamped into [0, T)). The row
+  // lane l holds column tp = l + 64 u (x column t0 + xoff + tp, clamped into [0, T)). The row
   // is wave-uniform, so each load is a buffer load with the column as its 32-bit offset and the
   // row, clamped to the chunk's last row, as a scalar offset: every load reads inside x. Clamped
   // values are zeroed when staged (a zero pad, and no 0 * inf from channels past C_in).
@@ -175,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   int tcol[NI];
 #pragma unroll
   for (int u = 0; u < NI; ++u)
-    tcol[u] = static_cast<int>(min(max(t0 - a.pad + lane + kWave * u, 0l), a.T - 1)) * ESZ;
+    tcol[u] = static_cast<int>(min(max(t0 + m.xoff + lane + kWave * u, 0l), a.T - 1)) * ESZ;
   uint32_t raw[NI][8];  // bit patterns; converted when staged so the loads stay in flight
   auto xload = [&](int c) {
     const long ch0 = static_cast<long>(c) * kChunk;
@@ -200,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
       const int tp = lane + kWave * u;
-      const long t = t0 - a.pad + tp;
+      const long t = t0 + m.xoff + tp;
       const bool tok = t >= 0 && t < a.T;
       h8 hi, lo;
 #pragma unroll
@@ -226,18 +289,18 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   // a row holds kWRow halves (32 + 8 padding) so that the 16 rows of a fragment read fall on
   // distinct banks.
   _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][16 NO][kWRow]
-  const int ng = (a.k + kTapGroup - 1) / kTapGroup;
+  const int ng = (m.kn + kTapGroup - 1) / kTapGroup;
   const int Q = a.nch * ng;
   u32x4 wraw[NO];
   auto wload = [&](int q) {
-    const int c = q / ng, kk0 = (q - c * ng) * kTapGroup, nt = min(kTapGroup, a.k - kk0);
-    const size_t s0 = static_cast<size_t>(c) * a.k + kk0;
+    const int c = q / ng, kk0 = (q - c * ng) * kTapGroup, nt = min(kTapGroup, m.kn - kk0);
+    const size_t s0 = static_cast<size_t>(c) * m.kn + kk0;
 #pragma unroll
     for (int u = 0; u < NO; ++u) {
       const int it = tid + kThreads * u;
       const int tap = it / (64 * NO), rem = it - tap * 64 * NO;
       const size_t row = (s0 + min(tap, nt - 1)) * a.opad + o0 + (rem >> 2);
-      wraw[u] = ld16<false>(a.wp + row * kChunk + (rem & 3) * 8);
+      wraw[u] = ld16<false>(m.wp + row * kChunk + (rem & 3) * 8);
     }
   };
   auto wstage = [&]() {
@@ -289,10 +352,11 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   // Group g of chunk c: refill LDS from the registers loaded one group earlier (x only at g = 0),
   // then load ahead: the next group's weights first, then, at g = 0, the next chunk's x. Issued in
   // that order, each weight load can be waited for without waiting for the x loads, which get the
-  // whole chunk to arrive. The last group reloads in-bounds data that is not used. The groups of a chunk are laid out in straight-line code (at most three
-  // for k <= 12; further groups loop) so the compiler can count the loads in flight exactly.
+  // whole chunk to arrive. The last group reloads in-bounds data that is not used. The groups of
+  // a chunk are laid out in straight-line code (at most three for k <= 12; further groups loop) so
+  // the compiler can count the loads in flight exactly.
   auto group = [&](int c, int g) {
-    const int kk0 = g * kTapGroup, nt = min(kTapGroup, a.k - kk0);
+    const int kk0 = g * kTapGroup, nt = min(kTapGroup, m.kn - kk0);
     if (c > 0 || g > 0) __syncthreads();  // every wave is done with the previous group
     if (g == 0) stage(c);
     wstage();
@@ -323,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
     for (int n = 0; n < NO; ++n)
 #pragma unroll
       for (int i = 0; i < NT; ++i)
-        cur[i][n] = load_cur<DT>(a, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
+        cur[i][n] = load_cur<DT>(a, m, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
   }
 #pragma unroll
   for (int n = 0; n < NO; ++n) {
@@ -332,7 +396,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
       const long t = t0 + wave * 16 * NT + 16 * i + 4 * grp;
-      if (t < a.T) finish4<DT>(a, o, t, acc[i][n], bias[n], cur[i][n]);
+      if (t < m.nq) finish4<DT>(a, m, o, t, acc[i][n], bias[n], cur[i][n]);
     }
   }
 }
@@ -353,9 +417,12 @@ int launch_tiles(const ConvArgs& a, hipStream_t st) {
                                                   static_cast<int>(lds)) == hipSuccess;
     if (!opted) return GSVK_E_HIP;
   }
-  const long gx = (a.T + kWaves * 16 * NT - 1) / (kWaves * 16 * NT);
+  const long npos = a.up ? a.T + 1 : a.T;  // a phase of a transposed convolution: <= T + 1
+  const long gx = (npos + kWaves * 16 * NT - 1) / (kWaves * 16 * NT);
   const long gy = (a.cout + 16 * NO - 1) / (16 * NO);
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
+  hipLaunchKernelGGL(kern,
+                     dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy),
+                          static_cast<unsigned>(a.up ? a.up : 1)),
                      dim3(kThreads), lds, st, a);
   return launch_status();
 }
@@ -384,9 +451,9 @@ int launch_plan(const ConvArgs& a, hipStream_t st) {
       break;
     }
   }
-  const long tiles64 = (a.T + 255) / 256 * ((ofr + no - 1) / no);
+  const long tiles64 = (a.T + 255) / 256 * ((ofr + no - 1) / no) * (a.up ? a.up : 1);
   const bool nt2 = tiles64 < 512;
-  const int halo = (a.k - 1) * a.dil;
+  const int halo = a.up ? (a.k + a.up - 1) / a.up - 1 : (a.k - 1) * a.dil;
   if (halo <= 64)
     return nt2 ? launch_no<XM, 2, 64>(a, no, st) : launch_no<XM, 4, 64>(a, no, st);
   return launch_no<XM, 1, kMaxHalo>(a, no, st);
@@ -459,6 +526,82 @@ extern "C" int gsvk_conv1d(int dtype, int round_x, const void* x, size_t ldx,
              static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad), epi, slope, false};
   const size_t va = esz * 4;  // one vector: four elements
   a.vec = T >= 4 && (!has_y || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % va == 0)) &&
+          (!has_res || (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(cur) % va == 0));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == GSVK_F16) return launch_plan<kXF16>(a, st);
+  return round_x ? launch_plan<kXRound>(a, st) : launch_plan<kXSplit>(a, st);
+}
+
+extern "C" size_t gsvk_convt1d_packed_elems(size_t c_out, size_t c_in, size_t k, size_t stride) {
+  if (!c_out || !c_in || !k || !stride || k < stride) return 0;
+  // the phases' tap counts ceil((k - r) / u) add up to k
+  return (c_in + kChunk - 1) / kChunk * k * ((c_out + kOPad - 1) / kOPad * kOPad) * kChunk;
+}
+
+extern "C" int gsvk_convt1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k,
+                                 size_t stride, uint16_t* w_packed, size_t packed_elems,
+                                 void* stream) {
+  if (!w || !w_packed) return GSVK_E_NULL;
+  if (!c_out || !c_in || !k || !stride || c_out > (1ul << 24) || c_in > (1ul << 24) || k > 4096 ||
+      stride > 4096)
+    return GSVK_E_SIZE;
+  if (k < stride) return GSVK_E_ARG;
+  const size_t total = gsvk_convt1d_packed_elems(c_out, c_in, k, stride);
+  if (packed_elems < total) return GSVK_E_SIZE;
+  if (overlaps(w, c_out * c_in * k * 2, w_packed, total * 2)) return GSVK_E_ALIAS;
+  const long opad = static_cast<long>((c_out + kOPad - 1) / kOPad * kOPad);
+  const long nch = static_cast<long>((c_in + kChunk - 1) / kChunk);
+  const long blocks = std::min<long>((static_cast<long>(total) + 255) / 256, 16384);
+  hipLaunchKernelGGL(convt_pack, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), w, w_packed, static_cast<long>(c_out),
+                     static_cast<long>(c_in), static_cast<long>(k), static_cast<long>(stride), nch,
+                     opad, static_cast<long>(total));
+  return launch_status();
+}
+
+extern "C" int gsvk_convt1d(int dtype, int round_x, const void* x, size_t ldx,
+                            const uint16_t* w_packed, const float* bias, int epi, float slope,
+                            void* cur, size_t ldc, void* y, size_t ldy, size_t c_in, size_t c_out,
+                            size_t T, size_t k, size_t stride, void* stream) {
+  if (dtype != GSVK_F32 && dtype != GSVK_F16) return GSVK_E_DTYPE;
+  if (epi < GSVK_CONV_EPI_BIAS || epi > GSVK_CONV_EPI_RES) return GSVK_E_DTYPE;
+  const bool has_res = epi == GSVK_CONV_EPI_RES_LRELU || epi == GSVK_CONV_EPI_RES;
+  const bool has_y = epi != GSVK_CONV_EPI_RES;
+  if (!x || !w_packed || (has_y && !y) || (has_res && !cur)) return GSVK_E_NULL;
+  if (!c_in || !c_out || !T || !k || !stride || ldx < T) return GSVK_E_SIZE;
+  if (c_in > (1ul << 24) || c_out > (1ul << 24) || k > 4096 || stride > 4096 ||
+      T > (1ul << 31) / stride - 512 || ldx > (1ul << 40) || ldy > (1ul << 40) ||
+      ldc > (1ul << 40))
+    return GSVK_E_SIZE;
+  const size_t Tout = T * stride;
+  if ((has_y && ldy < Tout) || (has_res && ldc < Tout)) return GSVK_E_SIZE;
+  // pad = (k - u) / 2 needs k >= u (ConvT1d, conv1d.hpp:262); each phase's taps share one LDS tile
+  if (k < stride || (k + stride - 1) / stride - 1 > 64) return GSVK_E_ARG;
+  if (kChunk * ldx * dtype_size(dtype) >= (1ul << 31)) return GSVK_E_SIZE;
+  if (!aligned16(w_packed)) return GSVK_E_ARG;
+  const size_t esz = dtype_size(dtype);
+  const size_t xb = span_bytes(c_in, T, ldx, esz);
+  const size_t wb = gsvk_convt1d_packed_elems(c_out, c_in, k, stride) * 2;
+  const size_t bb = bias ? c_out * 4 : 0;
+  const void* yp = has_y ? y : nullptr;
+  const void* cp = has_res ? cur : nullptr;
+  const size_t yb = has_y ? span_bytes(c_out, Tout, ldy, esz) : 0;
+  const size_t cb = has_res ? span_bytes(c_out, Tout, ldc, esz) : 0;
+  if (overlaps(yp, yb, x, xb) || overlaps(yp, yb, w_packed, wb) || overlaps(yp, yb, bias, bb) ||
+      overlaps(yp, yb, cp, cb) || overlaps(cp, cb, x, xb) || overlaps(cp, cb, w_packed, wb) ||
+      overlaps(cp, cb, bias, bb))
+    return GSVK_E_ALIAS;
+
+  ConvArgs a{x, w_packed, bias, cur, y, static_cast<long>(c_in), static_cast<long>(c_out),
+             static_cast<long>(T), static_cast<long>(ldx), static_cast<long>(has_res ? ldc : 0),
+             static_cast<long>(has_y ? ldy : 0), static_cast<int>(k), 1, 0,
+             static_cast<int>((c_in + kChunk - 1) / kChunk),
+             static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad), epi, slope, false,
+             static_cast<int>(stride), static_cast<long>(Tout),
+             static_cast<int>((k - stride) / 2)};
+  const size_t va = esz * 4;
+  a.vec = stride == 1 && T >= 4 &&
+          (!has_y || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % va == 0)) &&
           (!has_res || (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(cur) % va == 0));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GSVK_F16) return launch_plan<kXF16>(a, st);

@@ -34,6 +34,10 @@ SIGNATURES = {
                          _sz, _vp]),
     "gsvk_conv1d_packed_elems": (_sz, [_sz, _sz, _sz]),
     "gsvk_conv1d_pack": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
+    "gsvk_convt1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
+                          _sz, _vp]),
+    "gsvk_convt1d_packed_elems": (_sz, [_sz, _sz, _sz, _sz]),
+    "gsvk_convt1d_pack": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp]),
     "gsvk_groupnorm_gelu": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _d, _i, _vp]),
     "gsvk_leaky_relu": (_i, [_i, _vp, _vp, _sz, _f, _vp]),
     "gsvk_resblock_add_lrelu": (_i, [_i, _vp, _vp, _vp, _sz, _f, _vp]),
@@ -198,6 +202,54 @@ class Conv1d:
             y = torch.empty(self.out_c, x.shape[1], dtype=x.dtype, device=x.device)
         conv1d(x, self.wp, self.out_c, self.k, y, self.b, self.dilation, epi, slope, cur, round_x,
                stream)
+        return y
+
+
+def convt1d_pack(w, stride, stream=None):
+    """Pack a [c_in, c_out, k] fp16 ConvTranspose1d filter bank; returns the packed tensor."""
+    import torch
+    c_in, c_out, k = w.shape
+    assert w.dtype in (torch.float16, torch.int16) and w.is_contiguous()
+    n = lib().gsvk_convt1d_packed_elems(c_out, c_in, k, stride)
+    wp = torch.empty(max(n, 1), dtype=torch.int16, device=w.device)
+    _check("gsvk_convt1d_pack", lib().gsvk_convt1d_pack(_ptr(w), c_out, c_in, k, stride, _ptr(wp),
+                                                        n, _stream(stream)))
+    return wp
+
+
+def convt1d(x, wp, c_out, k, stride, y=None, bias=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None,
+            round_x=False, stream=None, check=True):
+    """SoVITS ConvTranspose1d on x [c_in, T] with packed weights (convt1d_pack) and a fused
+    epilogue; y / cur [c_out, T * stride]."""
+    c_in, T, ldx = _rows(x)
+    ldy = _rows(y)[2] if y is not None else 0
+    ldc = _rows(cur)[2] if cur is not None else 0
+    rc = lib().gsvk_convt1d(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(wp), _ptr(bias), epi,
+                            slope, _ptr(cur), ldc, _ptr(y), ldy, c_in, c_out, T, k, stride,
+                            _stream(stream))
+    return _check("gsvk_convt1d", rc) if check else rc
+
+
+class ConvT1d:
+    """Mirror of the reference's sovits::ConvT1d (conv1d.hpp:205-360): out_c, in_c, k, stride_u,
+    the torch-layout [in, out, k] fp16 weights packed once per phase, fp32 bias (zeros when
+    absent), forward(x, y) with y of length T * stride_u."""
+
+    def __init__(self, w16, bias, stride, stream=None):
+        import torch
+        self.in_c, self.out_c, self.k = (int(d) for d in w16.shape)
+        self.stride_u = int(stride)
+        self.wp = convt1d_pack(w16.contiguous(), self.stride_u, stream)
+        self.b = bias if bias is not None else torch.zeros(self.out_c, dtype=torch.float32,
+                                                           device=w16.device)
+
+    def forward(self, x, y=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None, round_x=False,
+                stream=None):
+        import torch
+        if y is None and epi != CONV_EPI_RES:
+            y = torch.empty(self.out_c, x.shape[1] * self.stride_u, dtype=x.dtype, device=x.device)
+        convt1d(x, self.wp, self.out_c, self.k, self.stride_u, y, self.b, epi, slope, cur, round_x,
+                stream)
         return y
 
 

@@ -188,6 +188,28 @@ int gsvk_conv1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k, uin
                      size_t packed_elems, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * SoVITS ConvTranspose1d (the upsampler), stride u, pad_t = (k - u) / 2, output length T * u:
+ *   v[o, t] = bias[o] + sum over (j, d) with j*u + d - pad_t = t of sum_i w[i, o, d] * x[i, j]
+ *   followed by the same epilogues as gsvk_conv1d (epi, slope, cur), on [c_out, T * u] outputs.
+ * Replaces ConvT1d::forward (src/sovits/conv1d.hpp:250-340: one sgemm per tap d, scatter-add into
+ * y at j*u + d - pad, then the bias), computed here per output phase r = (t + pad_t) mod u as a
+ * short convolution over x (ceil((k - r) / u) taps), all phases in one launch.
+ * Layout: x [c_in, T] (stride ldx >= T); y / cur [c_out, T * u] (strides >= T * u); bias fp32 or
+ * NULL; w_packed from gsvk_convt1d_pack. Requires k >= u (the reference's pad formula) and
+ * ceil(k / u) <= 65. Same dtype / round_x / aliasing rules and tolerance as gsvk_conv1d.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_convt1d(int dtype, int round_x, const void* x, size_t ldx, const uint16_t* w_packed,
+                 const float* bias, int epi, float slope, void* cur, size_t ldc, void* y,
+                 size_t ldy, size_t c_in, size_t c_out, size_t T, size_t k, size_t stride,
+                 void* stream);
+/* Elements of the packed transposed filter bank (0 for a zero size or k < stride). Host only. */
+size_t gsvk_convt1d_packed_elems(size_t c_out, size_t c_in, size_t k, size_t stride);
+/* Pack a torch-layout [c_in, c_out, k] fp16 ConvTranspose1d filter bank (the .gsv layout;
+ * ConvT1d::load, conv1d.hpp:219-237, re-slices it per tap the same way) for gsvk_convt1d. */
+int gsvk_convt1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k, size_t stride,
+                      uint16_t* w_packed, size_t packed_elems, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * GroupNorm with one group per channel, optionally followed by GELU(erf).
  *   mean_c, var_c over the T frames of channel c (biased); y = (x - mean)*rstd*gamma[c] + beta[c];
  *   y = gelu_erf(y) when apply_gelu != 0.

@@ -357,22 +357,44 @@ int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const 
  * The GEMM sums over K in order with one rounding per step (fmaf); Accelerate's sgemm order is not
  * published, so parity with it is tolerance-based in any case.
  * --------------------------------------------------------------------------------------------- */
+/* The epilogue of one fp32 output row (n columns) of output channel o, per epi (see above). */
+static int conv_epilogue(int dtype, float* row, size_t o, int epi, float slope, void* cur, size_t ldc,
+                         void* y, size_t ldy, size_t n) {
+  if (epi == 1) {
+    for (size_t t = 0; t < n; ++t) row[t] = leaky(row[t], slope);
+    oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
+  } else if (epi == 2 || epi == 3) {
+    float* c = (float*)malloc(n * 4);
+    if (!c) return -1;
+    oracle_to_f32(dtype, row_ptr(cur, dtype, o * ldc), c, n);
+    for (size_t t = 0; t < n; ++t) c[t] = c[t] + row[t];
+    oracle_from_f32(dtype, c, row_ptr_w(cur, dtype, o * ldc), n);
+    if (epi == 2) {
+      for (size_t t = 0; t < n; ++t) row[t] = leaky(c[t], slope);
+      oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
+    }
+    free(c);
+  } else {
+    oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
+  }
+  return 0;
+}
+
 int oracle_conv1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const float* bias, int epi,
                   float slope, void* cur, size_t ldc, void* y, size_t ldy, size_t cin, size_t cout,
                   size_t T, size_t k, size_t dil) {
   float* xr = (float*)malloc(cin * T * 4);
   float* wf = (float*)malloc(cout * cin * k * 4);
   float* row = (float*)malloc(T * 4);
+  int rc = 0;
   if (!xr || !wf || !row) {
-    free(xr);
-    free(wf);
-    free(row);
-    return -1;
+    rc = -1;
+    goto done;
   }
   for (size_t i = 0; i < cin; ++i) oracle_to_f32(dtype, row_ptr(x, dtype, i * ldx), xr + i * T, T);
   for (size_t e = 0; e < cout * cin * k; ++e) wf[e] = oracle_h2f(w[e]);
   const long pad = (long)((k - 1) * dil) / 2;
-  for (size_t o = 0; o < cout; ++o) {
+  for (size_t o = 0; o < cout && rc == 0; ++o) {
     for (size_t t = 0; t < T; ++t) {
       float s = 0.f;
       for (size_t i = 0; i < cin; ++i)
@@ -383,33 +405,56 @@ int oracle_conv1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const
         }
       row[t] = bias ? s + bias[o] : s;
     }
-    if (epi == 1) {
-      for (size_t t = 0; t < T; ++t) row[t] = leaky(row[t], slope);
-      oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), T);
-    } else if (epi == 2 || epi == 3) {
-      float* c = (float*)malloc(T * 4);
-      if (!c) {
-        free(xr);
-        free(wf);
-        free(row);
-        return -1;
-      }
-      oracle_to_f32(dtype, row_ptr(cur, dtype, o * ldc), c, T);
-      for (size_t t = 0; t < T; ++t) c[t] = c[t] + row[t];
-      oracle_from_f32(dtype, c, row_ptr_w(cur, dtype, o * ldc), T);
-      if (epi == 2) {
-        for (size_t t = 0; t < T; ++t) row[t] = leaky(c[t], slope);
-        oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), T);
-      }
-      free(c);
-    } else {
-      oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), T);
-    }
+    rc = conv_epilogue(dtype, row, o, epi, slope, cur, ldc, y, ldy, T);
   }
+done:
   free(xr);
   free(wf);
   free(row);
-  return 0;
+  return rc;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * SoVITS ConvTranspose1d (next-tier row 4): ConvT1d::forward's fallback path (conv1d.hpp:250-340).
+ * Weights w[i][o][d] (torch layout, upcast from fp16), stride u, pad = (k - u) / 2, T_out = T u:
+ *   y = 0; for d = 0 .. k-1: tmp[o][j] = sum_i W[i][o][d] x[i][j] (one sgemm per tap, the sum in
+ *   order with fmaf), then y[o][j u + d - pad] += tmp[o][j] where inside [0, T_out) (scatter_raw);
+ *   finally y += b, and the epilogue of Conv1d (epi 0 .. 3) on the T_out-column rows.
+ * --------------------------------------------------------------------------------------------- */
+int oracle_convt1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const float* bias,
+                   int epi, float slope, void* cur, size_t ldc, void* y, size_t ldy, size_t cin,
+                   size_t cout, size_t T, size_t k, size_t u) {
+  if (k < u || u == 0) return -2;
+  const size_t Tout = T * u;
+  const long pad = (long)(k - u) / 2;
+  float* xr = (float*)malloc(cin * T * 4);
+  float* wf = (float*)malloc(cin * cout * k * 4);
+  float* acc = (float*)calloc(Tout, 4);
+  int rc = 0;
+  if (!xr || !wf || !acc) {
+    rc = -1;
+    goto done;
+  }
+  for (size_t i = 0; i < cin; ++i) oracle_to_f32(dtype, row_ptr(x, dtype, i * ldx), xr + i * T, T);
+  for (size_t e = 0; e < cin * cout * k; ++e) wf[e] = oracle_h2f(w[e]);
+  for (size_t o = 0; o < cout && rc == 0; ++o) {
+    for (size_t t = 0; t < Tout; ++t) acc[t] = 0.f;
+    for (size_t d = 0; d < k; ++d)
+      for (size_t j = 0; j < T; ++j) {
+        float s = 0.f;
+        for (size_t i = 0; i < cin; ++i) s = fmaf(wf[(i * cout + o) * k + d], xr[i * T + j], s);
+        const long pos = (long)(j * u + d) - pad;
+        if (pos >= 0 && pos < (long)Tout) acc[pos] += s;
+      }
+    if (bias)
+      for (size_t t = 0; t < Tout; ++t) acc[t] += bias[o];
+    rc = conv_epilogue(dtype, acc, o, epi, slope, cur, ldc, y, ldy, Tout);
+  }
+done:
+  free(xr);
+  free(wf);
+  free(acc);
+  return rc;
 }
 
 /* ---------------------------------------------------------------------------------------------

@@ -78,6 +78,12 @@ int oracle_conv1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const
                   float slope, void* cur, size_t ldc, void* y, size_t ldy, size_t cin, size_t cout,
                   size_t T, size_t k, size_t dil);
 
+/* SoVITS ConvTranspose1d: w [cin][cout][k] fp16 bits, stride u, pad (k-u)/2, output [cout][T u]
+ * (rows ldy / ldc), the reference's per-tap GEMM + scatter order, bias last, then epi as conv1d. */
+int oracle_convt1d(int dtype, const void* x, size_t ldx, const uint16_t* w, const float* bias,
+                   int epi, float slope, void* cur, size_t ldc, void* y, size_t ldy, size_t cin,
+                   size_t cout, size_t T, size_t k, size_t u);
+
 /* Decode attention: KV append at pos[b] and single-query SDPA over keys 0..pos[b] per head
  * (t2s_engine.cpp:1051-1087). kv_dtype 0 = fp32 cache, 1 = fp16 cache. Caches [B][max_len][H*HD];
  * qkv rows [q | k | v] fp32 with stride ldq; out [B][H*HD] fp32 with stride ldo (NaN rows for a

@@ -39,6 +39,8 @@ _SIG = {
                               _sz]),
     "oracle_decode_attention": (_i, [_i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz]),
     "oracle_softmax": (None, [_vp, _vp, _sz]),
+    "oracle_convt1d": (_i, [_i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
+                            _sz]),
     "oracle_conv1d": (_i, [_i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
                            _sz]),
     "oracle_pe_row": (None, [_vp, _sz, _sz]),
@@ -202,6 +204,21 @@ def conv1d(dt, x, w, bias=None, dil=1, epi=0, slope=0.1, cur=None):
     c = None if cur is None else np.ascontiguousarray(cur).copy()
     rc = lib().oracle_conv1d(dt, _p(x), T, _p(w), _p(bias), epi, slope, _p(c), T, _p(y), T, cin,
                              cout, T, k, dil)
+    assert rc == 0
+    return (y, c) if epi in (2, 3) else y
+
+
+def convt1d(dt, x, w, u, bias=None, epi=0, slope=0.1, cur=None):
+    """SoVITS ConvTranspose1d + epilogue. x [cin, T] storage of dt; w [cin, cout, k] uint16 fp16
+    bits (torch layout); stride u. Returns y [cout, T u] (and the updated cur for epi 2 / 3)."""
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w).view(np.uint16)
+    cin, cout, k = w.shape
+    T = x.shape[1]
+    y = np.zeros((cout, T * u), dtype=storage_dtype(dt))
+    c = None if cur is None else np.ascontiguousarray(cur).copy()
+    rc = lib().oracle_convt1d(dt, _p(x), T, _p(w), _p(bias), epi, slope, _p(c), T * u, _p(y),
+                              T * u, cin, cout, T, k, u)
     assert rc == 0
     return (y, c) if epi in (2, 3) else y
 

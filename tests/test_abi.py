@@ -177,6 +177,30 @@ def test_conv_validation(gsvk_lib):
     assert p(A, 8, 16, 3, A + 64, n, None) == gsvk.E_ALIAS
 
 
+def test_convt_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_convt1d
+    assert gsvk_lib.gsvk_convt1d_packed_elems(8, 16, 16, 8) == 1 * 16 * 64 * 32  # taps add up to k
+    assert gsvk_lib.gsvk_convt1d_packed_elems(8, 16, 4, 8) == 0                  # k < stride
+
+    def call(dt=0, x=A, ldx=100, w=B, epi=0, cur=None, ldc=0, y=C, ldy=800, cin=16, cout=8, T=100,
+             k=16, u=8):
+        return f(dt, 0, x, ldx, w, None, epi, 0.1, cur, ldc, y, ldy, cin, cout, T, k, u, None)
+
+    assert call(dt=2) == gsvk.E_DTYPE
+    assert call(x=None) == gsvk.E_NULL
+    assert call(u=0) == gsvk.E_SIZE
+    assert call(ldy=799) == gsvk.E_SIZE          # output rows hold T * stride columns
+    assert call(k=4) == gsvk.E_ARG               # k < stride: the reference's pad is undefined
+    assert call(k=200, u=2) == gsvk.E_ARG        # 100 taps per phase do not fit one tile
+    assert call(w=B + 8) == gsvk.E_ARG
+    assert call(y=A + 64) == gsvk.E_ALIAS
+    p = gsvk_lib.gsvk_convt1d_pack
+    n = gsvk_lib.gsvk_convt1d_packed_elems(8, 16, 16, 8)
+    assert p(A, 8, 16, 16, 8, B, n - 1, None) == gsvk.E_SIZE
+    assert p(A, 8, 16, 4, 8, B, n, None) == gsvk.E_ARG
+    assert p(A, 8, 16, 16, 8, A + 64, n, None) == gsvk.E_ALIAS
+
+
 def test_embed_validation(gsvk_lib):
     f = gsvk_lib.gsvk_embed_pe
     args = dict(out=0, tab=1, it=0, table=A, vocab=10, ids=B, pos=None, pos0=0, pe=C, max_pos=4,

@@ -205,3 +205,99 @@ def test_full_stage_windows(C, T, k, dil):
         assert_conv_close(F32, c[:, a:bnd], wc[:, a - w0:bnd - w0], ref0, f"cur[{a}:{bnd}]")
         assert_conv_close(F32, y[:, a:bnd], wy[:, a - w0:bnd - w0], ref0, f"y[{a}:{bnd}]")
     say(f"full stage C={C} T={T} k={k} dil={dil}: {len(starts)} windows ok")
+
+
+# ---- ConvTranspose1d (the upsampler) ------------------------------------------------------------
+
+def run_gpu_t(dt, x, w, b, u, epi=0, cur=None, round_x=False, ld_pad=0):
+    cin, T = x.shape
+    _, cout, k = w.shape
+    xd = dev(x, dt)
+    conv = gsvk.ConvT1d(dev(w, F16), devf(b) if b is not None else None, u)
+    if b is None:
+        conv.b = None
+    yd = None
+    if epi != gsvk.CONV_EPI_RES:
+        buf = torch.empty(cout, T * u + ld_pad, dtype=xd.dtype, device="cuda")
+        yd = buf[:, :T * u]
+    cd = dev(cur, dt) if cur is not None else None
+    conv.forward(xd, yd, epi=epi, slope=0.1, cur=cd, round_x=round_x)
+    torch.cuda.synchronize()
+    return (host(yd, dt) if yd is not None else None), (host(cd, dt) if cd is not None else None)
+
+
+def check_t(dt, cin, cout, T, k, u, epi=0, round_x=False, use_bias=True, seed=0, ld_pad=0):
+    r = rng(seed)
+    x = O.to_storage(dt, r.standard_normal((cin, T)).astype(np.float32))
+    w = (r.standard_normal((cin, cout, k)) / np.sqrt(cin * k / u)).astype(np.float16).view(np.uint16)
+    b = (0.05 * r.standard_normal(cout)).astype(np.float32) if use_bias else None
+    cur = O.to_storage(dt, r.standard_normal((cout, T * u)).astype(np.float32)) if epi >= 2 else None
+    xo = O.to_storage(F32, O.to_f32(F16, O.to_storage(F16, x))) if round_x else x
+    ref0 = O.convt1d(dt, xo, w, u, b)
+    want = O.convt1d(dt, xo, w, u, b, epi=epi, slope=0.1, cur=cur)
+    y, c = run_gpu_t(dt, x, w, b, u, epi=epi, cur=cur, round_x=round_x, ld_pad=ld_pad)
+    tag = f"convT dt={dt} {cin}->{cout} T={T} k={k} u={u} epi={epi} rx={round_x}"
+    if epi in (2, 3):
+        e = assert_conv_close(dt, c, want[1], ref0, tag + " cur")
+        if epi == 2:
+            e = max(e, assert_conv_close(dt, y, want[0], ref0, tag + " y"))
+    else:
+        e = assert_conv_close(dt, y, want, ref0, tag)
+    say(f"{tag}: max err / peak {e:.2e}")
+
+
+# Generator.ups (dec.hpp:55-76): 768 -> 384 (k 20, u 10), 384 -> 192 (16, 8), 192 -> 96 (8, 2),
+# 96 -> 48 (2, 2), 48 -> 24 (2, 2), with T cut to oracle-friendly lengths.
+UPS = [(768, 384, 40, 20, 10), (384, 192, 150, 16, 8), (192, 96, 400, 8, 2), (96, 48, 900, 2, 2),
+       (48, 24, 2000, 2, 2)]
+
+
+@pytest.mark.parametrize("cin,cout,T,k,u", UPS)
+def test_upsample_stages_fp32(cin, cout, T, k, u):
+    check_t(F32, cin, cout, T, k, u, seed=cin + k)
+
+
+@pytest.mark.parametrize("cin,cout,T,k,u", [
+    (20, 5, 7, 5, 2),     # odd k - u: pad rounds down, phases of unequal length
+    (33, 17, 1, 3, 3),    # k == u (no overlap), one input column
+    (40, 70, 2, 7, 3),    # ragged taps per phase (3, 2, 2), two input columns
+    (64, 16, 37, 16, 8),
+    (45, 33, 60, 4, 1),   # stride 1: an ordinary convolution with flipped taps
+])
+def test_upsample_edges(cin, cout, T, k, u):
+    check_t(F32, cin, cout, T, k, u, seed=cin * 3 + T)
+
+
+@pytest.mark.parametrize("epi", [1, 2, 3])
+def test_upsample_epilogues(epi):
+    check_t(F32, 96, 48, 300, 8, 2, epi=epi, seed=200 + epi)
+
+
+def test_upsample_fp16_round_x_and_strided():
+    check_t(F16, 96, 48, 300, 8, 2, seed=210)
+    check_t(F32, 96, 48, 300, 16, 8, round_x=True, seed=211)
+    check_t(F32, 48, 24, 301, 2, 2, use_bias=False, ld_pad=5, seed=212)
+
+
+FULL_UPS = [(768, 384, 500, 20, 10), (384, 192, 5000, 16, 8), (192, 96, 40000, 8, 2),
+            (96, 48, 80000, 2, 2), (48, 24, 160000, 2, 2)]
+
+
+@pytest.mark.parametrize("cin,cout,T,k,u", FULL_UPS)
+def test_upsample_full_stage_windows(cin, cout, T, k, u):
+    r = rng(300 + cin)
+    x = r.standard_normal((cin, T)).astype(np.float32)
+    w = (r.standard_normal((cin, cout, k)) / np.sqrt(cin * k / u)).astype(np.float16).view(np.uint16)
+    b = (0.05 * r.standard_normal(cout)).astype(np.float32)
+    y, _ = run_gpu_t(F32, x, w, b, u)
+    M = -(-k // u) + 1  # input columns that reach past a window edge
+    width = 24
+    for ja in [0, T // 3, T - width]:
+        jb = ja + width
+        wa, wb = max(0, ja - M), min(T, jb + M)
+        win = O.convt1d(F32, x[:, wa:wb], w, u, b)
+        ga = 0 if ja == 0 else ja * u        # complete output columns of the window
+        gb = T * u if jb == T else jb * u
+        got, want = y[:, ga:gb], win[:, ga - wa * u:gb - wa * u]
+        assert_conv_close(F32, got, want, want, f"convT full {cin}->{cout} T={T} cols [{ga}, {gb})")
+    say(f"convT full stage {cin}->{cout} T={T} k={k} u={u}: windows ok")

@@ -125,3 +125,84 @@ def test_conv_f16_storage_rounds_each_output_once():
     c32 = (cur32 + y32).astype(np.float32)
     y2, c2 = O.conv1d(F16, x16, w, b, epi=2, slope=0.1, cur=cur16)
     assert np.array_equal(c2, O.to_storage(F16, c32)) and np.array_equal(y2, O.to_storage(F16, lr(c32)))
+
+
+# ---- ConvTranspose1d ------------------------------------------------------------------------------
+# Pinned against torch's own conv_transpose1d definition (float64, CPU), which shares nothing with
+# the oracle's per-tap GEMM + scatter, and against planted mistakes.
+
+def torch_convt(x, w, u, b=None):
+    import torch
+    cin, cout, k = w.shape
+    pad = (k - u) // 2
+    y = torch.nn.functional.conv_transpose1d(torch.from_numpy(x.astype(np.float64))[None],
+                                             torch.from_numpy(w.astype(np.float64)), stride=u,
+                                             padding=pad)[0].numpy()
+    y = y[:, :x.shape[1] * u]  # an odd k - u leaves torch one extra column past T u
+    return y + (0 if b is None else b.astype(np.float64)[:, None])
+
+
+@pytest.mark.parametrize("cin,cout,T,k,u", [(16, 8, 40, 20, 10), (12, 6, 50, 16, 8),
+                                            (10, 5, 60, 8, 2), (8, 4, 33, 2, 2), (6, 3, 21, 5, 2),
+                                            (5, 7, 13, 7, 3), (4, 4, 9, 3, 3), (9, 5, 11, 1, 1)])
+def test_convt_matches_torch_and_rejects_mistakes(cin, cout, T, k, u):
+    r = np.random.default_rng(100 + k * u)
+    x = rnd(r, cin, T)
+    w = (r.standard_normal((cin, cout, k)) / np.sqrt(cin)).astype(np.float16)
+    b = rnd(r, cout, std=0.05)
+    got = O.convt1d(F32, x, w.view(np.uint16), u, b).astype(np.float64)
+    want = torch_convt(x, w.astype(np.float64), u, b)
+    assert got.shape == want.shape == (cout, T * u)
+    tol = 1e-6 * (np.abs(want).max() + 1)
+    assert np.max(np.abs(got - want)) <= tol
+    w64 = w.astype(np.float64)
+    mistakes = {"no bias": torch_convt(x, w64, u)}
+    if k > 1:
+        mistakes["flipped taps"] = torch_convt(x, w64[:, :, ::-1], u, b)
+    if k - u >= 2:
+        import torch
+        mistakes["pad 0"] = torch.nn.functional.conv_transpose1d(
+            torch.from_numpy(x.astype(np.float64))[None], torch.from_numpy(w64), stride=u)[0] \
+            .numpy()[:, :T * u] + b[:, None]
+    if cin == cout:
+        mistakes["[out, in] layout"] = torch_convt(x, w64.transpose(1, 0, 2), u, b)
+    for name, bad in mistakes.items():
+        assert np.max(np.abs(got - bad)) > 100 * tol, name
+
+
+def test_convt_delta_input_gives_taps():
+    cin, cout, T, k, u = 3, 4, 10, 16, 8
+    r = np.random.default_rng(7)
+    w = (r.standard_normal((cin, cout, k)) / 4).astype(np.float16)
+    x = np.zeros((cin, T), np.float32)
+    i0, j0 = 2, 5
+    x[i0, j0] = 1.0
+    y = O.convt1d(F32, x, w.view(np.uint16), u)
+    pad = (k - u) // 2
+    for d in range(k):
+        assert np.array_equal(y[:, j0 * u + d - pad], w[i0, :, d].astype(np.float32))
+    touched = {j0 * u + d - pad for d in range(k)}
+    assert np.all(y[:, [t for t in range(T * u) if t not in touched]] == 0)
+
+
+def test_convt_stride1_k1_is_matmul():
+    r = np.random.default_rng(8)
+    x = rnd(r, 24, 50)
+    w = (0.2 * r.standard_normal((24, 9, 1))).astype(np.float16)
+    got = O.convt1d(F32, x, w.view(np.uint16), 1)
+    want = w[:, :, 0].astype(np.float64).T @ x.astype(np.float64)
+    assert np.max(np.abs(got - want)) < 1e-5
+
+
+def test_convt_epilogues():
+    r = np.random.default_rng(9)
+    cin, cout, T, k, u = 6, 4, 12, 8, 2
+    x = rnd(r, cin, T)
+    w = (0.3 * r.standard_normal((cin, cout, k))).astype(np.float16).view(np.uint16)
+    b = rnd(r, cout, std=0.1)
+    cur = rnd(r, cout, T * u)
+    y0 = O.convt1d(F32, x, w, u, b)
+    assert np.array_equal(O.convt1d(F32, x, w, u, b, epi=1, slope=0.1), O.leaky_relu(F32, y0, 0.1))
+    y2, c2 = O.convt1d(F32, x, w, u, b, epi=2, slope=0.1, cur=cur)
+    c_want, t_in = O.resblock_add_lrelu(F32, cur, y0, 0.1)
+    assert np.array_equal(c2, c_want) and np.array_equal(y2, t_in)
