@@ -511,6 +511,43 @@ def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
                          "note": "algorithmic flops; exact fp32 runs two fp16 products per term"}}
 
 
+def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5):
+    """The decoder's five Generator stages end to end (gsvk.GeneratorStage: upsampler, LeakyReLU,
+    3 ResBlocks x 3 fused conv pairs, branch mean + next LeakyReLU; 24 launches per stage), eager
+    launches on one stream, exact fp32. Per stage: the median of `reps` timed runs after one warm
+    run. Total = the 5 stages for 10 s of 32 kHz audio (conv_pre, cond and conv_post not included)."""
+    out, tot = [], 0.0
+    for (C, T), (cin_up, u, k_up) in zip(DECODER_GEOMETRIES[geometry], UPS[geometry]):
+        g = lambda *shape: torch.randn(*shape, device=dev)
+        ups = gsvk.ConvT1d((g(cin_up, C, k_up) / (cin_up * k_up / u) ** 0.5).half(), g(C) * 0.05, u)
+        blocks = []
+        for k in RES_KERNELS:
+            w = lambda: (g(C, C, k) / (C * k) ** 0.5).half()
+            blocks.append(gsvk.ResBlock1([w() for _ in range(3)], [g(C) * 0.05 for _ in range(3)],
+                                         [w() for _ in range(3)], [g(C) * 0.05 for _ in range(3)]))
+        stage = gsvk.GeneratorStage(ups, blocks)
+        x = g(cin_up, T // u)
+        y = torch.empty(C, T, device=dev)
+        stage.forward(x, y)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            stage.forward(x, y)
+            e.record()
+            e.synchronize()
+            ts.append(s.elapsed_time(e) * 1e3)
+        us = sorted(ts)[len(ts) // 2]
+        tot += us
+        out.append({"C": C, "T": T, "stage_us": round(us, 1), "launches": 24})
+        log(f"  generator stage {C}x{T}: {us:.1f} us end to end")
+        del stage, blocks, ups, x, y
+        torch.cuda.empty_cache()
+    return {"geometry": geometry, "stages": out, "us_per_10s_audio": round(tot, 1),
+            "realtime_factor": round(10.0 / (tot * 1e-6), 1)}
+
+
 # ---- whole T2S decode step ---------------------------------------------------------------------------
 
 def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
@@ -753,7 +790,9 @@ def main():
         print(json.dumps(full_decode_step(torch, gsvk, dev, kv_len=a.whole_step)), flush=True)
         return
     if a.conv:
-        print(json.dumps(sovits_conv(torch, gsvk, dev)), flush=True)
+        res = sovits_conv(torch, gsvk, dev)
+        res["generator"] = sovits_generator(torch, gsvk, dev)
+        print(json.dumps(res), flush=True)
         return
 
     bufs = make_step_buffers(torch, gsvk, dev)
@@ -826,6 +865,7 @@ def main():
         decoder = sovits_decoder(torch, gsvk, dev)
         full = [full_decode_step(torch, gsvk, dev, kv_len=n) for n in (1024, 2048)]
         conv = sovits_conv(torch, gsvk, dev)
+        conv["generator"] = sovits_generator(torch, gsvk, dev)
 
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,

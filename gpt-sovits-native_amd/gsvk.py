@@ -253,6 +253,62 @@ class ConvT1d:
         return y
 
 
+class ResBlock1:
+    """Mirror of the reference's sovits ResBlock1 (dec.hpp:18-43): convs1 with dilations 1 / 3 / 5
+    and convs2 with dilation 1, all of kernel size k, as device Conv1d objects."""
+
+    def __init__(self, w1, b1, w2, b2, dilations=(1, 3, 5)):
+        self.convs1 = [Conv1d(w, b, d) for w, b, d in zip(w1, b1, dilations)]
+        self.convs2 = [Conv1d(w, b, 1) for w, b in zip(w2, b2)]
+
+
+class GeneratorStage:
+    """One stage of the reference's Generator::forward (dec.hpp:283-336) on the GPU, with every
+    element-wise pass fused into a neighbouring kernel:
+      y = ups(x)                                  x arrives already LeakyReLU'd (fused into the
+                                                  previous stage's branch mean, dec.hpp:284)
+      t_in = lrelu(y, 0.1)                        the first pair's input, shared by the branches
+      for each ResBlock j: cur_j = y; for each pair m:
+          t_a = lrelu(convs1[m](t_in))            conv + leaky_relu_io (dec.hpp:323-324)
+          cur_j += convs2[m](t_a); t_in = lrelu(cur_j)   conv + add_inplace + next leaky_relu_write
+      out = lrelu(mean_j cur_j, slope_next)       mul_write / add_scaled_inplace + the next stage's
+                                                  leaky_relu_io (dec.hpp:328-336, 284 or 342)
+    Launches: 1 upsampler, 1 LeakyReLU, 3 copies, 18 convolutions, 1 branch mean."""
+
+    def __init__(self, ups, resblocks):
+        self.ups = ups
+        self.resblocks = resblocks
+        self._buf = None
+
+    def _buffers(self, C, T, dtype, device):
+        import torch
+        key = (C, T, dtype, device)
+        if self._buf is None or self._buf[0] != key:
+            mk = lambda: torch.empty(C, T, dtype=dtype, device=device)
+            self._buf = (key, mk(), mk(), mk(), mk(), [mk() for _ in self.resblocks])
+        return self._buf[1:]
+
+    def forward(self, x, out, slope_next=0.1, round_x=False, stream=None):
+        y, t_in0, t_in, t_a, curs = self._buffers(self.ups.out_c, x.shape[1] * self.ups.stride_u,
+                                                  x.dtype, x.device)
+        self.ups.forward(x, y, round_x=round_x, stream=stream)
+        leaky_relu(y, t_in0, 0.1, stream=stream)
+        for rb, cur in zip(self.resblocks, curs):
+            scaled_add(None, y, cur, 1.0, stream=stream)  # cur_j = y, on the same stream
+            src = t_in0
+            for m, (c1, c2) in enumerate(zip(rb.convs1, rb.convs2)):
+                c1.forward(src, t_a, epi=CONV_EPI_LRELU, slope=0.1, round_x=round_x, stream=stream)
+                if m + 1 < len(rb.convs2):
+                    c2.forward(t_a, t_in, epi=CONV_EPI_RES_LRELU, slope=0.1, cur=cur,
+                               round_x=round_x, stream=stream)
+                    src = t_in
+                else:
+                    c2.forward(t_a, None, epi=CONV_EPI_RES, cur=cur, round_x=round_x,
+                               stream=stream)
+        resblock_branch_mean(curs, None, out, True, slope_next, stream=stream)
+        return out
+
+
 _WS = {}
 
 

@@ -8,6 +8,7 @@
 //   gsv::sovits::leaky_relu_io / leaky_relu_write / add_inplace / add_scaled_inplace / mul_write
 //                                                    (src/sovits/nn_ops.hpp:48-105)
 //   gsv::bert::gelu_erf over a buffer                (src/bert/bert_ops.hpp:25-27, 394)
+//   gsv::sovits::Conv1d / ConvT1d, device-resident   (src/sovits/conv1d.hpp:56-360)
 // Differences, all deliberate: pointers are device pointers; every call is enqueued on the calling
 // thread's current stream (gsvk::set_stream) and returns before the GPU finishes (call
 // gsvk::sync() before reading results on the host); a rejected argument or a HIP launch failure
@@ -196,6 +197,76 @@ inline void branch_mean_leaky(const float* const cur[3], const float* const t_b[
                                         gsvk::current_stream()),
               "gsv::sovits::branch_mean_leaky");
 }
+
+// Device-resident Conv1d (conv1d.hpp:56-203): the reference's members out_c / in_c / k / dilation
+// and b, the fp16 [out, in, k] weights packed once at load, forward(x, y) on [C, T] rows. The
+// ResBlock passes after a convolution can be fused into it: epi = GSVK_CONV_EPI_LRELU is conv1 +
+// leaky_relu_io (dec.hpp:323-324); GSVK_CONV_EPI_RES_LRELU is conv2 + add_inplace into `cur` +
+// the next pair's leaky_relu_write into y (dec.hpp:325-326, 322).
+class Conv1d {
+ public:
+  size_t out_c = 0, in_c = 0, k = 0, dilation = 1;
+  const float* b = nullptr;      // device fp32 [out_c], or nullptr (conv_post has no bias)
+  uint16_t* w_packed = nullptr;  // device, owned
+
+  Conv1d() = default;
+  Conv1d(const Conv1d&) = delete;
+  Conv1d& operator=(const Conv1d&) = delete;
+  ~Conv1d() {
+    if (w_packed) (void)hipFree(w_packed);
+  }
+
+  // w_f16: device [o, i, kk] fp16 bits (for example inside a .gsv arena); bias: device or nullptr.
+  void load(const uint16_t* w_f16, const float* bias, size_t o, size_t i, size_t kk,
+            size_t dil = 1) {
+    out_c = o, in_c = i, k = kk, dilation = dil, b = bias;
+    const size_t n = gsvk_conv1d_packed_elems(o, i, kk);
+    if (!w_packed && hipMalloc(&w_packed, n * 2) != hipSuccess)
+      throw std::runtime_error("gsv::sovits::Conv1d::load: hipMalloc failed");
+    gsvk::check(gsvk_conv1d_pack(w_f16, o, i, kk, w_packed, n, gsvk::current_stream()),
+                "gsv::sovits::Conv1d::load");
+  }
+
+  // y[out_c, T] = conv(x[in_c, T]) + b, then the epilogue (x and y must not overlap).
+  void forward(const float* x, float* y, size_t T, int epi = GSVK_CONV_EPI_BIAS,
+               float slope = 0.1f, float* cur = nullptr) const {
+    gsvk::check(gsvk_conv1d(GSVK_F32, 0, x, T, w_packed, b, epi, slope, cur, T, y, T, in_c, out_c,
+                            T, k, dilation, gsvk::current_stream()),
+                "gsv::sovits::Conv1d::forward");
+  }
+};
+
+// Device-resident ConvT1d (conv1d.hpp:205-360): the torch-layout [in, out, k] weights packed once
+// per output phase, forward(x, y) with y [out_c, T * stride_u].
+class ConvT1d {
+ public:
+  size_t out_c = 0, in_c = 0, k = 0, stride_u = 1;
+  const float* b = nullptr;
+  uint16_t* w_packed = nullptr;
+
+  ConvT1d() = default;
+  ConvT1d(const ConvT1d&) = delete;
+  ConvT1d& operator=(const ConvT1d&) = delete;
+  ~ConvT1d() {
+    if (w_packed) (void)hipFree(w_packed);
+  }
+
+  void load(const uint16_t* w_f16, const float* bias, size_t i, size_t o, size_t kk, size_t u) {
+    in_c = i, out_c = o, k = kk, stride_u = u, b = bias;
+    const size_t n = gsvk_convt1d_packed_elems(o, i, kk, u);
+    if (!w_packed && hipMalloc(&w_packed, n * 2) != hipSuccess)
+      throw std::runtime_error("gsv::sovits::ConvT1d::load: hipMalloc failed");
+    gsvk::check(gsvk_convt1d_pack(w_f16, o, i, kk, u, w_packed, n, gsvk::current_stream()),
+                "gsv::sovits::ConvT1d::load");
+  }
+
+  void forward(const float* x, float* y, size_t T, int epi = GSVK_CONV_EPI_BIAS,
+               float slope = 0.1f, float* cur = nullptr) const {
+    gsvk::check(gsvk_convt1d(GSVK_F32, 0, x, T, w_packed, b, epi, slope, cur, T * stride_u, y,
+                             T * stride_u, in_c, out_c, T, k, stride_u, gsvk::current_stream()),
+                "gsv::sovits::ConvT1d::forward");
+  }
+};
 
 }  // namespace gsv::sovits
 

@@ -252,6 +252,13 @@ void engine_like(float* x, const float* g, const float* b, float* ff, float* cur
                              GSVK_ACT_RELU);
   gsv::kern::gemv_fmlal_rows(reinterpret_cast<const uint16_t*>(g), x, ff, 64, 2048, 512, b,
                              GSVK_ACT_RELU, x);
+  gsv::sovits::Conv1d c1;
+  c1.load(reinterpret_cast<const uint16_t*>(g), b, 192, 192, 11, 5);
+  c1.forward(cur, tin, 40000, GSVK_CONV_EPI_LRELU, 0.1f);
+  c1.forward(tin, sum, 40000, GSVK_CONV_EPI_RES_LRELU, 0.1f, cur);
+  gsv::sovits::ConvT1d up;
+  up.load(reinterpret_cast<const uint16_t*>(g), b, 384, 192, 16, 8);
+  up.forward(x, cur, 5000);
 }
 '''
     path = str(tmp_path / "compat_probe.cpp")
