@@ -43,7 +43,6 @@ constexpr int kWaves = 4;   // waves per workgroup, side by side along t
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxHalo = 256;
 constexpr int kTapGroup = 4;  // taps whose weights share one LDS refill
-constexpr int kWRow = 40;     // LDS halves per weight row: 32 channels + 8 padding
 
 struct ConvArgs {
   const void* x;
@@ -104,14 +103,24 @@ constexpr int planes() { return XM == kXSplit ? 2 : 1; }
 template <int XM>
 constexpr int storage_dt() { return XM == kXF16 ? GSVK_F16 : GSVK_F32; }
 
-// Packed weights: wp[((c k + kk) opad + o) 32 + j] = w[o, 32 c + j, kk], zero past C_out / C_in.
+// Packed weights, step s = c k + kk (chunk c, tap kk), channel group g = 0..3 of the chunk:
+// wp[((s 4 + g) opad + o) 8 + j] = w[o, 32 c + 8 g + j, kk], zero past C_out / C_in. One step's
+// group g is opad contiguous 16-byte rows, the layout of the B fragments in LDS.
+__device__ __forceinline__ void unpack_index(long e, long opad, long& s, long& g, long& o, long& j) {
+  j = e % 8;
+  o = (e / 8) % opad;
+  g = (e / (8 * opad)) % 4;
+  s = e / (kChunk * opad);
+}
+
 __global__ __launch_bounds__(256) void conv_pack(const uint16_t* __restrict__ w,
                                                  uint16_t* __restrict__ wp, long cout, long cin,
                                                  long k, long opad, long total) {
   for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
        e += static_cast<long>(gridDim.x) * blockDim.x) {
-    const long j = e % kChunk, o = (e / kChunk) % opad, s = e / (kChunk * opad);
-    const long c = s / k, kk = s % k, i = c * kChunk + j;
+    long s, g, o, j;
+    unpack_index(e, opad, s, g, o, j);
+    const long c = s / k, kk = s % k, i = c * kChunk + 8 * g + j;
     wp[e] = (o < cout && i < cin) ? w[(o * cin + i) * k + kk] : uint16_t(0);
   }
 }
@@ -130,8 +139,9 @@ __global__ __launch_bounds__(256) void convt_pack(const uint16_t* __restrict__ w
       ++r;
       kn = (k - r + u - 1) / u;
     }
-    const long j = rest % kChunk, o = (rest / kChunk) % opad, s = rest / (kChunk * opad);
-    const long c = s / kn, kk = s % kn, i = c * kChunk + j, d = r + (kn - 1 - kk) * u;
+    long s, g, o, j;
+    unpack_index(rest, opad, s, g, o, j);
+    const long c = s / kn, kk = s % kn, i = c * kChunk + 8 * g + j, d = r + (kn - 1 - kk) * u;
     wp[e] = (o < cout && i < cin) ? w[(i * cout + o) * k + d] : uint16_t(0);
   }
 }
@@ -209,8 +219,11 @@ __device__ __forceinline__ void finish4(const ConvArgs& a, const Map& m, long o,
 
 // XM: activation mode; NT: 16-t fragments per wave; NO: 16-row output fragments per wave;
 // HMAX: largest halo (k - 1) dil the LDS tile holds.
+// At least two waves per SIMD: the register budget is sized for them (every tile fits without
+// spilling; the compiler would otherwise keep two steps' fragments live).
 template <int XM, int NT, int NO, int HMAX>
-__global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void conv1d_mfma(
+    ConvArgs a) {
   constexpr int DT = storage_dt<XM>();
   constexpr int P = planes<XM>();
   constexpr int TT = kWaves * 16 * NT;  // output columns of the workgroup
@@ -283,12 +296,13 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   };
 
   // ---- weights: groups of up to kTapGroup taps of the chunk through LDS ------------------------
-  // Group q covers chunk c = q / ng, taps kk0 = 4 (q % ng) .. +3 (fewer at the end of k). Its
-  // packed rows [s][o0 .. o0 + 16 NO)[32] (s = c k + kk) are 16 NO x 64 contiguous bytes per tap:
-  // item it = tid + 256 u is tap it / (64 NO), row (it % (64 NO)) / 4, 16-byte part it % 4. In LDS
-  // a row holds kWRow halves (32 + 8 padding) so that the 16 rows of a fragment read fall on
-  // distinct banks.
-  _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][16 NO][kWRow]
+  // Group q covers chunk c = q / ng, taps kk0 = 4 (q % ng) .. +3 (fewer at the end of k). In LDS,
+  // ws[tap][channel group][16 NO rows][8]: a B fragment read is then 16 consecutive 16-byte rows,
+  // like the x reads (no bank conflicts). Item it = tid + 256 u is tap it / (64 NO), channel group
+  // (it / (16 NO)) % 4, row it % (16 NO): consecutive lanes read consecutive 16-byte rows of the
+  // packed weights and write consecutive rows of LDS.
+  constexpr int TO = 16 * NO;
+  _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][4][TO][8]
   const int ng = (m.kn + kTapGroup - 1) / kTapGroup;
   const int Q = a.nch * ng;
   u32x4 wraw[NO];
@@ -298,18 +312,16 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
 #pragma unroll
     for (int u = 0; u < NO; ++u) {
       const int it = tid + kThreads * u;
-      const int tap = it / (64 * NO), rem = it - tap * 64 * NO;
-      const size_t row = (s0 + min(tap, nt - 1)) * a.opad + o0 + (rem >> 2);
-      wraw[u] = ld16<false>(m.wp + row * kChunk + (rem & 3) * 8);
+      const int tap = it / (4 * TO), gq = (it / TO) & 3, row = it % TO;
+      const size_t r = ((s0 + min(tap, nt - 1)) * 4 + gq) * a.opad + o0 + row;
+      wraw[u] = ld16<false>(m.wp + r * 8);
     }
   };
   auto wstage = [&]() {
 #pragma unroll
     for (int u = 0; u < NO; ++u) {
-      const int it = tid + kThreads * u;
-      const int tap = it / (64 * NO), rem = it - tap * 64 * NO;
-      *reinterpret_cast<u32x4*>(ws + (tap * 16 * NO + (rem >> 2)) * kWRow + (rem & 3) * 8) =
-          wraw[u];
+      const int it = tid + kThreads * u;  // = ((tap 4 + group) TO + row): the LDS row
+      *reinterpret_cast<u32x4*>(ws + static_cast<size_t>(it) * 8) = wraw[u];
     }
   };
 
@@ -327,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   // One step: tap kk0 + tl (slot tl of the group) of the staged chunk. Only LDS reads feed the
   // MFMAs.
   const _Float16* xw = xs + (static_cast<size_t>(grp) * TTH + wave * 16 * NT + r16) * 8;
-  const _Float16* wr = ws + r16 * kWRow + 8 * grp;
+  const _Float16* wr = ws + (static_cast<size_t>(grp) * TO + r16) * 8;
   auto step = [&](int kk, int tl) {
     const int sh = kk * a.dil;
     h8 xf[NT][P], wf[NO];
@@ -339,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
             xw + (static_cast<size_t>(p) * 4 * TTH + 16 * i + sh) * 8);
 #pragma unroll
     for (int n = 0; n < NO; ++n)
-      wf[n] = *reinterpret_cast<const h8*>(wr + (tl * 16 * NO + 16 * n) * kWRow);
+      wf[n] = *reinterpret_cast<const h8*>(wr + (static_cast<size_t>(tl) * 4 * TO + 16 * n) * 8);
 #pragma unroll
     for (int p = 0; p < P; ++p)
 #pragma unroll
@@ -381,22 +393,24 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
   }
 
   // ---- epilogue ---------------------------------------------------------------------------------
-  f4v cur[NT][NO];
-  if (a.epi >= 2) {
+  // Output-row block n at a time; the residual epilogues read block n + 1's cur before block n is
+  // finished, so each block's loads are in flight together (two blocks of registers at most).
+  f4v cur[2][NT];
+  auto load_block = [&](f4v (&c)[NT], int n) {
 #pragma unroll
-    for (int n = 0; n < NO; ++n)
-#pragma unroll
-      for (int i = 0; i < NT; ++i)
-        cur[i][n] = load_cur<DT>(a, m, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
-  }
+    for (int i = 0; i < NT; ++i)
+      c[i] = load_cur<DT>(a, m, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
+  };
+  if (a.epi >= 2) load_block(cur[0], 0);
 #pragma unroll
   for (int n = 0; n < NO; ++n) {
+    if (a.epi >= 2 && n + 1 < NO) load_block(cur[(n + 1) & 1], n + 1);
     const long o = o0 + 16 * n + r16;
     if (o >= a.cout) continue;
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
       const long t = t0 + wave * 16 * NT + 16 * i + 4 * grp;
-      if (t < m.nq) finish4<DT>(a, m, o, t, acc[i][n], bias[n], cur[i][n]);
+      if (t < m.nq) finish4<DT>(a, m, o, t, acc[i][n], bias[n], cur[n & 1][i]);
     }
   }
 }
@@ -404,7 +418,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_mfma(ConvArgs a) {
 template <int XM, int NT, int NO, int HMAX>
 constexpr size_t lds_bytes() {
   return static_cast<size_t>(planes<XM>()) * 4 * (kWaves * 16 * NT + HMAX) * 16 +
-         static_cast<size_t>(kTapGroup) * 16 * NO * kWRow * 2;
+         static_cast<size_t>(kTapGroup) * 4 * 16 * NO * 16;
 }
 
 template <int XM, int NT, int NO, int HMAX>
@@ -438,8 +452,10 @@ int launch_no(const ConvArgs& a, int no, hipStream_t st) {
 }
 
 // Output rows per wave: the largest fragment count (4..1) that pads at most a sixth of the rows
-// it computes, and whose last tile stays inside the packed rows. Columns per wave: 64, or 32 when
-// that leaves fewer than two workgroups per CU.
+// it computes, and whose last tile stays inside the packed rows. Columns per wave: 32 (128 per
+// workgroup, three workgroups per CU). Measured on the decoder stages: more, smaller workgroups in
+// flight beat larger register tiles (64 columns or 96 rows per wave cut the LDS bytes per MFMA but
+// were slower on every stage: the group refills, not LDS bandwidth, set the pace).
 template <int XM>
 int launch_plan(const ConvArgs& a, hipStream_t st) {
   const long ofr = (a.cout + 15) / 16;
@@ -451,11 +467,8 @@ int launch_plan(const ConvArgs& a, hipStream_t st) {
       break;
     }
   }
-  const long tiles64 = (a.T + 255) / 256 * ((ofr + no - 1) / no) * (a.up ? a.up : 1);
-  const bool nt2 = tiles64 < 512;
   const int halo = a.up ? (a.k + a.up - 1) / a.up - 1 : (a.k - 1) * a.dil;
-  if (halo <= 64)
-    return nt2 ? launch_no<XM, 2, 64>(a, no, st) : launch_no<XM, 4, 64>(a, no, st);
+  if (halo <= 64) return launch_no<XM, 2, 64>(a, no, st);
   return launch_no<XM, 1, kMaxHalo>(a, no, st);
 }
 
