@@ -662,6 +662,69 @@ def cpu_baseline(torch, bufs, rep_s=0.3, reps=9):
     return res, threads_all
 
 
+def next_tier_cpu(reps=3):
+    """Bounded CPU samples of the next-tier rows on the oracle's C restatement (one thread; the
+    reference's own NEON / Accelerate code does not build on x86): one T2S decoder layer of the
+    whole decode step at B = 64, kv_len 1024 (scaled to 24 layers + the logits GEMV), and a
+    1,000-column window of the 192 x 40000, k 11, dilation 5 ResBlock convolution (scaled to 40,000
+    columns). Median of `reps` runs each."""
+    import numpy as np
+
+    import oracle as O
+    r = np.random.default_rng(SEED + 11)
+    w = lambda n, k: (0.05 * r.standard_normal((n, k))).astype(np.float16).view(np.uint16)
+    vec = lambda n, m=0.0: (m + 0.02 * r.standard_normal(n)).astype(np.float32)
+    H, KV = 16, 1024
+    x = O.to_storage(O.F16, r.standard_normal((B, D)).astype(np.float32))
+    ly = dict(wqkv=w(3 * D, D), bqkv=vec(3 * D), wout=w(D, D), bout=vec(D), n1g=vec(D, 1.0),
+              n1b=vec(D), w1=w(FF, D), b1=vec(FF), w2=w(D, FF), b2=vec(D), n2g=vec(D, 1.0),
+              n2b=vec(D))
+    kc = O.to_storage(O.F16, r.standard_normal((B, KV + 1, D)).astype(np.float32))
+    vc = O.to_storage(O.F16, r.standard_normal((B, KV + 1, D)).astype(np.float32))
+    kv_pos = np.full(B, KV, np.int64)
+    w_logits = w(VOCAB, D)
+
+    def layer():
+        qkv = O.gemv_f16w(O.F16, x, ly["wqkv"], O.F32, bias=ly["bqkv"])
+        attn = O.to_storage(O.F16, O.decode_attention(O.F16, qkv, kc, vc, kv_pos, H, D // H))
+        z = O.gemv_f16w(O.F16, attn, ly["wout"], O.F16, bias=ly["bout"], residual=x)
+        h = O.add_layernorm(O.F16, z, ly["n1g"], ly["n1b"], 1e-5)
+        ff = O.gemv_f16w(O.F16, h, ly["w1"], O.F16, bias=ly["b1"], act=1)
+        z = O.gemv_f16w(O.F16, ff, ly["w2"], O.F16, bias=ly["b2"], residual=h)
+        return O.add_layernorm(O.F16, z, ly["n2g"], ly["n2b"], 1e-5)
+
+    def med(fn):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    t_layer = med(layer)
+    t_logits = med(lambda: O.gemv_f16w(O.F16, x, w_logits, O.F32))
+    step_s = LAYERS * t_layer + t_logits
+    C, T, k, dil, win = 192, 40000, 11, 5, 1000
+    xs = r.standard_normal((C, win + (k - 1) * dil)).astype(np.float32)
+    wc = (r.standard_normal((C, C, k)) / np.sqrt(C * k)).astype(np.float16).view(np.uint16)
+    t_conv = med(lambda: O.conv1d(O.F32, xs, wc, vec(C), dil, epi=1)) * T / xs.shape[1]
+    model = cpu_model()
+    return {
+        "t2s_whole_decode_step": {
+            "value": round(B / step_s, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "us_per_step": round(step_s * 1e6, 0),
+            "sample": f"one decoder layer (QKV GEMV, attention over {KV} cached fp16 rows, out-proj, "
+                      f"LN1, W1 + ReLU, W2, LN2) at B={B} x {LAYERS} + the logits GEMV; median of "
+                      f"{reps}", "cpu_model": model},
+        "sovits_conv_192x40000_k11_d5": {
+            "value": round(2.0 * C * C * k * T / t_conv / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
+            "kind": "port", "us": round(t_conv * 1e6, 0),
+            "sample": f"a {xs.shape[1]}-column window scaled by {T / xs.shape[1]:.1f} to {T} "
+                      f"columns, exact fp32 with the LeakyReLU epilogue; median of {reps}",
+            "cpu_model": model},
+    }
+
+
 # ---- decode-step ops, copy reference, counter workload ---------------------------------------------
 
 def step_ops(gsvk, bufs):
@@ -792,6 +855,8 @@ def main():
     if a.conv:
         res = sovits_conv(torch, gsvk, dev)
         res["generator"] = sovits_generator(torch, gsvk, dev)
+        if not a.no_cpu:
+            res["cpu_baseline"] = next_tier_cpu()["sovits_conv_192x40000_k11_d5"]
         print(json.dumps(res), flush=True)
         return
 
@@ -866,6 +931,15 @@ def main():
         full = [full_decode_step(torch, gsvk, dev, kv_len=n) for n in (1024, 2048)]
         conv = sovits_conv(torch, gsvk, dev)
         conv["generator"] = sovits_generator(torch, gsvk, dev)
+        if not a.no_cpu:
+            nt = next_tier_cpu()
+            full[0]["cpu_baseline"] = nt["t2s_whole_decode_step"]
+            full[0]["vs_cpu"] = round(full[0]["tokens_per_s"] / nt["t2s_whole_decode_step"]["value"], 1)
+            conv["cpu_baseline"] = nt["sovits_conv_192x40000_k11_d5"]
+            big = [c for c in conv["stages"][1]["convs"] if c["k"] == 11 and c["dil"] == 5][0]
+            conv["vs_cpu"] = round(conv["cpu_baseline"]["us"] / big["us"], 1)
+            log(f"  CPU (oracle, 1 thread): decode step {nt['t2s_whole_decode_step']['us_per_step']:.0f}"
+                f" us, conv 192x40000 k11 {nt['sovits_conv_192x40000_k11_d5']['us']:.0f} us")
 
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
