@@ -42,13 +42,17 @@ constexpr int kOPad = 64;   // packed output rows: a multiple of the largest wav
 constexpr int kWaves = 4;   // waves per workgroup, side by side along t
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxHalo = 256;
-constexpr int kTapGroup = 4;  // taps whose weights share one LDS refill
+#ifndef GSVK_CONV_TAP_GROUP
+#define GSVK_CONV_TAP_GROUP 4
+#endif
+constexpr int kTapGroup = GSVK_CONV_TAP_GROUP;  // taps whose weights share one LDS refill
 
 struct ConvArgs {
   const void* x;
   const uint16_t* wp;
   const float* bias;
   void* cur;
+  const void* res;  // residual source of epi 2 / 3 (row stride ldc); nullptr: cur itself
   void* y;
   long cin, cout, T, ldx, ldc, ldy;  // T: input columns
   int k, dil, pad, nch, opad;
@@ -156,19 +160,36 @@ __device__ __forceinline__ float ld1(const void* p, size_t i) { return Store<DT>
 template <int DT>
 __device__ __forceinline__ f4v load_cur(const ConvArgs& a, const Map& m, long o, long t) {
   const size_t row = static_cast<size_t>(min(o, a.cout - 1)) * a.ldc + m.obase;
+  const void* src = a.res ? a.res : a.cur;
   f4v c;
   if (a.vec && m.ostr == 1 && t + 4 <= m.nq) {
     if constexpr (DT == GSVK_F32) {
-      c = *reinterpret_cast<const f4v*>(static_cast<const float*>(a.cur) + row + t);
+      c = *reinterpret_cast<const f4v*>(static_cast<const float*>(src) + row + t);
     } else {
-      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.cur) + row + t);
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) + row + t);
       c = f4v{h2f(q.x & 0xffffu), h2f(q.x >> 16), h2f(q.y & 0xffffu), h2f(q.y >> 16)};
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c[q] = ld1<DT>(a.cur, row + min(t + q, m.nq - 1) * m.ostr);
+    for (int q = 0; q < 4; ++q) c[q] = ld1<DT>(src, row + min(t + q, m.nq - 1) * m.ostr);
   }
   return c;
+}
+
+template <int DT>
+__device__ __forceinline__ void store4(void* base, size_t off, long stride, const float (&v)[4],
+                                       bool full, long valid) {
+  if (full) {
+    if constexpr (DT == GSVK_F32)
+      *reinterpret_cast<float4*>(static_cast<float*>(base) + off) = float4{v[0], v[1], v[2], v[3]};
+    else
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + off) =
+          uint2{f2h2(v[0], v[1]), f2h2(v[2], v[3])};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < valid) Store<DT>::store1(base, off + q * stride, v[q]);
+  }
 }
 
 // Positions t .. t+3 of row o: bias, epilogue, stores. Vector stores when the four columns are
@@ -182,43 +203,40 @@ __device__ __forceinline__ void finish4(const ConvArgs& a, const Map& m, long o,
   const size_t yo = static_cast<size_t>(o) * a.ldy + m.obase + t * m.ostr;
   const size_t co = static_cast<size_t>(o) * a.ldc + m.obase + t * m.ostr;
   const bool full = a.vec && m.ostr == 1 && t + 4 <= m.nq;
-  if (a.epi >= 2) {  // cur += conv (+ b); epi 2 also writes y = lrelu(cur)
-    float c[4];
+  const long valid = m.nq - t;
+  switch (a.epi) {
+    case GSVK_CONV_EPI_RES_LRELU:
+    case GSVK_CONV_EPI_RES: {  // cur = res + conv (+ b); RES_LRELU also writes y = lrelu(cur)
+      float c[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c[q] = cur[q] + v[q];
-    if (full) {
-      if constexpr (DT == GSVK_F32)
-        *reinterpret_cast<float4*>(static_cast<float*>(a.cur) + co) = float4{c[0], c[1], c[2], c[3]};
-      else
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.cur) + co) =
-            uint2{f2h2(c[0], c[1]), f2h2(c[2], c[3])};
-    } else {
+      for (int q = 0; q < 4; ++q) c[q] = cur[q] + v[q];
+      store4<DT>(a.cur, co, m.ostr, c, full, valid);
+      if (a.epi == GSVK_CONV_EPI_RES) return;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (t + q < m.nq) Store<DT>::store1(a.cur, co + q * m.ostr, c[q]);
+      for (int q = 0; q < 4; ++q) v[q] = lrelu_ref(c[q], a.slope);
+      break;
     }
-    if (a.epi == 3) return;
+    case GSVK_CONV_EPI_DUAL: {  // y = conv (+ b) and cur = lrelu(y)
+      float l[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = lrelu_ref(c[q], a.slope);
-  } else if (a.epi == 1) {
+      for (int q = 0; q < 4; ++q) l[q] = lrelu_ref(v[q], a.slope);
+      store4<DT>(a.cur, co, m.ostr, l, full, valid);
+      break;
+    }
+    case GSVK_CONV_EPI_LRELU:
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = lrelu_ref(v[q], a.slope);
+      for (int q = 0; q < 4; ++q) v[q] = lrelu_ref(v[q], a.slope);
+      break;
+    case GSVK_CONV_EPI_TANH:
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = tanhf(v[q]);
+      break;
+    default:
+      break;
   }
-  if (full) {
-    if constexpr (DT == GSVK_F32)
-      *reinterpret_cast<float4*>(static_cast<float*>(a.y) + yo) = float4{v[0], v[1], v[2], v[3]};
-    else
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + yo) =
-          uint2{f2h2(v[0], v[1]), f2h2(v[2], v[3])};
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (t + q < m.nq) Store<DT>::store1(a.y, yo + q * m.ostr, v[q]);
-  }
+  store4<DT>(a.y, yo, m.ostr, v, full, valid);
 }
 
-// XM: activation mode; NT: 16-t fragments per wave; NO: 16-row output fragments per wave;
-// HMAX: largest halo (k - 1) dil the LDS tile holds.
 // At least two waves per SIMD: the register budget is sized for them (every tile fits without
 // spilling; the compiler would otherwise keep two steps' fragments live).
 template <int XM, int NT, int NO, int HMAX>
@@ -296,22 +314,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   };
 
   // ---- weights: groups of up to kTapGroup taps of the chunk through LDS ------------------------
-  // Group q covers chunk c = q / ng, taps kk0 = 4 (q % ng) .. +3 (fewer at the end of k). In LDS,
-  // ws[tap][channel group][16 NO rows][8]: a B fragment read is then 16 consecutive 16-byte rows,
-  // like the x reads (no bank conflicts). Item it = tid + 256 u is tap it / (64 NO), channel group
-  // (it / (16 NO)) % 4, row it % (16 NO): consecutive lanes read consecutive 16-byte rows of the
-  // packed weights and write consecutive rows of LDS.
+  // Group q covers chunk c = q / ng, taps kk0 = kTapGroup (q % ng) and the next kTapGroup - 1
+  // (fewer at the end of k). In LDS, ws[tap][channel group][16 NO rows][8]: a B fragment read is
+  // then 16 consecutive 16-byte rows, like the x reads (no bank conflicts). Item it = tid + 256 u
+  // is tap it / (64 NO), channel group (it / (16 NO)) % 4, row it % (16 NO): consecutive lanes read
+  // consecutive 16-byte rows of the packed weights and write consecutive rows of LDS.
   constexpr int TO = 16 * NO;
+  constexpr int WITEMS = kTapGroup * 4 * TO;                 // 16-byte rows per group
+  constexpr int WPT = (WITEMS + kThreads - 1) / kThreads;   // per thread
   _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][4][TO][8]
   const int ng = (m.kn + kTapGroup - 1) / kTapGroup;
   const int Q = a.nch * ng;
-  u32x4 wraw[NO];
+  u32x4 wraw[WPT];
   auto wload = [&](int q) {
     const int c = q / ng, kk0 = (q - c * ng) * kTapGroup, nt = min(kTapGroup, m.kn - kk0);
     const size_t s0 = static_cast<size_t>(c) * m.kn + kk0;
 #pragma unroll
-    for (int u = 0; u < NO; ++u) {
-      const int it = tid + kThreads * u;
+    for (int u = 0; u < WPT; ++u) {
+      const int it = min(tid + kThreads * u, WITEMS - 1);
       const int tap = it / (4 * TO), gq = (it / TO) & 3, row = it % TO;
       const size_t r = ((s0 + min(tap, nt - 1)) * 4 + gq) * a.opad + o0 + row;
       wraw[u] = ld16<false>(m.wp + r * 8);
@@ -319,9 +339,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   };
   auto wstage = [&]() {
 #pragma unroll
-    for (int u = 0; u < NO; ++u) {
+    for (int u = 0; u < WPT; ++u) {
       const int it = tid + kThreads * u;  // = ((tap 4 + group) TO + row): the LDS row
-      *reinterpret_cast<u32x4*>(ws + static_cast<size_t>(it) * 8) = wraw[u];
+      if (WITEMS % kThreads == 0 || it < WITEMS)
+        *reinterpret_cast<u32x4*>(ws + static_cast<size_t>(it) * 8) = wraw[u];
     }
   };
 
@@ -401,10 +422,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int i = 0; i < NT; ++i)
       c[i] = load_cur<DT>(a, m, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
   };
-  if (a.epi >= 2) load_block(cur[0], 0);
+  const bool has_res = a.epi == GSVK_CONV_EPI_RES_LRELU || a.epi == GSVK_CONV_EPI_RES;
+  if (has_res) load_block(cur[0], 0);
 #pragma unroll
   for (int n = 0; n < NO; ++n) {
-    if (a.epi >= 2 && n + 1 < NO) load_block(cur[(n + 1) & 1], n + 1);
+    if (has_res && n + 1 < NO) load_block(cur[(n + 1) & 1], n + 1);
     const long o = o0 + 16 * n + r16;
     if (o >= a.cout) continue;
 #pragma unroll
@@ -499,50 +521,71 @@ extern "C" int gsvk_conv1d_pack(const uint16_t* w, size_t c_out, size_t c_in, si
   return launch_status();
 }
 
+namespace gsvk {
+namespace {
+
+// Validation and launch shared by both entry points. T: input columns; Tout: output columns.
+int conv_entry(ConvArgs a, int dtype, int round_x, size_t T, size_t Tout, size_t wb,
+               hipStream_t st) {
+  if (dtype != GSVK_F32 && dtype != GSVK_F16) return GSVK_E_DTYPE;
+  if (a.epi < GSVK_CONV_EPI_BIAS || a.epi > GSVK_CONV_EPI_TANH) return GSVK_E_DTYPE;
+  const bool reads_res = a.epi == GSVK_CONV_EPI_RES_LRELU || a.epi == GSVK_CONV_EPI_RES;
+  const bool has_cur = reads_res || a.epi == GSVK_CONV_EPI_DUAL;
+  const bool has_y = a.epi != GSVK_CONV_EPI_RES;
+  if (!a.x || !a.wp || (has_y && !a.y) || (has_cur && !a.cur)) return GSVK_E_NULL;
+  const size_t ldx = static_cast<size_t>(a.ldx), ldy = static_cast<size_t>(a.ldy),
+               ldc = static_cast<size_t>(a.ldc);
+  if (ldx < T || (has_y && ldy < Tout) || (has_cur && ldc < Tout)) return GSVK_E_SIZE;
+  if (kChunk * ldx * dtype_size(dtype) >= (1ul << 31)) return GSVK_E_SIZE;
+  if (!aligned16(a.wp)) return GSVK_E_ARG;
+  if (!has_y) a.y = nullptr, a.ldy = 0;
+  if (!has_cur) a.cur = nullptr, a.ldc = 0;
+  if (!reads_res || a.res == a.cur) a.res = nullptr;
+  const size_t esz = dtype_size(dtype);
+  const size_t xb = span_bytes(static_cast<size_t>(a.cin), T, ldx, esz);
+  const size_t bb = a.bias ? static_cast<size_t>(a.cout) * 4 : 0;
+  const size_t yb = has_y ? span_bytes(static_cast<size_t>(a.cout), Tout, ldy, esz) : 0;
+  const size_t cb = has_cur ? span_bytes(static_cast<size_t>(a.cout), Tout, ldc, esz) : 0;
+  const void* outs[2] = {a.y, a.cur};
+  const size_t outb[2] = {yb, cb};
+  for (int i = 0; i < 2; ++i)
+    if (overlaps(outs[i], outb[i], a.x, xb) || overlaps(outs[i], outb[i], a.wp, wb) ||
+        overlaps(outs[i], outb[i], a.bias, bb) || overlaps(outs[i], outb[i], a.res, cb))
+      return GSVK_E_ALIAS;
+  if (overlaps(a.y, yb, a.cur, cb)) return GSVK_E_ALIAS;
+  const size_t va = esz * 4;  // one vector: four elements
+  a.vec = Tout >= 4 && (!a.y || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(a.y) % va == 0)) &&
+          (!a.cur || (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(a.cur) % va == 0)) &&
+          (!a.res || reinterpret_cast<uintptr_t>(a.res) % va == 0);
+  if (a.up && a.up != 1) a.vec = false;  // interleaved phases: element stores
+  if (dtype == GSVK_F16) return launch_plan<kXF16>(a, st);
+  return round_x ? launch_plan<kXRound>(a, st) : launch_plan<kXSplit>(a, st);
+}
+
+}  // namespace
+}  // namespace gsvk
+
 extern "C" int gsvk_conv1d(int dtype, int round_x, const void* x, size_t ldx,
                            const uint16_t* w_packed, const float* bias, int epi, float slope,
-                           void* cur, size_t ldc, void* y, size_t ldy, size_t c_in, size_t c_out,
-                           size_t T, size_t k, size_t dilation, void* stream) {
-  if (dtype != GSVK_F32 && dtype != GSVK_F16) return GSVK_E_DTYPE;
-  if (epi < GSVK_CONV_EPI_BIAS || epi > GSVK_CONV_EPI_RES) return GSVK_E_DTYPE;
-  const bool has_res = epi == GSVK_CONV_EPI_RES_LRELU || epi == GSVK_CONV_EPI_RES;
-  const bool has_y = epi != GSVK_CONV_EPI_RES;
-  if (!x || !w_packed || (has_y && !y) || (has_res && !cur)) return GSVK_E_NULL;
-  if (!c_in || !c_out || !T || !k || !dilation || ldx < T || (has_y && ldy < T) ||
-      (has_res && ldc < T))
-    return GSVK_E_SIZE;
+                           void* cur, const void* res, size_t ldc, void* y, size_t ldy,
+                           size_t c_in, size_t c_out, size_t T, size_t k, size_t dilation,
+                           void* stream) {
+  if (!c_in || !c_out || !T || !k || !dilation) return GSVK_E_SIZE;
   if (c_in > (1ul << 24) || c_out > (1ul << 24) || k > 4096 || dilation > 4096 ||
       T > (1ul << 31) - 512 || ldx > (1ul << 40) || ldy > (1ul << 40) || ldc > (1ul << 40))
     return GSVK_E_SIZE;
   if ((k - 1) * dilation > static_cast<size_t>(kMaxHalo)) return GSVK_E_ARG;
-  // a chunk of 32 input rows is addressed with 32-bit byte offsets
-  if (kChunk * ldx * dtype_size(dtype) >= (1ul << 31)) return GSVK_E_SIZE;
-  if (!aligned16(w_packed)) return GSVK_E_ARG;
-  const size_t esz = dtype_size(dtype);
-  const size_t xb = span_bytes(c_in, T, ldx, esz);
-  const size_t wb = gsvk_conv1d_packed_elems(c_out, c_in, k) * 2;
-  const size_t bb = bias ? c_out * 4 : 0;
-  const void* yp = has_y ? y : nullptr;
-  const void* cp = has_res ? cur : nullptr;
-  const size_t yb = has_y ? span_bytes(c_out, T, ldy, esz) : 0;
-  const size_t cb = has_res ? span_bytes(c_out, T, ldc, esz) : 0;
-  if (overlaps(yp, yb, x, xb) || overlaps(yp, yb, w_packed, wb) || overlaps(yp, yb, bias, bb) ||
-      overlaps(yp, yb, cp, cb) || overlaps(cp, cb, x, xb) || overlaps(cp, cb, w_packed, wb) ||
-      overlaps(cp, cb, bias, bb))
-    return GSVK_E_ALIAS;
-
-  ConvArgs a{x, w_packed, bias, cur, y, static_cast<long>(c_in), static_cast<long>(c_out),
-             static_cast<long>(T), static_cast<long>(ldx), static_cast<long>(has_res ? ldc : 0),
-             static_cast<long>(has_y ? ldy : 0), static_cast<int>(k), static_cast<int>(dilation),
-             static_cast<int>((k - 1) * dilation / 2),
-             static_cast<int>((c_in + kChunk - 1) / kChunk),
-             static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad), epi, slope, false};
-  const size_t va = esz * 4;  // one vector: four elements
-  a.vec = T >= 4 && (!has_y || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % va == 0)) &&
-          (!has_res || (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(cur) % va == 0));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == GSVK_F16) return launch_plan<kXF16>(a, st);
-  return round_x ? launch_plan<kXRound>(a, st) : launch_plan<kXSplit>(a, st);
+  ConvArgs a{};
+  a.x = x, a.wp = w_packed, a.bias = bias, a.cur = cur, a.res = res, a.y = y;
+  a.cin = static_cast<long>(c_in), a.cout = static_cast<long>(c_out), a.T = static_cast<long>(T);
+  a.ldx = static_cast<long>(ldx), a.ldc = static_cast<long>(ldc), a.ldy = static_cast<long>(ldy);
+  a.k = static_cast<int>(k), a.dil = static_cast<int>(dilation);
+  a.pad = static_cast<int>((k - 1) * dilation / 2);
+  a.nch = static_cast<int>((c_in + kChunk - 1) / kChunk);
+  a.opad = static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad);
+  a.epi = epi, a.slope = slope;
+  return conv_entry(a, dtype, round_x, T, T, gsvk_conv1d_packed_elems(c_out, c_in, k) * 2,
+                    static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t gsvk_convt1d_packed_elems(size_t c_out, size_t c_in, size_t k, size_t stride) {
@@ -574,49 +617,27 @@ extern "C" int gsvk_convt1d_pack(const uint16_t* w, size_t c_out, size_t c_in, s
 
 extern "C" int gsvk_convt1d(int dtype, int round_x, const void* x, size_t ldx,
                             const uint16_t* w_packed, const float* bias, int epi, float slope,
-                            void* cur, size_t ldc, void* y, size_t ldy, size_t c_in, size_t c_out,
-                            size_t T, size_t k, size_t stride, void* stream) {
-  if (dtype != GSVK_F32 && dtype != GSVK_F16) return GSVK_E_DTYPE;
-  if (epi < GSVK_CONV_EPI_BIAS || epi > GSVK_CONV_EPI_RES) return GSVK_E_DTYPE;
-  const bool has_res = epi == GSVK_CONV_EPI_RES_LRELU || epi == GSVK_CONV_EPI_RES;
-  const bool has_y = epi != GSVK_CONV_EPI_RES;
-  if (!x || !w_packed || (has_y && !y) || (has_res && !cur)) return GSVK_E_NULL;
-  if (!c_in || !c_out || !T || !k || !stride || ldx < T) return GSVK_E_SIZE;
+                            void* cur, const void* res, size_t ldc, void* y, size_t ldy,
+                            size_t c_in, size_t c_out, size_t T, size_t k, size_t stride,
+                            void* stream) {
+  if (!c_in || !c_out || !T || !k || !stride) return GSVK_E_SIZE;
   if (c_in > (1ul << 24) || c_out > (1ul << 24) || k > 4096 || stride > 4096 ||
       T > (1ul << 31) / stride - 512 || ldx > (1ul << 40) || ldy > (1ul << 40) ||
       ldc > (1ul << 40))
     return GSVK_E_SIZE;
-  const size_t Tout = T * stride;
-  if ((has_y && ldy < Tout) || (has_res && ldc < Tout)) return GSVK_E_SIZE;
   // pad = (k - u) / 2 needs k >= u (ConvT1d, conv1d.hpp:262); each phase's taps share one LDS tile
   if (k < stride || (k + stride - 1) / stride - 1 > 64) return GSVK_E_ARG;
-  if (kChunk * ldx * dtype_size(dtype) >= (1ul << 31)) return GSVK_E_SIZE;
-  if (!aligned16(w_packed)) return GSVK_E_ARG;
-  const size_t esz = dtype_size(dtype);
-  const size_t xb = span_bytes(c_in, T, ldx, esz);
-  const size_t wb = gsvk_convt1d_packed_elems(c_out, c_in, k, stride) * 2;
-  const size_t bb = bias ? c_out * 4 : 0;
-  const void* yp = has_y ? y : nullptr;
-  const void* cp = has_res ? cur : nullptr;
-  const size_t yb = has_y ? span_bytes(c_out, Tout, ldy, esz) : 0;
-  const size_t cb = has_res ? span_bytes(c_out, Tout, ldc, esz) : 0;
-  if (overlaps(yp, yb, x, xb) || overlaps(yp, yb, w_packed, wb) || overlaps(yp, yb, bias, bb) ||
-      overlaps(yp, yb, cp, cb) || overlaps(cp, cb, x, xb) || overlaps(cp, cb, w_packed, wb) ||
-      overlaps(cp, cb, bias, bb))
-    return GSVK_E_ALIAS;
-
-  ConvArgs a{x, w_packed, bias, cur, y, static_cast<long>(c_in), static_cast<long>(c_out),
-             static_cast<long>(T), static_cast<long>(ldx), static_cast<long>(has_res ? ldc : 0),
-             static_cast<long>(has_y ? ldy : 0), static_cast<int>(k), 1, 0,
-             static_cast<int>((c_in + kChunk - 1) / kChunk),
-             static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad), epi, slope, false,
-             static_cast<int>(stride), static_cast<long>(Tout),
-             static_cast<int>((k - stride) / 2)};
-  const size_t va = esz * 4;
-  a.vec = stride == 1 && T >= 4 &&
-          (!has_y || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % va == 0)) &&
-          (!has_res || (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(cur) % va == 0));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == GSVK_F16) return launch_plan<kXF16>(a, st);
-  return round_x ? launch_plan<kXRound>(a, st) : launch_plan<kXSplit>(a, st);
+  ConvArgs a{};
+  a.x = x, a.wp = w_packed, a.bias = bias, a.cur = cur, a.res = res, a.y = y;
+  a.cin = static_cast<long>(c_in), a.cout = static_cast<long>(c_out), a.T = static_cast<long>(T);
+  a.ldx = static_cast<long>(ldx), a.ldc = static_cast<long>(ldc), a.ldy = static_cast<long>(ldy);
+  a.k = static_cast<int>(k), a.dil = 1, a.pad = 0;
+  a.nch = static_cast<int>((c_in + kChunk - 1) / kChunk);
+  a.opad = static_cast<int>((c_out + kOPad - 1) / kOPad * kOPad);
+  a.epi = epi, a.slope = slope;
+  a.up = static_cast<int>(stride), a.Tout = static_cast<long>(T * stride);
+  a.pad_t = static_cast<int>((k - stride) / 2);
+  return conv_entry(a, dtype, round_x, T, T * stride,
+                    gsvk_convt1d_packed_elems(c_out, c_in, k, stride) * 2,
+                    static_cast<hipStream_t>(stream));
 }

@@ -1,4 +1,5 @@
-"""ctypes binding of libgsvk.so, the C ABI declared in include/gsvk.h and include/gsvk_t2s.h.
+"""ctypes binding of libgsvk.so, the C ABI declared in include/gsvk.h, gsvk_t2s.h, gsvk_gsv.h and
+gsvk_sovits.h.
 
 The library is the product; this module only marshals arguments. Device buffers are passed as
 torch tensors (for their data pointers and strides) or as raw integer addresses. Every call checks
@@ -15,7 +16,8 @@ F32, F16, BF16 = 0, 1, 2
 I64, I32 = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_LEAKY_RELU = 0, 1, 2, 3
 OK, E_NULL, E_SIZE, E_DTYPE, E_ALIAS, E_ARG, E_HIP, E_FORMAT, E_IO = 0, -1, -2, -3, -4, -5, -6, -7, -8
-CONV_EPI_BIAS, CONV_EPI_LRELU, CONV_EPI_RES_LRELU, CONV_EPI_RES = 0, 1, 2, 3
+CONV_EPI_BIAS, CONV_EPI_LRELU, CONV_EPI_RES_LRELU, CONV_EPI_RES, CONV_EPI_DUAL, CONV_EPI_TANH = \
+    0, 1, 2, 3, 4, 5
 
 # Every exported symbol of the C ABI with (restype, argtypes).
 _vp, _sz, _i, _f, _d = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_double
@@ -30,12 +32,12 @@ SIGNATURES = {
     "gsvk_decode_attention": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz,
                                    _sz, _vp, _sz, _vp, _vp]),
     "gsvk_decode_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
-    "gsvk_conv1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
-                         _sz, _vp]),
+    "gsvk_conv1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                         _sz, _sz, _vp]),
     "gsvk_conv1d_packed_elems": (_sz, [_sz, _sz, _sz]),
     "gsvk_conv1d_pack": (_i, [_vp, _sz, _sz, _sz, _vp, _sz, _vp]),
-    "gsvk_convt1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _sz,
-                          _sz, _vp]),
+    "gsvk_convt1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                          _sz, _sz, _vp]),
     "gsvk_convt1d_packed_elems": (_sz, [_sz, _sz, _sz, _sz]),
     "gsvk_convt1d_pack": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp]),
     "gsvk_groupnorm_gelu": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _d, _i, _vp]),
@@ -66,6 +68,9 @@ SIGNATURES = {
     "gsvk_gsv_upload": (_i, [_vp, _i, _vp, _sz, _vp]),
     "gsvk_gsv_device_ptr": (_vp, [_vp, _i, _vp, _sz]),
     "gsvk_t2s_decode_create": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "gsvk_sovits_decoder_workspace_bytes": (_sz, [_vp]),
+    "gsvk_sovits_decoder_eager": (_i, [_vp, _vp]),
+    "gsvk_sovits_decoder_create": (_i, [_vp, ctypes.POINTER(_vp)]),
 }
 
 
@@ -171,15 +176,16 @@ def conv1d_pack(w, stream=None):
 
 
 def conv1d(x, wp, c_out, k, y=None, bias=None, dilation=1, epi=CONV_EPI_BIAS, slope=0.1, cur=None,
-           round_x=False, stream=None, check=True):
+           round_x=False, stream=None, check=True, res=None):
     """SoVITS Conv1d on channel-major x [c_in, T] with packed weights (conv1d_pack) and a fused
-    epilogue (CONV_EPI_*); y / cur [c_out, T] of x's dtype."""
+    epilogue (CONV_EPI_*); y / cur / res [c_out, T] of x's dtype (res: the residual source of the
+    RES epilogues when it is not cur itself; it shares cur's row stride)."""
     c_in, T, ldx = _rows(x)
     ldy = _rows(y)[2] if y is not None else 0
     ldc = _rows(cur)[2] if cur is not None else 0
     rc = lib().gsvk_conv1d(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(wp), _ptr(bias), epi,
-                           slope, _ptr(cur), ldc, _ptr(y), ldy, c_in, c_out, T, k, dilation,
-                           _stream(stream))
+                           slope, _ptr(cur), _ptr(res), ldc, _ptr(y), ldy, c_in, c_out, T, k,
+                           dilation, _stream(stream))
     return _check("gsvk_conv1d", rc) if check else rc
 
 
@@ -196,12 +202,12 @@ class Conv1d:
                                                            device=w16.device)
 
     def forward(self, x, y=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None, round_x=False,
-                stream=None):
+                stream=None, res=None):
         import torch
         if y is None and epi != CONV_EPI_RES:
             y = torch.empty(self.out_c, x.shape[1], dtype=x.dtype, device=x.device)
         conv1d(x, self.wp, self.out_c, self.k, y, self.b, self.dilation, epi, slope, cur, round_x,
-               stream)
+               stream, res=res)
         return y
 
 
@@ -218,15 +224,15 @@ def convt1d_pack(w, stride, stream=None):
 
 
 def convt1d(x, wp, c_out, k, stride, y=None, bias=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None,
-            round_x=False, stream=None, check=True):
+            round_x=False, stream=None, check=True, res=None):
     """SoVITS ConvTranspose1d on x [c_in, T] with packed weights (convt1d_pack) and a fused
-    epilogue; y / cur [c_out, T * stride]."""
+    epilogue; y / cur / res [c_out, T * stride]."""
     c_in, T, ldx = _rows(x)
     ldy = _rows(y)[2] if y is not None else 0
     ldc = _rows(cur)[2] if cur is not None else 0
     rc = lib().gsvk_convt1d(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(wp), _ptr(bias), epi,
-                            slope, _ptr(cur), ldc, _ptr(y), ldy, c_in, c_out, T, k, stride,
-                            _stream(stream))
+                            slope, _ptr(cur), _ptr(res), ldc, _ptr(y), ldy, c_in, c_out, T, k,
+                            stride, _stream(stream))
     return _check("gsvk_convt1d", rc) if check else rc
 
 
@@ -244,12 +250,12 @@ class ConvT1d:
                                                            device=w16.device)
 
     def forward(self, x, y=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None, round_x=False,
-                stream=None):
+                stream=None, res=None):
         import torch
         if y is None and epi != CONV_EPI_RES:
             y = torch.empty(self.out_c, x.shape[1] * self.stride_u, dtype=x.dtype, device=x.device)
         convt1d(x, self.wp, self.out_c, self.k, self.stride_u, y, self.b, epi, slope, cur, round_x,
-                stream)
+                stream, res=res)
         return y
 
 
@@ -265,15 +271,17 @@ class ResBlock1:
 class GeneratorStage:
     """One stage of the reference's Generator::forward (dec.hpp:283-336) on the GPU, with every
     element-wise pass fused into a neighbouring kernel:
-      y = ups(x)                                  x arrives already LeakyReLU'd (fused into the
-                                                  previous stage's branch mean, dec.hpp:284)
-      t_in = lrelu(y, 0.1)                        the first pair's input, shared by the branches
+      y = ups(x), t_in = lrelu(y, 0.1)            one launch (CONV_EPI_DUAL); x arrives already
+                                                  LeakyReLU'd (the previous stage's branch mean,
+                                                  dec.hpp:284)
       for each ResBlock j: cur_j = y; for each pair m:
           t_a = lrelu(convs1[m](t_in))            conv + leaky_relu_io (dec.hpp:323-324)
           cur_j += convs2[m](t_a); t_in = lrelu(cur_j)   conv + add_inplace + next leaky_relu_write
+                                                  (the first pair reads y as its residual and
+                                                  writes cur_j: no copy of y)
       out = lrelu(mean_j cur_j, slope_next)       mul_write / add_scaled_inplace + the next stage's
                                                   leaky_relu_io (dec.hpp:328-336, 284 or 342)
-    Launches: 1 upsampler, 1 LeakyReLU, 3 copies, 18 convolutions, 1 branch mean."""
+    Launches: 1 upsampler, 18 convolutions, 1 branch mean."""
 
     def __init__(self, ups, resblocks):
         self.ups = ups
@@ -291,22 +299,110 @@ class GeneratorStage:
     def forward(self, x, out, slope_next=0.1, round_x=False, stream=None):
         y, t_in0, t_in, t_a, curs = self._buffers(self.ups.out_c, x.shape[1] * self.ups.stride_u,
                                                   x.dtype, x.device)
-        self.ups.forward(x, y, round_x=round_x, stream=stream)
-        leaky_relu(y, t_in0, 0.1, stream=stream)
+        self.ups.forward(x, y, epi=CONV_EPI_DUAL, slope=0.1, cur=t_in0, round_x=round_x,
+                         stream=stream)
         for rb, cur in zip(self.resblocks, curs):
-            scaled_add(None, y, cur, 1.0, stream=stream)  # cur_j = y, on the same stream
-            src = t_in0
+            src, res = t_in0, y
             for m, (c1, c2) in enumerate(zip(rb.convs1, rb.convs2)):
                 c1.forward(src, t_a, epi=CONV_EPI_LRELU, slope=0.1, round_x=round_x, stream=stream)
-                if m + 1 < len(rb.convs2):
-                    c2.forward(t_a, t_in, epi=CONV_EPI_RES_LRELU, slope=0.1, cur=cur,
-                               round_x=round_x, stream=stream)
-                    src = t_in
-                else:
-                    c2.forward(t_a, None, epi=CONV_EPI_RES, cur=cur, round_x=round_x,
-                               stream=stream)
+                last = m + 1 == len(rb.convs2)
+                c2.forward(t_a, None if last else t_in,
+                           epi=CONV_EPI_RES if last else CONV_EPI_RES_LRELU, slope=0.1, cur=cur,
+                           res=res, round_x=round_x, stream=stream)
+                src, res = t_in, None
         resblock_branch_mean(curs, None, out, True, slope_next, stream=stream)
         return out
+
+
+class SovitsStage(ctypes.Structure):
+    """gsvk_sovits_stage: one upsampler and its three ResBlock1s (packed weights, fp32 biases)."""
+    _fields_ = [
+        ("c_in", _sz), ("c_out", _sz), ("ups_k", _sz), ("ups_u", _sz), ("ups_w", _vp),
+        ("ups_b", _vp), ("res_k", _sz * 3), ("res_dil", _sz * 3), ("w1", (_vp * 3) * 3),
+        ("b1", (_vp * 3) * 3), ("w2", (_vp * 3) * 3), ("b2", (_vp * 3) * 3),
+    ]
+
+
+class SovitsDecoderDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int), ("round_x", ctypes.c_int), ("frames", _sz), ("c_z", _sz),
+        ("c0", _sz), ("pre_k", _sz), ("pre_w", _vp), ("pre_b", _vp), ("g_in", _sz),
+        ("cond_w", _vp), ("cond_b", _vp), ("n_stages", _sz),
+        ("stage", ctypes.POINTER(SovitsStage)), ("post_k", _sz), ("post_w", _vp), ("z", _vp),
+        ("ge", _vp), ("out", _vp), ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class SovitsDecoder:
+    """The whole SoVITS decoder (Generator::forward, dec.hpp:264-345) over one set of device
+    buffers: conv_pre (+ cond(ge) folded into its bias) and LeakyReLU, the GeneratorStages, the final
+    LeakyReLU(0.01), conv_post and tanh, as gsvk_sovits_decoder_* launches (a HIP graph unless
+    graph=False). conv_pre / cond / conv_post are Conv1d, stages GeneratorStage objects; z
+    [c_z, frames] fp32, ge [g_in] fp32 (one frame; None without cond), out [frames * prod(u)].
+    The workspace is this object's own device allocation."""
+
+    def __init__(self, conv_pre, cond, stages, conv_post, z, ge, out, round_x=False, graph=True):
+        import torch
+        self._keep = (conv_pre, cond, stages, conv_post, z, ge, out)
+        n = len(stages)
+        self._stages = (SovitsStage * n)()
+        for i, st in enumerate(stages):
+            S = self._stages[i]
+            S.c_in, S.c_out = st.ups.in_c, st.ups.out_c
+            S.ups_k, S.ups_u = st.ups.k, st.ups.stride_u
+            S.ups_w, S.ups_b = _ptr(st.ups.wp), _ptr(st.ups.b)
+            for j, rb in enumerate(st.resblocks):
+                S.res_k[j] = rb.convs1[0].k
+                for m in range(3):
+                    S.res_dil[m] = rb.convs1[m].dilation
+                    S.w1[j][m], S.b1[j][m] = _ptr(rb.convs1[m].wp), _ptr(rb.convs1[m].b)
+                    S.w2[j][m], S.b2[j][m] = _ptr(rb.convs2[m].wp), _ptr(rb.convs2[m].b)
+        d = SovitsDecoderDesc()
+        d.dtype, d.round_x = dtype_code(z), int(round_x)
+        d.c_z, d.frames = z.shape
+        d.c0, d.pre_k = conv_pre.out_c, conv_pre.k
+        d.pre_w, d.pre_b = _ptr(conv_pre.wp), _ptr(conv_pre.b)
+        if cond is not None:
+            d.g_in, d.cond_w, d.cond_b = cond.in_c, _ptr(cond.wp), _ptr(cond.b)
+            d.ge = _ptr(ge)
+        d.n_stages = n
+        d.stage = ctypes.cast(self._stages, ctypes.POINTER(SovitsStage))
+        d.post_k, d.post_w = conv_post.k, _ptr(conv_post.wp)
+        d.z, d.out = _ptr(z), _ptr(out)
+        need = lib().gsvk_sovits_decoder_workspace_bytes(ctypes.byref(d))
+        if need == 0:
+            raise GsvkError("gsvk_sovits_decoder_workspace_bytes", E_SIZE)
+        self.ws = torch.empty(need, dtype=torch.uint8, device=z.device)
+        d.workspace, d.workspace_bytes = self.ws.data_ptr(), need
+        self.desc = d
+        self.handle = None
+        if graph:
+            h = _vp()
+            _check("gsvk_sovits_decoder_create",
+                   lib().gsvk_sovits_decoder_create(ctypes.byref(d), ctypes.byref(h)))
+            self.handle = h
+
+    @property
+    def launches(self):
+        return lib().gsvk_t2s_step_launches(self.handle) if self.handle else 0
+
+    def run(self, stream=None):
+        if self.handle:
+            return _check("gsvk_t2s_step_run", lib().gsvk_t2s_step_run(self.handle,
+                                                                       _stream(stream)))
+        return _check("gsvk_sovits_decoder_eager",
+                      lib().gsvk_sovits_decoder_eager(ctypes.byref(self.desc), _stream(stream)))
+
+    def close(self):
+        if self.handle:
+            lib().gsvk_t2s_step_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 _WS = {}

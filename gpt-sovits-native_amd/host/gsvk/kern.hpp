@@ -228,10 +228,11 @@ class Conv1d {
   }
 
   // y[out_c, T] = conv(x[in_c, T]) + b, then the epilogue (x and y must not overlap).
+  // res: the residual source of the RES epilogues when it is not cur itself.
   void forward(const float* x, float* y, size_t T, int epi = GSVK_CONV_EPI_BIAS,
-               float slope = 0.1f, float* cur = nullptr) const {
-    gsvk::check(gsvk_conv1d(GSVK_F32, 0, x, T, w_packed, b, epi, slope, cur, T, y, T, in_c, out_c,
-                            T, k, dilation, gsvk::current_stream()),
+               float slope = 0.1f, float* cur = nullptr, const float* res = nullptr) const {
+    gsvk::check(gsvk_conv1d(GSVK_F32, 0, x, T, w_packed, b, epi, slope, cur, res, T, y, T, in_c,
+                            out_c, T, k, dilation, gsvk::current_stream()),
                 "gsv::sovits::Conv1d::forward");
   }
 };
@@ -261,8 +262,8 @@ class ConvT1d {
   }
 
   void forward(const float* x, float* y, size_t T, int epi = GSVK_CONV_EPI_BIAS,
-               float slope = 0.1f, float* cur = nullptr) const {
-    gsvk::check(gsvk_convt1d(GSVK_F32, 0, x, T, w_packed, b, epi, slope, cur, T * stride_u, y,
+               float slope = 0.1f, float* cur = nullptr, const float* res = nullptr) const {
+    gsvk::check(gsvk_convt1d(GSVK_F32, 0, x, T, w_packed, b, epi, slope, cur, res, T * stride_u, y,
                              T * stride_u, in_c, out_c, T, k, stride_u, gsvk::current_stream()),
                 "gsv::sovits::ConvT1d::forward");
   }

@@ -1,0 +1,189 @@
+// sovits_decoder.cpp — the SoVITS decoder (Generator::forward, src/sovits/dec.hpp:264-345) issued
+// through the C ABI as a fixed sequence of fused convolution launches, eager or recorded into a HIP
+// graph (gsvk_sovits_decoder_*).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gsvk.h"
+#include "gsvk_sovits.h"
+
+namespace {
+
+constexpr size_t kAlignElems = 64;  // 256-byte alignment of every workspace slot (fp32)
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Workspace layout in fp32 elements: cv [c0], bias [c0], then 8 activation slots of `slot`
+// elements each: X (stage input, then the stage output), Y (upsampler output, the first residual),
+// TIN0 (lrelu(Y)), TIN (the next pair's LeakyReLU input), TA (the pair's middle activation) and
+// CUR0..CUR2 (the three branch accumulators).
+enum Slot { kX, kY, kTin0, kTin, kTa, kCur0, kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS };
+
+struct Layout {
+  size_t vec = 0;   // elements of cv and of bias (c0 rounded up)
+  size_t slot = 0;  // elements of one activation slot
+  size_t t_out = 0; // samples of the output
+  size_t bytes = 0;
+};
+
+// The shapes a valid descriptor must have (no buffer pointers needed) and the workspace layout.
+int shapes(const gsvk_sovits_decoder_desc* d, Layout* lay) {
+  if (!d || !d->stage) return GSVK_E_NULL;
+  if (d->dtype != GSVK_F32) return GSVK_E_DTYPE;
+  if (d->frames == 0 || d->c_z == 0 || d->c0 == 0 || d->pre_k == 0 || d->post_k == 0 ||
+      d->n_stages == 0 || d->n_stages > GSVK_SOVITS_MAX_STAGES)
+    return GSVK_E_SIZE;
+  size_t c = d->c0, T = d->frames, slot = d->c0 * d->frames;
+  for (size_t s = 0; s < d->n_stages; ++s) {
+    const gsvk_sovits_stage& S = d->stage[s];
+    if (S.c_in != c || S.c_out == 0 || S.ups_k == 0 || S.ups_u == 0) return GSVK_E_SIZE;
+    for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS; ++j)
+      if (S.res_k[j] == 0) return GSVK_E_SIZE;
+    for (size_t m = 0; m < GSVK_SOVITS_PAIRS; ++m)
+      if (S.res_dil[m] == 0) return GSVK_E_SIZE;
+    if (T > SIZE_MAX / S.ups_u) return GSVK_E_SIZE;
+    c = S.c_out;
+    T *= S.ups_u;
+    if (T > SIZE_MAX / c) return GSVK_E_SIZE;
+    if (c * T > slot) slot = c * T;
+  }
+  lay->vec = round_up(d->c0, kAlignElems);
+  lay->slot = round_up(slot, kAlignElems);
+  lay->t_out = T;
+  if (lay->slot > (SIZE_MAX / sizeof(float) - 2 * lay->vec) / kSlots) return GSVK_E_SIZE;
+  lay->bytes = (2 * lay->vec + kSlots * lay->slot) * sizeof(float);
+  return GSVK_OK;
+}
+
+// Shapes, every weight and buffer pointer, and the workspace; the convolutions check the rest
+// (aliasing, strides) themselves.
+int check_workspace(const gsvk_sovits_decoder_desc* d, Layout* lay) {
+  const int rc = shapes(d, lay);
+  if (rc) return rc;
+  if (!d->pre_w || !d->post_w || !d->z || !d->out) return GSVK_E_NULL;
+  if (d->g_in && (!d->cond_w || !d->ge)) return GSVK_E_NULL;
+  for (size_t s = 0; s < d->n_stages; ++s) {
+    const gsvk_sovits_stage& S = d->stage[s];
+    if (!S.ups_w) return GSVK_E_NULL;
+    for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS; ++j)
+      for (size_t m = 0; m < GSVK_SOVITS_PAIRS; ++m)
+        if (!S.w1[j][m] || !S.w2[j][m]) return GSVK_E_NULL;
+  }
+  if (!d->workspace) return GSVK_E_NULL;
+  if (reinterpret_cast<uintptr_t>(d->workspace) % 16 != 0) return GSVK_E_ARG;
+  if (d->workspace_bytes < lay->bytes) return GSVK_E_SIZE;
+  return GSVK_OK;
+}
+
+int count_launches(const gsvk_sovits_decoder_desc* d) {
+  // cond + bias fold (with conditioning), conv_pre, 20 per stage, conv_post
+  return (d->g_in ? 2 : 0) + 1 + 20 * static_cast<int>(d->n_stages) + 1;
+}
+
+// The launches of one decoder pass in Generator::forward's order.
+int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
+  const int dt = d->dtype, rx = d->round_x;
+  const float slope = 0.1f;  // LRELU_SLOPE (dec.hpp:284, 322, 324)
+  float* ws = static_cast<float*>(d->workspace);
+  float* cv = ws;
+  float* bias = ws + lay.vec;
+  float* slot[kSlots];
+  for (int i = 0; i < kSlots; ++i) slot[i] = ws + 2 * lay.vec + static_cast<size_t>(i) * lay.slot;
+  int rc;
+
+  // x = lrelu(conv_pre(z) + b_pre + cond(ge)[:, 0], 0.1): the broadcast add of dec.hpp:275-279
+  // folded into the bias, the stage-0 leaky_relu_io (dec.hpp:284) into the store.
+  const float* pre_bias = d->pre_b;
+  if (d->g_in) {
+    if ((rc = gsvk_conv1d(dt, rx, d->ge, 1, d->cond_w, d->cond_b, GSVK_CONV_EPI_BIAS, 0.f, nullptr,
+                          nullptr, 0, cv, 1, d->g_in, d->c0, 1, 1, 1, st)))
+      return rc;
+    if ((rc = gsvk_scaled_add(GSVK_F32, d->pre_b, cv, bias, d->c0, 1.f, st))) return rc;
+    pre_bias = bias;
+  }
+  size_t T = d->frames;
+  if ((rc = gsvk_conv1d(dt, rx, d->z, T, d->pre_w, pre_bias, GSVK_CONV_EPI_LRELU, slope, nullptr,
+                        nullptr, 0, slot[kX], T, d->c_z, d->c0, T, d->pre_k, 1, st)))
+    return rc;
+
+  for (size_t s = 0; s < d->n_stages; ++s) {
+    const gsvk_sovits_stage& S = d->stage[s];
+    const size_t C = S.c_out, Tu = T * S.ups_u;
+    // y = ups(x), t_in0 = lrelu(y)  (dec.hpp:285; the first pair's leaky_relu_write, dec.hpp:322)
+    if ((rc = gsvk_convt1d(dt, rx, slot[kX], T, S.ups_w, S.ups_b, GSVK_CONV_EPI_DUAL, slope,
+                           slot[kTin0], nullptr, Tu, slot[kY], Tu, S.c_in, C, T, S.ups_k, S.ups_u,
+                           st)))
+      return rc;
+    T = Tu;
+    const void* curs[GSVK_SOVITS_RESBLOCKS];
+    for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS; ++j) {
+      float* cur = slot[kCur0 + j];
+      curs[j] = cur;
+      const float* src = slot[kTin0];
+      const float* res = slot[kY];  // cur_j starts as a copy of y (dec.hpp:316): read it in place
+      for (size_t m = 0; m < GSVK_SOVITS_PAIRS; ++m) {
+        // t_a = lrelu(convs1[m](t_in))  (dec.hpp:323-324)
+        if ((rc = gsvk_conv1d(dt, rx, src, T, S.w1[j][m], S.b1[j][m], GSVK_CONV_EPI_LRELU, slope,
+                              nullptr, nullptr, 0, slot[kTa], T, C, C, T, S.res_k[j], S.res_dil[m],
+                              st)))
+          return rc;
+        // cur_j = res + convs2[m](t_a) (dec.hpp:325-326); t_in = lrelu(cur_j) for the next pair
+        const bool last = m + 1 == GSVK_SOVITS_PAIRS;
+        if ((rc = gsvk_conv1d(dt, rx, slot[kTa], T, S.w2[j][m], S.b2[j][m],
+                              last ? GSVK_CONV_EPI_RES : GSVK_CONV_EPI_RES_LRELU, slope, cur, res,
+                              T, last ? nullptr : slot[kTin], T, C, C, T, S.res_k[j], 1, st)))
+          return rc;
+        src = slot[kTin];
+        res = nullptr;  // in place from the second pair on
+      }
+    }
+    // x = lrelu(mean_j cur_j): mul_write / add_scaled_inplace (dec.hpp:328-333) with the next
+    // stage's leaky_relu_io (dec.hpp:284, 0.1) or the final one (dec.hpp:342, 0.01).
+    const float next_slope = s + 1 < d->n_stages ? slope : 0.01f;
+    if ((rc = gsvk_resblock_branch_mean(dt, curs, nullptr, GSVK_SOVITS_RESBLOCKS, slot[kX], C * T,
+                                        1, next_slope, st)))
+      return rc;
+  }
+  // out = tanh(conv_post(x))  (dec.hpp:343-344; conv_post has no bias)
+  return gsvk_conv1d(dt, rx, slot[kX], T, d->post_w, nullptr, GSVK_CONV_EPI_TANH, 0.f, nullptr,
+                     nullptr, 0, d->out, T, d->stage[d->n_stages - 1].c_out, 1, T, d->post_k, 1,
+                     st);
+}
+
+}  // namespace
+
+// The graph handle and its recorder live in t2s_decode_step.cpp.
+__attribute__((visibility("hidden"))) int gsvk_record_graph_(
+    int (*issue_fn)(const void*, hipStream_t), const void* ctx, int launches,
+    gsvk_t2s_step** out);
+
+extern "C" size_t gsvk_sovits_decoder_workspace_bytes(const gsvk_sovits_decoder_desc* desc) {
+  Layout lay;
+  return shapes(desc, &lay) == GSVK_OK ? lay.bytes : 0;
+}
+
+extern "C" int gsvk_sovits_decoder_eager(const gsvk_sovits_decoder_desc* desc, void* stream) {
+  Layout lay;
+  const int rc = check_workspace(desc, &lay);
+  return rc ? rc : issue(desc, lay, stream);
+}
+
+extern "C" int gsvk_sovits_decoder_create(const gsvk_sovits_decoder_desc* desc,
+                                          gsvk_t2s_step** out) {
+  if (!out) return GSVK_E_NULL;
+  *out = nullptr;
+  Layout lay;
+  const int rc = check_workspace(desc, &lay);
+  if (rc) return rc;
+  struct Ctx {
+    const gsvk_sovits_decoder_desc* d;
+    Layout lay;
+  } ctx{desc, lay};
+  return gsvk_record_graph_(
+      [](const void* c, hipStream_t st) {
+        const Ctx* x = static_cast<const Ctx*>(c);
+        return issue(x->d, x->lay, st);
+      },
+      &ctx, count_launches(desc), out);
+}

@@ -147,6 +147,16 @@ int record(Issue issue, int launches, gsvk_t2s_step** out) {
   return GSVK_OK;
 }
 
+// The recorder for other drivers of this library (the SoVITS decoder): issue_fn(ctx, stream)
+// makes the launches.
+__attribute__((visibility("hidden"))) int gsvk_record_graph_(
+    int (*issue_fn)(const void*, hipStream_t), const void* ctx, int launches,
+    gsvk_t2s_step** out) {
+  if (!out) return GSVK_E_NULL;
+  *out = nullptr;
+  return record([issue_fn, ctx](hipStream_t st) { return issue_fn(ctx, st); }, launches, out);
+}
+
 extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_step** out) {
   if (!out) return GSVK_E_NULL;
   *out = nullptr;

@@ -51,6 +51,9 @@ typedef enum gsvk_conv_epi {
   GSVK_CONV_EPI_RES_LRELU = 2,  /* cur += conv + bias; y = lrelu(cur)  conv2, add_inplace, next
                                    leaky_relu_write (dec.hpp:325-326, 322) */
   GSVK_CONV_EPI_RES = 3,        /* cur += conv + bias (y unused)      a branch's last conv2 (dec.hpp:325-326) */
+  GSVK_CONV_EPI_DUAL = 4,       /* y = conv + bias and cur = lrelu(y)  upsampler + the first pair's
+                                   leaky_relu_write (dec.hpp:285, 322) */
+  GSVK_CONV_EPI_TANH = 5,       /* y = tanh(conv + bias)              conv_post then tanh (dec.hpp:343-344) */
 } gsvk_conv_epi;
 
 typedef enum gsvk_status {
@@ -159,8 +162,11 @@ size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t 
  * SoVITS Conv1d, same padding with dilation, and the ResBlock passes that follow it.
  *   v[o, t] = bias[o] + sum_{i < c_in, kk < k} w[o, i, kk] * x[i, t + kk*dilation - pad],
  *   pad = (k - 1) * dilation / 2, x = 0 outside [0, T); the output has T columns.
- *   epi (gsvk_conv_epi): BIAS y = v; LRELU y = lrelu(v, slope); RES_LRELU cur += v, y =
- *   lrelu(cur, slope) (from the fp32 sum); RES cur += v (y may be NULL).
+ *   epi (gsvk_conv_epi): BIAS y = v; LRELU y = lrelu(v, slope); RES_LRELU cur = r + v, y =
+ *   lrelu(cur, slope) (from the fp32 sum); RES cur = r + v (y may be NULL); DUAL y = v, cur =
+ *   lrelu(v, slope); TANH y = tanhf(v). For RES_LRELU / RES the residual r is read from `res`
+ *   (row stride ldc) or, when res is NULL or equal to cur, from cur itself (in place): a branch's
+ *   first pair can then add onto the stage input without copying it into cur first.
  * Replaces Conv1d::forward (src/sovits/conv1d.hpp:109-194: im2col, sgemm, add_bias) and, fused
  * into its store, the ResBlock passes after each convolution in Generator::forward
  * (src/sovits/dec.hpp:322-326: leaky_relu_io after conv1, add_inplace after conv2 and the next
@@ -171,13 +177,15 @@ size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t 
  * (round_x = 0, the reference's sgemm path; |x| < 65504) or rounded to fp16 (round_x = 1, as the
  * reference's AMX path packs them, conv1d.hpp:130-151); F16 storage rounds each output once.
  * (k - 1) * dilation <= 256. y and cur must not overlap x, the weights, the bias or each other
- * (the reference's in-place x == y goes through a copy; here the caller keeps them apart).
+ * (the reference's in-place x == y goes through a copy; here the caller keeps them apart); res may
+ * equal cur but must not otherwise overlap an output.
  * The sum is formed in the matrix cores' order: |y - ref| <= 1e-5 * max(1, max_t |ref[o, t]|)
  * against the fp32 reference (fp32 storage). Deterministic.
  * ------------------------------------------------------------------------------------------------ */
 int gsvk_conv1d(int dtype, int round_x, const void* x, size_t ldx, const uint16_t* w_packed,
-                const float* bias, int epi, float slope, void* cur, size_t ldc, void* y, size_t ldy,
-                size_t c_in, size_t c_out, size_t T, size_t k, size_t dilation, void* stream);
+                const float* bias, int epi, float slope, void* cur, const void* res, size_t ldc,
+                void* y, size_t ldy, size_t c_in, size_t c_out, size_t T, size_t k,
+                size_t dilation, void* stream);
 /* Elements (uint16_t) of the packed weights of a [c_out, c_in, k] filter bank (0 for a zero size).
  * Host only. */
 size_t gsvk_conv1d_packed_elems(size_t c_out, size_t c_in, size_t k);
@@ -190,7 +198,8 @@ int gsvk_conv1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k, uin
 /* ------------------------------------------------------------------------------------------------
  * SoVITS ConvTranspose1d (the upsampler), stride u, pad_t = (k - u) / 2, output length T * u:
  *   v[o, t] = bias[o] + sum over (j, d) with j*u + d - pad_t = t of sum_i w[i, o, d] * x[i, j]
- *   followed by the same epilogues as gsvk_conv1d (epi, slope, cur), on [c_out, T * u] outputs.
+ *   followed by the same epilogues as gsvk_conv1d (epi, slope, cur, res), on [c_out, T * u]
+ *   outputs.
  * Replaces ConvT1d::forward (src/sovits/conv1d.hpp:250-340: one sgemm per tap d, scatter-add into
  * y at j*u + d - pad, then the bias), computed here per output phase r = (t + pad_t) mod u as a
  * short convolution over x (ceil((k - r) / u) taps), all phases in one launch.
@@ -199,9 +208,9 @@ int gsvk_conv1d_pack(const uint16_t* w, size_t c_out, size_t c_in, size_t k, uin
  * ceil(k / u) <= 65. Same dtype / round_x / aliasing rules and tolerance as gsvk_conv1d.
  * ------------------------------------------------------------------------------------------------ */
 int gsvk_convt1d(int dtype, int round_x, const void* x, size_t ldx, const uint16_t* w_packed,
-                 const float* bias, int epi, float slope, void* cur, size_t ldc, void* y,
-                 size_t ldy, size_t c_in, size_t c_out, size_t T, size_t k, size_t stride,
-                 void* stream);
+                 const float* bias, int epi, float slope, void* cur, const void* res, size_t ldc,
+                 void* y, size_t ldy, size_t c_in, size_t c_out, size_t T, size_t k,
+                 size_t stride, void* stream);
 /* Elements of the packed transposed filter bank (0 for a zero size or k < stride). Host only. */
 size_t gsvk_convt1d_packed_elems(size_t c_out, size_t c_in, size_t k, size_t stride);
 /* Pack a torch-layout [c_in, c_out, k] fp16 ConvTranspose1d filter bank (the .gsv layout;

@@ -354,6 +354,8 @@ int oracle_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const 
  *   0: y                                   1: leaky_relu_io(y, slope)      (dec.hpp:323-324)
  *   2: cur += y; y_out = lrelu(cur, slope) (add_inplace then the next leaky_relu_write, 322-326)
  *   3: cur += y                            (add_inplace only: the branch's last pair)
+ *   4: y, and cur = lrelu(y, slope)        (the upsampler's output and the first pair's input)
+ *   5: tanh(y)                             (conv_post then std::tanh, dec.hpp:343-344)
  * The GEMM sums over K in order with one rounding per step (fmaf); Accelerate's sgemm order is not
  * published, so parity with it is tolerance-based in any case.
  * --------------------------------------------------------------------------------------------- */
@@ -374,6 +376,13 @@ static int conv_epilogue(int dtype, float* row, size_t o, int epi, float slope, 
       oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
     }
     free(c);
+  } else if (epi == 4) {  /* y = v; cur = lrelu(v): the upsampler and the first pair's input */
+    oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
+    for (size_t t = 0; t < n; ++t) row[t] = leaky(row[t], slope);
+    oracle_from_f32(dtype, row, row_ptr_w(cur, dtype, o * ldc), n);
+  } else if (epi == 5) {  /* y = tanh(v): conv_post then std::tanh (dec.hpp:343-344) */
+    for (size_t t = 0; t < n; ++t) row[t] = tanhf(row[t]);
+    oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
   } else {
     oracle_from_f32(dtype, row, row_ptr_w(y, dtype, o * ldy), n);
   }

@@ -202,10 +202,12 @@ def conv1d(dt, x, w, bias=None, dil=1, epi=0, slope=0.1, cur=None):
     T = x.shape[1]
     y = np.zeros((cout, T), dtype=storage_dtype(dt))
     c = None if cur is None else np.ascontiguousarray(cur).copy()
+    if epi == 4:
+        c = np.zeros((cout, T), dtype=storage_dtype(dt))
     rc = lib().oracle_conv1d(dt, _p(x), T, _p(w), _p(bias), epi, slope, _p(c), T, _p(y), T, cin,
                              cout, T, k, dil)
     assert rc == 0
-    return (y, c) if epi in (2, 3) else y
+    return (y, c) if epi in (2, 3, 4) else y
 
 
 def convt1d(dt, x, w, u, bias=None, epi=0, slope=0.1, cur=None):
@@ -217,10 +219,12 @@ def convt1d(dt, x, w, u, bias=None, epi=0, slope=0.1, cur=None):
     T = x.shape[1]
     y = np.zeros((cout, T * u), dtype=storage_dtype(dt))
     c = None if cur is None else np.ascontiguousarray(cur).copy()
+    if epi == 4:
+        c = np.zeros((cout, T * u), dtype=storage_dtype(dt))
     rc = lib().oracle_convt1d(dt, _p(x), T, _p(w), _p(bias), epi, slope, _p(c), T * u, _p(y),
                               T * u, cin, cout, T, k, u)
     assert rc == 0
-    return (y, c) if epi in (2, 3) else y
+    return (y, c) if epi in (2, 3, 4) else y
 
 
 def softmax(x):

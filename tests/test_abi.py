@@ -16,7 +16,7 @@ import gsvk
 
 def _declared_functions():
     names = []
-    for h in ("gsvk.h", "gsvk_t2s.h", "gsvk_gsv.h"):
+    for h in ("gsvk.h", "gsvk_t2s.h", "gsvk_gsv.h", "gsvk_sovits.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(gsvk_\w+)\s*\(", text, flags=re.M)
@@ -147,12 +147,17 @@ def test_conv_validation(gsvk_lib):
     assert gsvk_lib.gsvk_conv1d_packed_elems(0, 16, 3) == 0
     assert gsvk_lib.gsvk_conv1d_packed_elems(65, 33, 1) == 2 * 1 * 128 * 32
 
-    def call(dt=0, x=A, ldx=100, w=B, bias=None, epi=0, cur=None, ldc=0, y=C, ldy=100, cin=16,
-             cout=8, T=100, k=3, dil=1):
-        return f(dt, 0, x, ldx, w, bias, epi, 0.1, cur, ldc, y, ldy, cin, cout, T, k, dil, None)
+    def call(dt=0, x=A, ldx=100, w=B, bias=None, epi=0, cur=None, res=None, ldc=0, y=C, ldy=100,
+             cin=16, cout=8, T=100, k=3, dil=1):
+        return f(dt, 0, x, ldx, w, bias, epi, 0.1, cur, res, ldc, y, ldy, cin, cout, T, k, dil,
+                 None)
 
     assert call(dt=2) == gsvk.E_DTYPE           # bf16 activations are not a reference input
-    assert call(epi=4) == gsvk.E_DTYPE
+    assert call(epi=6) == gsvk.E_DTYPE
+    assert call(epi=4, cur=None) == gsvk.E_NULL   # the dual epilogue writes cur too
+    assert call(epi=2, cur=0x700000, ldc=100, res=0x700000 + 8) == gsvk.E_ALIAS  # res inside cur
+    assert call(epi=2, cur=0x700000, ldc=100, res=C + 8) == gsvk.E_ALIAS          # res inside y
+    assert call(epi=4, cur=C + 64, ldc=100) == gsvk.E_ALIAS                        # cur over y
     assert call(x=None) == gsvk.E_NULL
     assert call(w=None) == gsvk.E_NULL
     assert call(y=None) == gsvk.E_NULL
@@ -184,7 +189,7 @@ def test_convt_validation(gsvk_lib):
 
     def call(dt=0, x=A, ldx=100, w=B, epi=0, cur=None, ldc=0, y=C, ldy=800, cin=16, cout=8, T=100,
              k=16, u=8):
-        return f(dt, 0, x, ldx, w, None, epi, 0.1, cur, ldc, y, ldy, cin, cout, T, k, u, None)
+        return f(dt, 0, x, ldx, w, None, epi, 0.1, cur, None, ldc, y, ldy, cin, cout, T, k, u, None)
 
     assert call(dt=2) == gsvk.E_DTYPE
     assert call(x=None) == gsvk.E_NULL
@@ -227,6 +232,77 @@ def test_t2s_step_validation(gsvk_lib):
     assert gsvk_lib.gsvk_t2s_step_run(None, None) == gsvk.E_NULL
     assert gsvk_lib.gsvk_t2s_step_launches(None) == 0
     gsvk_lib.gsvk_t2s_step_destroy(None)
+
+
+def _decoder_desc(frames=500, c0=768, n_stages=5, fake=0x1000):
+    """A decoder descriptor of the reference's geometry (dec.hpp:54-75) with fake, never
+    dereferenced device addresses: every call below fails validation or is host-only."""
+    ups_u, ups_k = (10, 8, 2, 2, 2), (20, 16, 8, 2, 2)
+    stages = (gsvk.SovitsStage * n_stages)()
+    c = c0
+    for s in range(n_stages):
+        S = stages[s]
+        S.c_in, S.c_out, S.ups_k, S.ups_u = c, c // 2, ups_k[s], ups_u[s]
+        S.ups_w = S.ups_b = fake
+        for j, k in enumerate((3, 7, 11)):
+            S.res_k[j] = k
+            S.res_dil[j] = (1, 3, 5)[j]
+            for m in range(3):
+                S.w1[j][m] = S.b1[j][m] = S.w2[j][m] = S.b2[j][m] = fake
+        c //= 2
+    d = gsvk.SovitsDecoderDesc()
+    d.dtype, d.frames, d.c_z, d.c0, d.pre_k = gsvk.F32, frames, 192, c0, 7
+    d.pre_w = d.pre_b = d.cond_w = d.cond_b = d.post_w = d.z = d.ge = d.out = fake
+    d.g_in, d.n_stages, d.post_k = 1024, n_stages, 7
+    d.stage = ctypes.cast(stages, ctypes.POINTER(gsvk.SovitsStage))
+    return d, stages
+
+
+def test_sovits_decoder_workspace_and_validation(gsvk_lib):
+    d, keep = _decoder_desc()
+    # cv and the folded bias (768 each), 8 slots of the largest stage tensor (192 x 40000 = 7.68M)
+    want = (2 * 768 + 8 * 7_680_000) * 4
+    assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(ctypes.byref(d)) == want
+    assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(None) == 0
+    h = ctypes.c_void_p()
+    assert gsvk_lib.gsvk_sovits_decoder_create(ctypes.byref(d), None) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_sovits_decoder_create(None, ctypes.byref(h)) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_sovits_decoder_eager(ctypes.byref(d), None) == gsvk.E_NULL  # workspace
+    d.workspace, d.workspace_bytes = 0x10000, want - 4
+    assert gsvk_lib.gsvk_sovits_decoder_eager(ctypes.byref(d), None) == gsvk.E_SIZE
+    assert gsvk_lib.gsvk_sovits_decoder_create(ctypes.byref(d), ctypes.byref(h)) == gsvk.E_SIZE
+    assert not h.value
+    d.workspace, d.workspace_bytes = 0x10008, want  # not 16-byte aligned
+    assert gsvk_lib.gsvk_sovits_decoder_eager(ctypes.byref(d), None) == gsvk.E_ARG
+    d.workspace = 0x10000
+
+    def bad(**kw):
+        e, k2 = _decoder_desc()
+        e.workspace, e.workspace_bytes = 0x10000, want
+        for key, v in kw.items():
+            if key.startswith("stage1_"):
+                setattr(k2[1], key[7:], v)
+            else:
+                setattr(e, key, v)
+        return gsvk_lib.gsvk_sovits_decoder_eager(ctypes.byref(e), None)
+
+    assert bad(dtype=gsvk.F16) == gsvk.E_DTYPE
+    assert bad(frames=0) == gsvk.E_SIZE
+    assert bad(n_stages=0) == gsvk.E_SIZE
+    assert bad(n_stages=9) == gsvk.E_SIZE
+    assert bad(stage1_c_in=100) == gsvk.E_SIZE       # stage chain: c_in must be the previous c_out
+    assert bad(stage1_ups_u=0) == gsvk.E_SIZE
+    assert bad(stage1_ups_w=None) == gsvk.E_NULL
+    assert bad(z=None) == gsvk.E_NULL
+    assert bad(ge=None) == gsvk.E_NULL               # g_in > 0 needs ge
+    assert bad(post_w=None) == gsvk.E_NULL
+    e, k2 = _decoder_desc()
+    k2[2].w2[1][2] = None
+    e.workspace, e.workspace_bytes = 0x10000, want
+    assert gsvk_lib.gsvk_sovits_decoder_eager(ctypes.byref(e), None) == gsvk.E_NULL
+    # shapes alone size the workspace: NULL buffers still give the figure
+    e, k2 = _decoder_desc(fake=0)
+    assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(ctypes.byref(e)) == want
 
 
 def test_host_mirror_header_compiles(tmp_path):

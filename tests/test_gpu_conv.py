@@ -91,8 +91,9 @@ def check_case(dt, cin, cout, T, k, dil, epi=0, round_x=False, use_bias=True, se
     b = b if use_bias else None
     xo = O.to_storage(F32, O.to_f32(F16, O.to_storage(F16, x))) if round_x else x
     ref0 = O.conv1d(dt, xo, w, b, dil)  # the plain convolution: the tolerance scale
-    want = O.conv1d(dt, xo, w, b, dil, epi=epi, slope=0.1, cur=cur if epi >= 2 else None)
-    y, c = run_gpu(dt, x, w, b, dil, epi, cur=cur if epi >= 2 else None, round_x=round_x,
+    has_res = epi in (gsvk.CONV_EPI_RES_LRELU, gsvk.CONV_EPI_RES)
+    want = O.conv1d(dt, xo, w, b, dil, epi=epi, slope=0.1, cur=cur if has_res else None)
+    y, c = run_gpu(dt, x, w, b, dil, epi, cur=cur if has_res else None, round_x=round_x,
                    ld_pad=ld_pad, y_offset=y_offset)
     tag = f"{what} dt={dt} {cin}->{cout} T={T} k={k} dil={dil} epi={epi} rx={round_x}"
     if epi in (2, 3):
@@ -301,3 +302,58 @@ def test_upsample_full_stage_windows(cin, cout, T, k, u):
         got, want = y[:, ga:gb], win[:, ga - wa * u:gb - wa * u]
         assert_conv_close(F32, got, want, want, f"convT full {cin}->{cout} T={T} cols [{ga}, {gb})")
     say(f"convT full stage {cin}->{cout} T={T} k={k} u={u}: windows ok")
+
+
+
+# ---- fused-pass epilogues used by the Generator stage ---------------------------------------------
+
+def test_dual_epilogue_and_res_input_are_bitwise_the_plain_paths():
+    """CONV_EPI_DUAL equals the plain convolution and a separate LeakyReLU of it, bit for bit; a
+    residual read from `res` equals the in-place form on a copy, bit for bit (same tiles, same
+    sums); for the transposed convolution as well."""
+    r = rng(400)
+    C, T = 48, 700
+    x, w, b, cur = make(r, C, C, T, 7)
+    xd, wd = dev(x, F32), dev(w, F16)
+    conv = gsvk.Conv1d(wd, devf(b), 3)
+    y0 = conv.forward(xd)
+    y4 = torch.empty_like(y0)
+    l4 = torch.empty_like(y0)
+    conv.forward(xd, y4, epi=gsvk.CONV_EPI_DUAL, slope=0.1, cur=l4)
+    lr = torch.empty_like(y0)
+    gsvk.leaky_relu(y0, lr, 0.1)
+    torch.cuda.synchronize()
+    assert torch.equal(y4.view(torch.int32), y0.view(torch.int32))
+    assert torch.equal(l4.view(torch.int32), lr.view(torch.int32))
+    res = dev(cur, F32)
+    c_a = res.clone()
+    y_a = torch.empty_like(y0)
+    conv.forward(xd, y_a, epi=gsvk.CONV_EPI_RES_LRELU, slope=0.1, cur=c_a)       # in place
+    c_b = torch.full_like(y0, float("nan"))
+    y_b = torch.empty_like(y0)
+    conv.forward(xd, y_b, epi=gsvk.CONV_EPI_RES_LRELU, slope=0.1, cur=c_b, res=res)
+    c_c = torch.full_like(y0, float("nan"))
+    conv.forward(xd, None, epi=gsvk.CONV_EPI_RES, cur=c_c, res=res)
+    torch.cuda.synchronize()
+    assert torch.equal(c_b.view(torch.int32), c_a.view(torch.int32))
+    assert torch.equal(y_b.view(torch.int32), y_a.view(torch.int32))
+    assert torch.equal(c_c.view(torch.int32), c_a.view(torch.int32))
+    assert torch.equal(res, dev(cur, F32))  # the residual source is only read
+    # transposed: dual epilogue
+    wt = (r.standard_normal((C, 24, 8)) / np.sqrt(C * 4)).astype(np.float16).view(np.uint16)
+    up = gsvk.ConvT1d(dev(wt, F16), devf(b[:24]), 2)
+    u0 = up.forward(xd)
+    u4, ul = torch.empty_like(u0), torch.empty_like(u0)
+    up.forward(xd, u4, epi=gsvk.CONV_EPI_DUAL, slope=0.1, cur=ul)
+    ulr = torch.empty_like(u0)
+    gsvk.leaky_relu(u0, ulr, 0.1)
+    torch.cuda.synchronize()
+    assert torch.equal(u4.view(torch.int32), u0.view(torch.int32))
+    assert torch.equal(ul.view(torch.int32), ulr.view(torch.int32))
+
+
+@pytest.mark.parametrize("dt", [F32, F16])
+def test_tanh_epilogue_conv_post(dt):
+    """conv_post (24 -> 1, k 7, no bias) with tanh fused (dec.hpp:343-344) against the oracle's
+    conv + tanhf; tolerance: the convolution's, since |tanh'| <= 1, plus one fp32 / fp16 step."""
+    check_case(dt, 24, 1, 3000, 7, 1, epi=gsvk.CONV_EPI_TANH, use_bias=False, seed=410)

@@ -206,3 +206,22 @@ def test_convt_epilogues():
     y2, c2 = O.convt1d(F32, x, w, u, b, epi=2, slope=0.1, cur=cur)
     c_want, t_in = O.resblock_add_lrelu(F32, cur, y0, 0.1)
     assert np.array_equal(c2, c_want) and np.array_equal(y2, t_in)
+
+
+def test_conv_dual_and_tanh_epilogues():
+    """epi 4 writes y and lrelu(y) (the upsampler output and the first pair's input); epi 5 is
+    conv_post's tanh, against numpy's tanh of the plain convolution (float64, 1 ulp band)."""
+    r = np.random.default_rng(11)
+    x = rnd(r, 6, 40)
+    w = (0.3 * r.standard_normal((4, 6, 7))).astype(np.float16).view(np.uint16)
+    b = rnd(r, 4, std=0.1)
+    y0 = O.conv1d(F32, x, w, b)
+    y4, c4 = O.conv1d(F32, x, w, b, epi=4, slope=0.1)
+    assert np.array_equal(y4, y0) and np.array_equal(c4, O.leaky_relu(F32, y0, 0.1))
+    y5 = O.conv1d(F32, x, w, b, epi=5).astype(np.float64)
+    want = np.tanh(y0.astype(np.float64))
+    assert np.all(np.abs(y5 - want) <= 2 * np.spacing(np.abs(want).astype(np.float32)) + 1e-30)
+    assert np.max(np.abs(y5 - y0)) > 0.01  # tanh is applied
+    yt, ct = O.convt1d(F32, x, w.reshape(6, 4, 7), 2, b, epi=4, slope=0.1)
+    assert np.array_equal(yt, O.convt1d(F32, x, w.reshape(6, 4, 7), 2, b))
+    assert np.array_equal(ct, O.leaky_relu(F32, yt, 0.1))
