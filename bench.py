@@ -511,14 +511,31 @@ def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
                          "note": "algorithmic flops; exact fp32 runs two fp16 products per term"}}
 
 
-def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5):
-    """The decoder's five Generator stages end to end (gsvk.GeneratorStage: upsampler, LeakyReLU,
-    3 ResBlocks x 3 fused conv pairs, branch mean + next LeakyReLU; 24 launches per stage), eager
-    launches on one stream, exact fp32. Per stage: the median of `reps` timed runs after one warm
-    run. Total = the 5 stages for 10 s of 32 kHz audio (conv_pre, cond and conv_post not included)."""
-    out, tot = [], 0.0
+def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=500):
+    """The decoder's five Generator stages (gsvk.GeneratorStage: upsampler with the LeakyReLU copy
+    fused, 3 ResBlocks x 3 fused conv pairs, branch mean + next LeakyReLU; 20 launches per stage)
+    timed one by one as eager launches, then the whole decoder (gsvk.SovitsDecoder: cond folded into
+    conv_pre's bias, conv_pre + LeakyReLU, the 5 stages, conv_post + tanh; 104 launches) replayed as
+    one HIP graph on z [192, frames]. Exact fp32, random-init weights of the reference's shapes.
+    Each figure is the median of `reps` timed runs after one warm run; 500 frames = 10 s of 32 kHz
+    audio."""
+    g = lambda *shape: torch.randn(*shape, device=dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            ts.append(s.elapsed_time(e) * 1e3)
+        return sorted(ts)[len(ts) // 2]
+
+    out, tot, stages = [], 0.0, []
     for (C, T), (cin_up, u, k_up) in zip(DECODER_GEOMETRIES[geometry], UPS[geometry]):
-        g = lambda *shape: torch.randn(*shape, device=dev)
         ups = gsvk.ConvT1d((g(cin_up, C, k_up) / (cin_up * k_up / u) ** 0.5).half(), g(C) * 0.05, u)
         blocks = []
         for k in RES_KERNELS:
@@ -526,26 +543,37 @@ def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5):
             blocks.append(gsvk.ResBlock1([w() for _ in range(3)], [g(C) * 0.05 for _ in range(3)],
                                          [w() for _ in range(3)], [g(C) * 0.05 for _ in range(3)]))
         stage = gsvk.GeneratorStage(ups, blocks)
+        stages.append(stage)
         x = g(cin_up, T // u)
         y = torch.empty(C, T, device=dev)
-        stage.forward(x, y)
-        torch.cuda.synchronize()
-        ts = []
-        for _ in range(reps):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            stage.forward(x, y)
-            e.record()
-            e.synchronize()
-            ts.append(s.elapsed_time(e) * 1e3)
-        us = sorted(ts)[len(ts) // 2]
+        us = timed(lambda: stage.forward(x, y))
         tot += us
-        out.append({"C": C, "T": T, "stage_us": round(us, 1), "launches": 24})
+        out.append({"C": C, "T": T, "stage_us": round(us, 1), "launches": 20})
         log(f"  generator stage {C}x{T}: {us:.1f} us end to end")
-        del stage, blocks, ups, x, y
+        del x, y
+        stage._buf = None  # the decoder below brings its own activations
         torch.cuda.empty_cache()
-    return {"geometry": geometry, "stages": out, "us_per_10s_audio": round(tot, 1),
-            "realtime_factor": round(10.0 / (tot * 1e-6), 1)}
+    c0, c_last, c_z, g_in = UPS[geometry][0][0], DECODER_GEOMETRIES[geometry][-1][0], 192, 1024
+    pre = gsvk.Conv1d((g(c0, c_z, 7) / (c_z * 7) ** 0.5).half(), g(c0) * 0.05)
+    cond = gsvk.Conv1d((g(c0, g_in, 1) / g_in ** 0.5).half(), g(c0) * 0.05)
+    post = gsvk.Conv1d((g(1, c_last, 7) / (c_last * 7) ** 0.5).half(), None)
+    z, ge = g(c_z, frames), g(g_in)
+    n_out = frames
+    for _, u, _ in UPS[geometry]:
+        n_out *= u
+    wav = torch.empty(n_out, device=dev)
+    dec = gsvk.SovitsDecoder(pre, cond, stages, post, z, ge, wav, graph=True)
+    dus = timed(dec.run)
+    audio_s = n_out / 32000.0
+    log(f"  whole decoder (graph, {dec.launches} launches): {dus:.1f} us for {audio_s:g} s of audio")
+    res = {"geometry": geometry, "stages": out, "stages_us_per_10s_audio": round(tot, 1),
+           "decoder": {"frames": frames, "samples": n_out, "launches": dec.launches,
+                       "graph": True, "us": round(dus, 1),
+                       "realtime_factor": round(audio_s / (dus * 1e-6), 1),
+                       "workspace_bytes": dec.ws.numel()}}
+    del dec, stages, pre, cond, post, z, ge, wav
+    torch.cuda.empty_cache()
+    return res
 
 
 # ---- whole T2S decode step ---------------------------------------------------------------------------

@@ -244,6 +244,27 @@ def test_groupnorm_edge_shapes(C, T, dt, gelu):
     assert_close(dt, host(X, dt), want, f"groupnorm {C}x{T}")
 
 
+@pytest.mark.parametrize("C,T,dt,params", [
+    (1031, 8000, F32, True),    # 4 channels per workgroup and a ragged tail: both register buffers
+    (600, 31999, F32, False),   # config 4's rows, no gamma / beta (1 / 0)
+    (777, 9000, F16, True),     # 16-bit rows, 4 chunks per thread
+])
+def test_groupnorm_many_channels_per_workgroup(C, T, dt, params):
+    """More channels than workgroups: each workgroup walks its channels through the two register
+    buffers and the LDS buffer, and ends on either buffer."""
+    say(f"groupnorm pipeline C={C} T={T} dt={dt} params={params}")
+    r = rng(C + T)
+    x = st(dt, r.standard_normal((C, T)) * 0.7 - 0.2)
+    g = (1 + 0.1 * r.standard_normal(C)).astype(np.float32) if params else None
+    b = (0.1 * r.standard_normal(C)).astype(np.float32) if params else None
+    want = O.groupnorm_gelu(dt, x, g, b, 1e-5)
+    X = dev(x, dt)
+    Y = torch.empty_like(X)
+    gsvk.groupnorm_gelu(X, devf(g) if params else None, devf(b) if params else None, Y, 1e-5)
+    sync()
+    assert_close(dt, host(Y, dt), want, f"groupnorm {C}x{T}")
+
+
 def test_groupnorm_out_of_phase_buffers_use_generic_path():
     r = rng(55)
     C, T = 4, 999
