@@ -561,17 +561,24 @@ def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=
     n_out = frames
     for _, u, _ in UPS[geometry]:
         n_out *= u
-    wav = torch.empty(n_out, device=dev)
-    dec = gsvk.SovitsDecoder(pre, cond, stages, post, z, ge, wav, graph=True)
-    dus = timed(dec.run)
     audio_s = n_out / 32000.0
-    log(f"  whole decoder (graph, {dec.launches} launches): {dus:.1f} us for {audio_s:g} s of audio")
-    res = {"geometry": geometry, "stages": out, "stages_us_per_10s_audio": round(tot, 1),
-           "decoder": {"frames": frames, "samples": n_out, "launches": dec.launches,
-                       "graph": True, "us": round(dus, 1),
-                       "realtime_factor": round(audio_s / (dus * 1e-6), 1),
-                       "workspace_bytes": dec.ws.numel()}}
-    del dec, stages, pre, cond, post, z, ge, wav
+    res = {"geometry": geometry, "stages": out, "stages_us_per_10s_audio": round(tot, 1)}
+    # exact fp32 (the reference's default numerics), fp32 with fp16-rounded convolution inputs
+    # (its AMX numerics), fp16 storage
+    for name, zz, rx in (("decoder", z, False), ("decoder_round_x", z, True),
+                         ("decoder_f16", z.half(), False)):
+        wav = torch.empty(n_out, dtype=zz.dtype, device=dev)
+        dec = gsvk.SovitsDecoder(pre, cond, stages, post, zz, ge, wav, round_x=rx, graph=True)
+        dus = timed(dec.run)
+        log(f"  whole {name} (graph, {dec.launches} launches): {dus:.1f} us for {audio_s:g} s of audio")
+        res[name] = {"frames": frames, "samples": n_out, "launches": dec.launches, "graph": True,
+                     "us": round(dus, 1), "realtime_factor": round(audio_s / (dus * 1e-6), 1),
+                     "workspace_bytes": dec.ws.numel(),
+                     "activations": "f16" if zz.dtype == torch.float16 else "f32",
+                     "round_x": rx}
+        del dec, wav
+        torch.cuda.empty_cache()
+    del stages, pre, cond, post, z, ge
     torch.cuda.empty_cache()
     return res
 

@@ -338,7 +338,8 @@ class SovitsDecoder:
     buffers: conv_pre (+ cond(ge) folded into its bias) and LeakyReLU, the GeneratorStages, the final
     LeakyReLU(0.01), conv_post and tanh, as gsvk_sovits_decoder_* launches (a HIP graph unless
     graph=False). conv_pre / cond / conv_post are Conv1d, stages GeneratorStage objects; z
-    [c_z, frames] fp32, ge [g_in] fp32 (one frame; None without cond), out [frames * prod(u)].
+    [c_z, frames] fp32 or fp16 (the activation dtype), ge [g_in] fp32 (one frame; None without
+    cond), out [frames * prod(u)] of z's dtype.
     The workspace is this object's own device allocation."""
 
     def __init__(self, conv_pre, cond, stages, conv_post, z, ge, out, round_x=False, graph=True):
@@ -363,6 +364,7 @@ class SovitsDecoder:
         d.c0, d.pre_k = conv_pre.out_c, conv_pre.k
         d.pre_w, d.pre_b = _ptr(conv_pre.wp), _ptr(conv_pre.b)
         if cond is not None:
+            assert ge.dtype == torch.float32, "ge is fp32 for either activation dtype"
             d.g_in, d.cond_w, d.cond_b = cond.in_c, _ptr(cond.wp), _ptr(cond.b)
             d.ge = _ptr(ge)
         d.n_stages = n

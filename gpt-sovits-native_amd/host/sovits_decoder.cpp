@@ -10,27 +10,27 @@
 
 namespace {
 
-constexpr size_t kAlignElems = 64;  // 256-byte alignment of every workspace slot (fp32)
+constexpr size_t kAlign = 256;  // bytes: alignment of every workspace region
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout in fp32 elements: cv [c0], bias [c0], then 8 activation slots of `slot`
-// elements each: X (stage input, then the stage output), Y (upsampler output, the first residual),
-// TIN0 (lrelu(Y)), TIN (the next pair's LeakyReLU input), TA (the pair's middle activation) and
-// CUR0..CUR2 (the three branch accumulators).
+// Workspace layout: cv [c0] and bias [c0] in fp32, then 8 activation slots of `slot` elements of the
+// activation dtype each: X (stage input, then the stage output), Y (upsampler output, the first
+// residual), TIN0 (lrelu(Y)), TIN (the next pair's LeakyReLU input), TA (the pair's middle
+// activation) and CUR0..CUR2 (the three branch accumulators).
 enum Slot { kX, kY, kTin0, kTin, kTa, kCur0, kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS };
 
 struct Layout {
-  size_t vec = 0;   // elements of cv and of bias (c0 rounded up)
-  size_t slot = 0;  // elements of one activation slot
-  size_t t_out = 0; // samples of the output
+  size_t vec_bytes = 0;   // bytes of cv and of bias (c0 floats, rounded up)
+  size_t slot_bytes = 0;  // bytes of one activation slot
+  size_t t_out = 0;       // samples of the output
   size_t bytes = 0;
 };
 
 // The shapes a valid descriptor must have (no buffer pointers needed) and the workspace layout.
 int shapes(const gsvk_sovits_decoder_desc* d, Layout* lay) {
   if (!d || !d->stage) return GSVK_E_NULL;
-  if (d->dtype != GSVK_F32) return GSVK_E_DTYPE;
+  if (d->dtype != GSVK_F32 && d->dtype != GSVK_F16) return GSVK_E_DTYPE;
   if (d->frames == 0 || d->c_z == 0 || d->c0 == 0 || d->pre_k == 0 || d->post_k == 0 ||
       d->n_stages == 0 || d->n_stages > GSVK_SOVITS_MAX_STAGES)
     return GSVK_E_SIZE;
@@ -48,11 +48,12 @@ int shapes(const gsvk_sovits_decoder_desc* d, Layout* lay) {
     if (T > SIZE_MAX / c) return GSVK_E_SIZE;
     if (c * T > slot) slot = c * T;
   }
-  lay->vec = round_up(d->c0, kAlignElems);
-  lay->slot = round_up(slot, kAlignElems);
+  const size_t esz = d->dtype == GSVK_F32 ? 4 : 2;
+  if (slot > (SIZE_MAX / 2) / esz / kSlots) return GSVK_E_SIZE;
+  lay->vec_bytes = round_up(d->c0 * sizeof(float), kAlign);
+  lay->slot_bytes = round_up(slot * esz, kAlign);
   lay->t_out = T;
-  if (lay->slot > (SIZE_MAX / sizeof(float) - 2 * lay->vec) / kSlots) return GSVK_E_SIZE;
-  lay->bytes = (2 * lay->vec + kSlots * lay->slot) * sizeof(float);
+  lay->bytes = 2 * lay->vec_bytes + kSlots * lay->slot_bytes;
   return GSVK_OK;
 }
 
@@ -85,19 +86,21 @@ int count_launches(const gsvk_sovits_decoder_desc* d) {
 int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
   const int dt = d->dtype, rx = d->round_x;
   const float slope = 0.1f;  // LRELU_SLOPE (dec.hpp:284, 322, 324)
-  float* ws = static_cast<float*>(d->workspace);
-  float* cv = ws;
-  float* bias = ws + lay.vec;
-  float* slot[kSlots];
-  for (int i = 0; i < kSlots; ++i) slot[i] = ws + 2 * lay.vec + static_cast<size_t>(i) * lay.slot;
+  char* ws = static_cast<char*>(d->workspace);
+  float* cv = reinterpret_cast<float*>(ws);
+  float* bias = reinterpret_cast<float*>(ws + lay.vec_bytes);
+  void* slot[kSlots];
+  for (int i = 0; i < kSlots; ++i)
+    slot[i] = ws + 2 * lay.vec_bytes + static_cast<size_t>(i) * lay.slot_bytes;
   int rc;
 
   // x = lrelu(conv_pre(z) + b_pre + cond(ge)[:, 0], 0.1): the broadcast add of dec.hpp:275-279
   // folded into the bias, the stage-0 leaky_relu_io (dec.hpp:284) into the store.
   const float* pre_bias = d->pre_b;
   if (d->g_in) {
-    if ((rc = gsvk_conv1d(dt, rx, d->ge, 1, d->cond_w, d->cond_b, GSVK_CONV_EPI_BIAS, 0.f, nullptr,
-                          nullptr, 0, cv, 1, d->g_in, d->c0, 1, 1, 1, st)))
+    // ge and cv are fp32 for either activation dtype: the fold is an fp32 bias
+    if ((rc = gsvk_conv1d(GSVK_F32, rx, d->ge, 1, d->cond_w, d->cond_b, GSVK_CONV_EPI_BIAS, 0.f,
+                          nullptr, nullptr, 0, cv, 1, d->g_in, d->c0, 1, 1, 1, st)))
       return rc;
     if ((rc = gsvk_scaled_add(GSVK_F32, d->pre_b, cv, bias, d->c0, 1.f, st))) return rc;
     pre_bias = bias;
@@ -118,10 +121,10 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
     T = Tu;
     const void* curs[GSVK_SOVITS_RESBLOCKS];
     for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS; ++j) {
-      float* cur = slot[kCur0 + j];
+      void* cur = slot[kCur0 + j];
       curs[j] = cur;
-      const float* src = slot[kTin0];
-      const float* res = slot[kY];  // cur_j starts as a copy of y (dec.hpp:316): read it in place
+      const void* src = slot[kTin0];
+      const void* res = slot[kY];  // cur_j starts as a copy of y (dec.hpp:316): read it in place
       for (size_t m = 0; m < GSVK_SOVITS_PAIRS; ++m) {
         // t_a = lrelu(convs1[m](t_in))  (dec.hpp:323-324)
         if ((rc = gsvk_conv1d(dt, rx, src, T, S.w1[j][m], S.b1[j][m], GSVK_CONV_EPI_LRELU, slope,

@@ -17,7 +17,8 @@
  * The folded broadcast rounds (W z + b_pre) + cv as W z + (b_pre + cv): within the convolution's
  * tolerance. Weights are the packed forms (gsvk_conv1d_pack / gsvk_convt1d_pack of the .gsv's fp16
  * [out, in, k] / [in, out, k] tensors); biases fp32. Activations of `dtype` (F32, the reference's,
- * or F16 storage); round_x as in gsvk_conv1d.
+ * or F16 storage: every stored activation rounded to fp16, arithmetic in fp32); round_x as in
+ * gsvk_conv1d (F32 only). ge, cv and the folded bias are fp32 for either dtype.
  */
 #ifndef GSVK_SOVITS_H
 #define GSVK_SOVITS_H
@@ -64,7 +65,7 @@ typedef struct gsvk_sovits_decoder_desc {
   size_t post_k;
   const uint16_t* post_w; /* packed conv_post (c_out of the last stage -> 1, no bias) */
   const void* z;  /* [c_z, frames], dtype */
-  const void* ge; /* [g_in] (one frame), dtype; NULL when g_in == 0 */
+  const void* ge; /* [g_in] fp32 (column 0 of the reference's ge); NULL when g_in == 0 */
   void* out;      /* [frames * prod(ups_u)], dtype */
   void* workspace; /* gsvk_sovits_decoder_workspace_bytes(desc) bytes, 16-byte aligned */
   size_t workspace_bytes;

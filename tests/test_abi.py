@@ -286,7 +286,11 @@ def test_sovits_decoder_workspace_and_validation(gsvk_lib):
                 setattr(e, key, v)
         return gsvk_lib.gsvk_sovits_decoder_eager(ctypes.byref(e), None)
 
-    assert bad(dtype=gsvk.F16) == gsvk.E_DTYPE
+    assert bad(dtype=gsvk.BF16) == gsvk.E_DTYPE
+    e, k2 = _decoder_desc()
+    e.dtype = gsvk.F16  # fp16 activation slots (2 bytes); cv and the folded bias stay fp32
+    assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(ctypes.byref(e)) == 2 * 768 * 4 + \
+        8 * 7_680_000 * 2
     assert bad(frames=0) == gsvk.E_SIZE
     assert bad(n_stages=0) == gsvk.E_SIZE
     assert bad(n_stages=9) == gsvk.E_SIZE

@@ -60,6 +60,36 @@ def oracle_decoder(m, z, ge, round_x=False):
     return O.conv1d(F32, q(x), m["post"].view(np.uint16), None, 1, epi=gsvk.CONV_EPI_TANH)[0]
 
 
+def oracle_decoder_f16(m, z, ge):
+    """The oracle chain with fp16 storage at the GPU's rounding points: each launch rounds what it
+    stores to fp16 once (its fused epilogue computed in fp32 first, as the oracle's fused conv
+    epilogues do), cond and the folded bias stay fp32."""
+    w_pre, b_pre = m["pre"]
+    bias = b_pre
+    if m["cond"] is not None:
+        w_c, b_c = m["cond"]
+        cv = O.conv1d(F32, ge[:, None], w_c.view(np.uint16), b_c, 1)[:, 0]
+        bias = (b_pre + cv).astype(np.float32)
+    x = O.conv1d(F16, O.to_storage(F16, z), w_pre.view(np.uint16), bias, 1,
+                 epi=gsvk.CONV_EPI_LRELU, slope=0.1)
+    n = len(m["stages"])
+    for s, ((w_up, b_up), rbs) in enumerate(m["stages"]):
+        y, t_in0 = O.convt1d(F16, x, w_up.view(np.uint16), UPS_U[s], b_up,
+                             epi=gsvk.CONV_EPI_DUAL, slope=0.1)
+        curs = []
+        for w1, b1, w2, b2 in rbs:
+            src, cur = t_in0, y
+            for k in range(3):
+                t_a = O.conv1d(F16, src, w1[k].view(np.uint16), b1[k], (1, 3, 5)[k],
+                               epi=gsvk.CONV_EPI_LRELU, slope=0.1)
+                epi = gsvk.CONV_EPI_RES if k == 2 else gsvk.CONV_EPI_RES_LRELU
+                src, cur = O.conv1d(F16, t_a, w2[k].view(np.uint16), b2[k], 1, epi=epi,
+                                    slope=0.1, cur=cur)
+            curs.append(cur)
+        x = O.resblock_branch_mean(F16, curs, None, True, 0.1 if s + 1 < n else 0.01)
+    return O.conv1d(F16, x, m["post"].view(np.uint16), None, 1, epi=gsvk.CONV_EPI_TANH)[0]
+
+
 class GpuDecoder:
     """Device objects of one decoder's weights (packed once)."""
 
@@ -126,6 +156,33 @@ def test_decoder_matches_oracle_chain(c_z, c0, g_in, frames, round_x):
     say(f"  max |d| {err.max():.2e} (tol {tol:g}), peak |out| {np.abs(want).max():.3f}")
     assert np.isfinite(got).all()
     assert err.max() <= tol
+
+
+def test_decoder_fp16_storage():
+    """fp16 activations (every stored activation rounded to fp16, arithmetic in fp32; ge, cond and
+    the folded bias in fp32) against the oracle chain with the same rounding points. The only
+    difference left is the fp32 summation order inside each convolution, which can move an fp16
+    rounding by one step (2^-11 relative) and carry it downstream: compared at |d| <= 4e-3 on the
+    tanh output (8 fp16 steps at |out| ~ 1). Also reported: the distance to the fp32 chain."""
+    r = np.random.default_rng(20250921)
+    m = make_decoder(r, 16, 64, 32)
+    frames = 12
+    z = r.standard_normal((16, frames)).astype(np.float32)
+    ge = r.standard_normal(32).astype(np.float32)
+    say("decoder fp16: oracle chains")
+    want = O.to_f32(F16, oracle_decoder_f16(m, z, ge)).astype(np.float64)
+    want32 = oracle_decoder(m, z, ge).astype(np.float64)
+    g = GpuDecoder(m)
+    zd = dev(O.to_storage(F16, z), F16)
+    out = torch.full((frames * 640,), float("nan"), dtype=torch.float16, device="cuda")
+    dec = g.bind(zd, devf(ge), out)
+    dec.run()
+    torch.cuda.synchronize()
+    got = O.to_f32(F16, host(out, F16)).astype(np.float64)
+    err = np.abs(got - want).max()
+    say(f"  max |d| vs fp16 chain {err:.2e}, vs fp32 chain {np.abs(got - want32).max():.2e}")
+    assert np.isfinite(got).all()
+    assert err <= 4e-3
 
 
 def test_decoder_full_shape_graph_eager_and_python_chain_agree():
