@@ -26,6 +26,7 @@
 // lo = f16(x - hi) separately: hi + lo equals x to about 2^-22 relative (|x| < 65504), and the
 // products with fp16 weights are exact in fp32. Sums are fp32 in the matrix cores' order.
 #include <algorithm>
+#include <type_traits>
 
 #include "gsvk_common.hpp"
 
@@ -34,6 +35,7 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
 
 enum XMode { kXF16 = 0, kXRound = 1, kXSplit = 2 };
 
@@ -237,22 +239,34 @@ __device__ __forceinline__ void finish4(const ConvArgs& a, const Map& m, long o,
   store4<DT>(a.y, yo, m.ostr, v, full, valid);
 }
 
+// Fragment shapes. FS = 16: v_mfma_f32_16x16x32_f16, one 32-channel step per MFMA (above). FS =
+// 32: v_mfma_f32_32x32x16_f16 on 32 t x 32 o fragments, two 16-channel halves h of the chunk per
+// step: operand A is a 32 t x 16 channel slice of X^T (lane l: position l & 31, the 8 channels of
+// group 2 h + (l >> 5)), operand B a 16 channel x 32 o slice of W^T (lane l: output row l & 31),
+// and the accumulator holds in lane l output row (l & 31) at positions 8 q + 4 (l >> 5) .. +3,
+// q = 0..3: four runs of four consecutive positions, one 16-byte store each. A wave tile of
+// 64 t x 64 o in 32-wide fragments reads a quarter fewer LDS bytes per multiply than 32 t x 64 o in
+// 16-wide ones, and each refill of LDS (x per chunk, weights per tap group) feeds twice the
+// matrix-core work of a workgroup.
+//
 // At least two waves per SIMD: the register budget is sized for them (every tile fits without
 // spilling; the compiler would otherwise keep two steps' fragments live).
-template <int XM, int NT, int NO, int HMAX>
+template <int XM, int NT, int NO, int HMAX, int FS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void conv1d_mfma(
     ConvArgs a) {
   constexpr int DT = storage_dt<XM>();
   constexpr int P = planes<XM>();
-  constexpr int TT = kWaves * 16 * NT;  // output columns of the workgroup
+  constexpr int TT = kWaves * FS * NT;  // output columns of the workgroup
   constexpr int TTH = TT + HMAX;        // staged columns (tile + halo)
   constexpr int NI = TTH / kWave;       // staged columns per lane
   extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [P][4][TTH][8]
+  static_assert(FS == 16 || FS == 32, "fragment size");
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int r16 = lane & 15, grp = lane >> 4;
+  const int r32 = lane & 31, hl = lane >> 5;
   const long t0 = static_cast<long>(blockIdx.x) * TT;
-  const long o0 = static_cast<long>(blockIdx.y) * (16 * NO);
+  const long o0 = static_cast<long>(blockIdx.y) * (FS * NO);
   const Map m = block_map(a);
   if (t0 >= m.nq) return;  // a phase with fewer positions than the grid covers (whole workgroup)
 
@@ -319,7 +333,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // then 16 consecutive 16-byte rows, like the x reads (no bank conflicts). Item it = tid + 256 u
   // is tap it / (64 NO), channel group (it / (16 NO)) % 4, row it % (16 NO): consecutive lanes read
   // consecutive 16-byte rows of the packed weights and write consecutive rows of LDS.
-  constexpr int TO = 16 * NO;
+  constexpr int TO = FS * NO;
   constexpr int WITEMS = kTapGroup * 4 * TO;                 // 16-byte rows per group
   constexpr int WPT = (WITEMS + kThreads - 1) / kThreads;   // per thread
   _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][4][TO][8]
@@ -346,40 +360,71 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
   };
 
+  const int orow = FS == 16 ? r16 : r32;  // this lane's output row within a fragment
   float bias[NO];
 #pragma unroll
   for (int n = 0; n < NO; ++n)
-    bias[n] = a.bias ? a.bias[min(o0 + 16 * n + r16, a.cout - 1)] : 0.f;
+    bias[n] = a.bias ? a.bias[min(o0 + FS * n + orow, a.cout - 1)] : 0.f;
 
-  f4v acc[NT][NO];
+  using Acc = typename std::conditional<FS == 16, f4v, f16v>::type;
+  Acc acc[NT][NO];
 #pragma unroll
   for (int i = 0; i < NT; ++i)
 #pragma unroll
-    for (int n = 0; n < NO; ++n) acc[i][n] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n < NO; ++n) acc[i][n] = Acc{};
 
   // One step: tap kk0 + tl (slot tl of the group) of the staged chunk. Only LDS reads feed the
   // MFMAs.
-  const _Float16* xw = xs + (static_cast<size_t>(grp) * TTH + wave * 16 * NT + r16) * 8;
-  const _Float16* wr = ws + (static_cast<size_t>(grp) * TO + r16) * 8;
   auto step = [&](int kk, int tl) {
     const int sh = kk * a.dil;
-    h8 xf[NT][P], wf[NO];
+    if constexpr (FS == 16) {
+      const _Float16* xw = xs + (static_cast<size_t>(grp) * TTH + wave * 16 * NT + r16) * 8;
+      const _Float16* wr = ws + (static_cast<size_t>(grp) * TO + r16) * 8;
+      h8 xf[NT][P], wf[NO];
 #pragma unroll
-    for (int p = 0; p < P; ++p)
-#pragma unroll
-      for (int i = 0; i < NT; ++i)
-        xf[i][p] = *reinterpret_cast<const h8*>(
-            xw + (static_cast<size_t>(p) * 4 * TTH + 16 * i + sh) * 8);
-#pragma unroll
-    for (int n = 0; n < NO; ++n)
-      wf[n] = *reinterpret_cast<const h8*>(wr + (static_cast<size_t>(tl) * 4 * TO + 16 * n) * 8);
-#pragma unroll
-    for (int p = 0; p < P; ++p)
-#pragma unroll
-      for (int n = 0; n < NO; ++n)
+      for (int p = 0; p < P; ++p)
 #pragma unroll
         for (int i = 0; i < NT; ++i)
-          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[i][p], wf[n], acc[i][n], 0, 0, 0);
+          xf[i][p] = *reinterpret_cast<const h8*>(
+              xw + (static_cast<size_t>(p) * 4 * TTH + 16 * i + sh) * 8);
+#pragma unroll
+      for (int n = 0; n < NO; ++n)
+        wf[n] = *reinterpret_cast<const h8*>(wr + (static_cast<size_t>(tl) * 4 * TO + 16 * n) * 8);
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int n = 0; n < NO; ++n)
+#pragma unroll
+          for (int i = 0; i < NT; ++i)
+            acc[i][n] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[i][p], wf[n], acc[i][n], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int gq = 2 * h + hl;  // channel group this lane feeds
+        const _Float16* xw = xs + (static_cast<size_t>(gq) * TTH + wave * 32 * NT + r32) * 8;
+        const _Float16* wr = ws + (static_cast<size_t>(gq) * TO + r32) * 8;
+        h8 xf[NT][P], wf[NO];
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int i = 0; i < NT; ++i)
+            xf[i][p] = *reinterpret_cast<const h8*>(
+                xw + (static_cast<size_t>(p) * 4 * TTH + 32 * i + sh) * 8);
+#pragma unroll
+        for (int n = 0; n < NO; ++n)
+          wf[n] =
+              *reinterpret_cast<const h8*>(wr + (static_cast<size_t>(tl) * 4 * TO + 32 * n) * 8);
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int n = 0; n < NO; ++n)
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+              acc[i][n] =
+                  __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[i][p], wf[n], acc[i][n], 0, 0, 0);
+      }
+    }
   };
 
   // Group g of chunk c: refill LDS from the registers loaded one group earlier (x only at g = 0),
@@ -414,39 +459,54 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 
   // ---- epilogue ---------------------------------------------------------------------------------
-  // Output-row block n at a time; the residual epilogues read block n + 1's cur before block n is
-  // finished, so each block's loads are in flight together (two blocks of registers at most).
-  f4v cur[2][NT];
-  auto load_block = [&](f4v (&c)[NT], int n) {
+  // A lane's results come in runs of four consecutive positions of one output row: per fragment
+  // one run (FS 16) or four (FS 32, q = 0..3). Output-row block n at a time; the residual
+  // epilogues read block n + 1's cur before block n is finished, so each block's loads are in
+  // flight together (two blocks of registers at most).
+  constexpr int RUNS = FS == 16 ? 1 : 4;
+  auto run_t = [&](int i, int q) -> long {
+    if constexpr (FS == 16) return t0 + wave * 16 * NT + 16 * i + 4 * grp;
+    else return t0 + wave * 32 * NT + 32 * i + 8 * q + 4 * hl;
+  };
+  auto run_v = [&](int i, int n, int q) -> f4v {
+    if constexpr (FS == 16) return acc[i][n];
+    else return f4v{acc[i][n][4 * q], acc[i][n][4 * q + 1], acc[i][n][4 * q + 2], acc[i][n][4 * q + 3]};
+  };
+  f4v cur[2][NT * RUNS];
+  auto load_block = [&](f4v (&c)[NT * RUNS], int n) {
 #pragma unroll
     for (int i = 0; i < NT; ++i)
-      c[i] = load_cur<DT>(a, m, o0 + 16 * n + r16, t0 + wave * 16 * NT + 16 * i + 4 * grp);
+#pragma unroll
+      for (int q = 0; q < RUNS; ++q)
+        c[i * RUNS + q] = load_cur<DT>(a, m, o0 + FS * n + orow, run_t(i, q));
   };
   const bool has_res = a.epi == GSVK_CONV_EPI_RES_LRELU || a.epi == GSVK_CONV_EPI_RES;
   if (has_res) load_block(cur[0], 0);
 #pragma unroll
   for (int n = 0; n < NO; ++n) {
     if (has_res && n + 1 < NO) load_block(cur[(n + 1) & 1], n + 1);
-    const long o = o0 + 16 * n + r16;
+    const long o = o0 + FS * n + orow;
     if (o >= a.cout) continue;
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const long t = t0 + wave * 16 * NT + 16 * i + 4 * grp;
-      if (t < m.nq) finish4<DT>(a, m, o, t, acc[i][n], bias[n], cur[n & 1][i]);
-    }
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+      for (int q = 0; q < RUNS; ++q) {
+        const long t = run_t(i, q);
+        if (t < m.nq) finish4<DT>(a, m, o, t, run_v(i, n, q), bias[n], cur[n & 1][i * RUNS + q]);
+      }
   }
 }
 
-template <int XM, int NT, int NO, int HMAX>
+template <int XM, int NT, int NO, int HMAX, int FS>
 constexpr size_t lds_bytes() {
-  return static_cast<size_t>(planes<XM>()) * 4 * (kWaves * 16 * NT + HMAX) * 16 +
-         static_cast<size_t>(kTapGroup) * 4 * 16 * NO * 16;
+  return static_cast<size_t>(planes<XM>()) * 4 * (kWaves * FS * NT + HMAX) * 16 +
+         static_cast<size_t>(kTapGroup) * 4 * FS * NO * 16;
 }
 
-template <int XM, int NT, int NO, int HMAX>
+template <int XM, int NT, int NO, int HMAX, int FS = 16>
 int launch_tiles(const ConvArgs& a, hipStream_t st) {
-  constexpr size_t lds = lds_bytes<XM, NT, NO, HMAX>();
-  auto kern = conv1d_mfma<XM, NT, NO, HMAX>;
+  constexpr size_t lds = lds_bytes<XM, NT, NO, HMAX, FS>();
+  auto kern = conv1d_mfma<XM, NT, NO, HMAX, FS>;
   if constexpr (lds > 64 * 1024) {
     static const bool opted = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -454,8 +514,8 @@ int launch_tiles(const ConvArgs& a, hipStream_t st) {
     if (!opted) return GSVK_E_HIP;
   }
   const long npos = a.up ? a.T + 1 : a.T;  // a phase of a transposed convolution: <= T + 1
-  const long gx = (npos + kWaves * 16 * NT - 1) / (kWaves * 16 * NT);
-  const long gy = (a.cout + 16 * NO - 1) / (16 * NO);
+  const long gx = (npos + kWaves * FS * NT - 1) / (kWaves * FS * NT);
+  const long gy = (a.cout + FS * NO - 1) / (FS * NO);
   hipLaunchKernelGGL(kern,
                      dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy),
                           static_cast<unsigned>(a.up ? a.up : 1)),
@@ -490,6 +550,18 @@ int launch_plan(const ConvArgs& a, hipStream_t st) {
     }
   }
   const int halo = a.up ? (a.k + a.up - 1) / a.up - 1 : (a.k - 1) * a.dil;
+  if (halo <= 64 && a.cout >= 24) {
+    // 32-wide fragments, 64 positions x 64 output rows per wave (256 x 64 per workgroup), when
+    // 64-row tiles pad at most a sixth of the rows and the grid still holds about 1.5 workgroups
+    // per CU of the 256 (two fit on a CU). Measured on the decoder stages: 3-10% faster than the
+    // 16-wide tiles at 192 channels; with 32-row tiles (96, 48, 24 channels) slower, so those keep
+    // the 16-wide kernel.
+    const long r64 = (a.cout + 63) / 64 * 64;
+    const int nw = 6 * (r64 - a.cout) <= r64 ? 2 : 1;
+    const long npos = a.up ? a.T + 1 : a.T;
+    const long groups = (npos + 255) / 256 * ((a.cout + 32 * nw - 1) / (32 * nw)) * (a.up ? a.up : 1);
+    if (nw == 2 && groups >= 384) return launch_tiles<XM, 2, 2, 64, 32>(a, st);
+  }
   if (halo <= 64) return launch_no<XM, 2, 64>(a, no, st);
   return launch_no<XM, 1, kMaxHalo>(a, no, st);
 }

@@ -357,3 +357,31 @@ def test_tanh_epilogue_conv_post(dt):
     """conv_post (24 -> 1, k 7, no bias) with tanh fused (dec.hpp:343-344) against the oracle's
     conv + tanhf; tolerance: the convolution's, since |tanh'| <= 1, plus one fp32 / fp16 step."""
     check_case(dt, 24, 1, 3000, 7, 1, epi=gsvk.CONV_EPI_TANH, use_bias=False, seed=410)
+
+
+# ---- 32-wide fragments (v_mfma_f32_32x32x16_f16, 256 positions x 64 rows per workgroup) --------
+# The launcher takes them when 64-row tiles pad at most a sixth of the rows, the halo is <= 64 and
+# the grid holds >= 384 such workgroups: the shapes below are the smallest that do (columns
+# 256-ragged, output rows whole or 64-ragged within the sixth).
+@pytest.mark.parametrize("C,T,k,dil,epi", [
+    (64, 98305, 11, 5, gsvk.CONV_EPI_LRELU),       # one row block, ragged columns
+    (64, 98304, 3, 1, gsvk.CONV_EPI_RES_LRELU),    # whole tiles only; residual + next LeakyReLU
+    (120, 51201, 7, 3, gsvk.CONV_EPI_RES),          # 120 of 128 rows: a ragged second block
+    (64, 98305, 11, 1, gsvk.CONV_EPI_BIAS),
+])
+def test_wide_tiles_fp32(C, T, k, dil, epi):
+    check_case(F32, C, C, T, k, dil, epi=epi, seed=500 + C + k, what="wide")
+
+
+def test_wide_tiles_fp16_round_x_and_strided():
+    check_case(F16, 64, 64, 98305, 7, 3, epi=gsvk.CONV_EPI_RES_LRELU, seed=520, what="wide")
+    check_case(F32, 64, 64, 98305, 11, 5, round_x=True, seed=521, what="wide")
+    check_case(F32, 64, 64, 98305, 3, 1, epi=gsvk.CONV_EPI_LRELU, ld_pad=5, seed=522,
+               what="wide ld")
+
+
+def test_wide_tiles_transposed():
+    """An upsampler phase grid of >= 384 wide workgroups: 128 -> 64, k 16, u 8 (stage 2's
+    geometry, narrowed)."""
+    check_t(F32, 128, 64, 12289, 16, 8, seed=530)
+    check_t(F32, 128, 64, 12289, 16, 8, epi=gsvk.CONV_EPI_RES_LRELU, seed=531)
