@@ -29,6 +29,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-
        python bench.py --only KERNEL   (one kernel of the suite, for rocprofv3 runs)
        python bench.py --pmc           (dominant kernel + a 256 MiB copy, for rocprofv3 --pmc runs)
        python bench.py --whole-step 1024   (the whole decode step alone, for rocprofv3 runs)
+       python bench.py --conv          (SoVITS convolutions per stage, stages and whole decoder)
+       python bench.py --decoder       (Generator stages and the whole decoder graph alone)
 """
 import argparse
 import json
@@ -555,7 +557,7 @@ def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=
         torch.cuda.empty_cache()
     c0, c_last, c_z, g_in = UPS[geometry][0][0], DECODER_GEOMETRIES[geometry][-1][0], 192, 1024
     pre = gsvk.Conv1d((g(c0, c_z, 7) / (c_z * 7) ** 0.5).half(), g(c0) * 0.05)
-    cond = gsvk.Conv1d((g(c0, g_in, 1) / g_in ** 0.5).half(), g(c0) * 0.05)
+    cond = ((g(c0, g_in) / g_in ** 0.5).half(), g(c0) * 0.05)  # k = 1: the [c0, g_in] matrix
     post = gsvk.Conv1d((g(1, c_last, 7) / (c_last * 7) ** 0.5).half(), None)
     z, ge = g(c_z, frames), g(g_in)
     n_out = frames
@@ -866,6 +868,8 @@ def main():
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
     ap.add_argument("--conv", action="store_true",
                     help="time the SoVITS ResBlock convolutions per decoder stage and exit")
+    ap.add_argument("--decoder", action="store_true",
+                    help="the SoVITS Generator stages and the whole decoder graph only (rocprofv3 runs)")
     ap.add_argument("--whole-step", type=int, default=0, metavar="KV_LEN",
                     help="run only the whole T2S decode step at this KV length (rocprofv3 runs)")
     a = ap.parse_args()
@@ -886,6 +890,9 @@ def main():
         return
     if a.whole_step:
         print(json.dumps(full_decode_step(torch, gsvk, dev, kv_len=a.whole_step)), flush=True)
+        return
+    if a.decoder:
+        print(json.dumps(sovits_generator(torch, gsvk, dev)), flush=True)
         return
     if a.conv:
         res = sovits_conv(torch, gsvk, dev)

@@ -337,9 +337,9 @@ class SovitsDecoder:
     """The whole SoVITS decoder (Generator::forward, dec.hpp:264-345) over one set of device
     buffers: conv_pre (+ cond(ge) folded into its bias) and LeakyReLU, the GeneratorStages, the final
     LeakyReLU(0.01), conv_post and tanh, as gsvk_sovits_decoder_* launches (a HIP graph unless
-    graph=False). conv_pre / cond / conv_post are Conv1d, stages GeneratorStage objects; z
-    [c_z, frames] fp32 or fp16 (the activation dtype), ge [g_in] fp32 (one frame; None without
-    cond), out [frames * prod(u)] of z's dtype.
+    graph=False). conv_pre / conv_post are Conv1d, stages GeneratorStage objects, cond a pair
+    (w16 [c0, g_in] fp16, bias [c0] fp32) or None; z [c_z, frames] fp32 or fp16 (the activation
+    dtype), ge [g_in] fp32 (one frame; None without cond), out [frames * prod(u)] of z's dtype.
     The workspace is this object's own device allocation."""
 
     def __init__(self, conv_pre, cond, stages, conv_post, z, ge, out, round_x=False, graph=True):
@@ -364,8 +364,10 @@ class SovitsDecoder:
         d.c0, d.pre_k = conv_pre.out_c, conv_pre.k
         d.pre_w, d.pre_b = _ptr(conv_pre.wp), _ptr(conv_pre.b)
         if cond is not None:
+            w_cond, b_cond = cond
             assert ge.dtype == torch.float32, "ge is fp32 for either activation dtype"
-            d.g_in, d.cond_w, d.cond_b = cond.in_c, _ptr(cond.wp), _ptr(cond.b)
+            assert w_cond.shape == (conv_pre.out_c, ge.numel()) and w_cond.is_contiguous()
+            d.g_in, d.cond_w, d.cond_b = w_cond.shape[1], _ptr(w_cond), _ptr(b_cond)
             d.ge = _ptr(ge)
         d.n_stages = n
         d.stage = ctypes.cast(self._stages, ctypes.POINTER(SovitsStage))

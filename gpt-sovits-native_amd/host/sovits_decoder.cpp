@@ -14,14 +14,14 @@ constexpr size_t kAlign = 256;  // bytes: alignment of every workspace region
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout: cv [c0] and bias [c0] in fp32, then 8 activation slots of `slot` elements of the
+// Workspace layout: the folded bias (c0 floats), then 8 activation slots of `slot` elements of the
 // activation dtype each: X (stage input, then the stage output), Y (upsampler output, the first
 // residual), TIN0 (lrelu(Y)), TIN (the next pair's LeakyReLU input), TA (the pair's middle
 // activation) and CUR0..CUR2 (the three branch accumulators).
 enum Slot { kX, kY, kTin0, kTin, kTa, kCur0, kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS };
 
 struct Layout {
-  size_t vec_bytes = 0;   // bytes of cv and of bias (c0 floats, rounded up)
+  size_t vec_bytes = 0;   // bytes of the folded bias (c0 floats, rounded up)
   size_t slot_bytes = 0;  // bytes of one activation slot
   size_t t_out = 0;       // samples of the output
   size_t bytes = 0;
@@ -53,7 +53,7 @@ int shapes(const gsvk_sovits_decoder_desc* d, Layout* lay) {
   lay->vec_bytes = round_up(d->c0 * sizeof(float), kAlign);
   lay->slot_bytes = round_up(slot * esz, kAlign);
   lay->t_out = T;
-  lay->bytes = 2 * lay->vec_bytes + kSlots * lay->slot_bytes;
+  lay->bytes = lay->vec_bytes + kSlots * lay->slot_bytes;
   return GSVK_OK;
 }
 
@@ -78,8 +78,8 @@ int check_workspace(const gsvk_sovits_decoder_desc* d, Layout* lay) {
 }
 
 int count_launches(const gsvk_sovits_decoder_desc* d) {
-  // cond + bias fold (with conditioning), conv_pre, 20 per stage, conv_post
-  return (d->g_in ? 2 : 0) + 1 + 20 * static_cast<int>(d->n_stages) + 1;
+  // cond with the bias fold (with conditioning), conv_pre, 20 per stage, conv_post
+  return (d->g_in ? 1 : 0) + 1 + 20 * static_cast<int>(d->n_stages) + 1;
 }
 
 // The launches of one decoder pass in Generator::forward's order.
@@ -87,22 +87,21 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
   const int dt = d->dtype, rx = d->round_x;
   const float slope = 0.1f;  // LRELU_SLOPE (dec.hpp:284, 322, 324)
   char* ws = static_cast<char*>(d->workspace);
-  float* cv = reinterpret_cast<float*>(ws);
-  float* bias = reinterpret_cast<float*>(ws + lay.vec_bytes);
+  float* bias = reinterpret_cast<float*>(ws);
   void* slot[kSlots];
   for (int i = 0; i < kSlots; ++i)
-    slot[i] = ws + 2 * lay.vec_bytes + static_cast<size_t>(i) * lay.slot_bytes;
+    slot[i] = ws + lay.vec_bytes + static_cast<size_t>(i) * lay.slot_bytes;
   int rc;
 
   // x = lrelu(conv_pre(z) + b_pre + cond(ge)[:, 0], 0.1): the broadcast add of dec.hpp:275-279
-  // folded into the bias, the stage-0 leaky_relu_io (dec.hpp:284) into the store.
+  // folded into the bias, the stage-0 leaky_relu_io (dec.hpp:284) into the store. cond is a k = 1
+  // convolution of one frame, i.e. a GEMV; b_pre enters as its residual, so one launch leaves
+  // bias = (W_cond ge + b_cond) + b_pre in fp32.
   const float* pre_bias = d->pre_b;
   if (d->g_in) {
-    // ge and cv are fp32 for either activation dtype: the fold is an fp32 bias
-    if ((rc = gsvk_conv1d(GSVK_F32, rx, d->ge, 1, d->cond_w, d->cond_b, GSVK_CONV_EPI_BIAS, 0.f,
-                          nullptr, nullptr, 0, cv, 1, d->g_in, d->c0, 1, 1, 1, st)))
+    if ((rc = gsvk_gemv_f16w(GSVK_F32, rx, d->ge, d->g_in, d->cond_w, d->cond_b, GSVK_ACT_NONE, 0.f,
+                             d->pre_b, GSVK_F32, bias, d->c0, 1, d->c0, d->g_in, st)))
       return rc;
-    if ((rc = gsvk_scaled_add(GSVK_F32, d->pre_b, cv, bias, d->c0, 1.f, st))) return rc;
     pre_bias = bias;
   }
   size_t T = d->frames;

@@ -4,8 +4,9 @@
  * graph. Every convolution is gsvk_conv1d / gsvk_convt1d (include/gsvk.h) with the element-wise
  * passes around it fused into its store:
  *
- *   cv   = cond(ge)                          [c0, 1]       (dec.hpp:271)          1 launch
- *   bias = b_pre + cv                        the broadcast add folded into a bias  1 launch
+ *   bias = (W_cond ge + b_cond) + b_pre      cond (dec.hpp:271) as a GEMV of one  1 launch
+ *                                            frame (gsvk_gemv_f16w), the broadcast add
+ *                                            (dec.hpp:275-279) folded into its output
  *   x    = lrelu(conv_pre(z) + bias, 0.1)    (dec.hpp:268, 275-279, 284)          1 launch
  *   per stage s (dec.hpp:283-336):                                               20 launches
  *     y = ups(x), t_in = lrelu(y, 0.1)                                  (DUAL epilogue)
@@ -15,10 +16,11 @@
  *   out  = tanh(conv_post(x))                [1, T out]    (dec.hpp:343-344)       1 launch
  *
  * The folded broadcast rounds (W z + b_pre) + cv as W z + (b_pre + cv): within the convolution's
- * tolerance. Weights are the packed forms (gsvk_conv1d_pack / gsvk_convt1d_pack of the .gsv's fp16
- * [out, in, k] / [in, out, k] tensors); biases fp32. Activations of `dtype` (F32, the reference's,
+ * tolerance. Convolution weights are the packed forms (gsvk_conv1d_pack / gsvk_convt1d_pack of the
+ * .gsv's fp16 [out, in, k] / [in, out, k] tensors); cond's is its fp16 [c0, g_in] matrix as stored
+ * (the k = 1 weight, row-major, unpacked); biases fp32. Activations of `dtype` (F32, the reference's,
  * or F16 storage: every stored activation rounded to fp16, arithmetic in fp32); round_x as in
- * gsvk_conv1d (F32 only). ge, cv and the folded bias are fp32 for either dtype.
+ * gsvk_conv1d (F32 only). ge and the folded bias are fp32 for either dtype.
  */
 #ifndef GSVK_SOVITS_H
 #define GSVK_SOVITS_H
@@ -58,7 +60,7 @@ typedef struct gsvk_sovits_decoder_desc {
   const uint16_t* pre_w; /* packed conv_pre */
   const float* pre_b;    /* may be NULL */
   size_t g_in;           /* cond input channels; 0: no conditioning */
-  const uint16_t* cond_w; /* packed cond (k = 1) */
+  const uint16_t* cond_w; /* cond's fp16 [c0, g_in] weight matrix (not packed) */
   const float* cond_b;
   size_t n_stages;
   const gsvk_sovits_stage* stage;

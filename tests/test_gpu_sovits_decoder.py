@@ -97,9 +97,9 @@ class GpuDecoder:
         w_pre, b_pre = m["pre"]
         self.pre = gsvk.Conv1d(dev(w_pre.view(np.uint16), F16), devf(b_pre))
         self.cond = None
-        if m["cond"] is not None:
+        if m["cond"] is not None:  # cond is k = 1: its fp16 [c0, g_in] matrix, unpacked
             w_c, b_c = m["cond"]
-            self.cond = gsvk.Conv1d(dev(w_c.view(np.uint16), F16), devf(b_c))
+            self.cond = (dev(w_c[:, :, 0].view(np.uint16), F16), devf(b_c))
         self.stages = [gpu_stage(up, rbs, UPS_U[s]) for s, (up, rbs) in enumerate(m["stages"])]
         self.post = gsvk.Conv1d(dev(m["post"].view(np.uint16), F16), None)
 
@@ -108,13 +108,15 @@ class GpuDecoder:
                                   round_x=round_x, graph=graph)
 
     def python_chain(self, z, ge, out, round_x=False):
-        """The same launches issued one by one from Python: cond, bias fold, conv_pre + lrelu,
-        GeneratorStage.forward per stage, conv_post + tanh."""
+        """The same launches issued one by one from Python: cond as a GEMV with b_pre as its
+        residual (the bias fold), conv_pre + lrelu, GeneratorStage.forward per stage, conv_post +
+        tanh."""
         bias = self.pre.b
         if self.cond is not None:
-            cv = self.cond.forward(ge.view(-1, 1), round_x=round_x).view(-1)
-            bias = torch.empty_like(cv)
-            gsvk.scaled_add(self.pre.b, cv, bias, 1.0)
+            w_c, b_c = self.cond
+            bias = torch.empty_like(self.pre.b)
+            gsvk.gemv_f16w(ge.view(1, -1), w_c, bias.view(1, -1), bias=b_c,
+                           residual=self.pre.b.view(1, -1), round_x=round_x)
         x = torch.empty(self.pre.out_c, z.shape[1], dtype=z.dtype, device=z.device)
         gsvk.conv1d(z, self.pre.wp, self.pre.out_c, self.pre.k, x, bias, 1, gsvk.CONV_EPI_LRELU,
                     0.1, round_x=round_x)
@@ -147,7 +149,7 @@ def test_decoder_matches_oracle_chain(c_z, c0, g_in, frames, round_x):
     n_out = frames * int(np.prod(UPS_U))
     out = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
     dec = g.bind(zd, ged, out, round_x=round_x)
-    assert dec.launches == (2 if g_in else 0) + 1 + 5 * 20 + 1
+    assert dec.launches == (1 if g_in else 0) + 1 + 5 * 20 + 1
     dec.run()
     torch.cuda.synchronize()
     got = host(out, F32)
