@@ -21,7 +21,17 @@ namespace gsvk {
 namespace {
 
 constexpr int kAttnWaves = 4;
-constexpr int kKeysPerGroup = 4;  // keys per wave per pipeline step
+#ifndef GSVK_ATTN_KPG
+#define GSVK_ATTN_KPG 4
+#endif
+#ifndef GSVK_ATTN_DEPTH
+#define GSVK_ATTN_DEPTH 2
+#endif
+#ifndef GSVK_ATTN_KEYS_PER_WG
+#define GSVK_ATTN_KEYS_PER_WG 128
+#endif
+constexpr int kKeysPerGroup = GSVK_ATTN_KPG;  // keys per wave per pipeline step
+constexpr int kDepth = GSVK_ATTN_DEPTH;        // groups of loads in flight per wave
 constexpr int kMaxChunks = 16;
 
 struct AttnArgs {
@@ -141,7 +151,7 @@ __global__ __launch_bounds__(kWave * kAttnWaves) void attn_chunk(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = 0.f;
 
-  // This wave's keys: k0 + wave + 4 j. Groups of kKeysPerGroup, two groups of loads in flight.
+  // This wave's keys: k0 + wave + 4 j. Groups of kKeysPerGroup, kDepth groups of loads in flight.
   const long nk = k1 > k0 + wave ? (k1 - k0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
   const long ng = (nk + kKeysPerGroup - 1) / kKeysPerGroup;
   auto key_of = [&](long g, int u) { return k0 + wave + kAttnWaves * (g * kKeysPerGroup + u); };
@@ -196,14 +206,17 @@ __global__ __launch_bounds__(kWave * kAttnWaves) void attn_chunk(AttnArgs a) {
     m = mn;
   };
   if (ng > 0) {
-    KeyGroup<KVT> f0, f1;
-    load(f0, 0);
-    load(f1, min(1L, ng - 1));
-    for (long g = 0; g < ng; g += 2) {
-      step(f0, g);
-      load(f0, min(g + 2, ng - 1));
-      if (g + 1 < ng) step(f1, g + 1);
-      load(f1, min(g + 3, ng - 1));
+    // Group g sits in f[g % kDepth]; its reload (group g + kDepth, clamped: an in-bounds reread
+    // past the end) is issued right after it is used, so the loads stay unconditional.
+    KeyGroup<KVT> f[kDepth];
+#pragma unroll
+    for (int s = 0; s < kDepth; ++s) load(f[s], min(static_cast<long>(s), ng - 1));
+    for (long g = 0; g < ng; g += kDepth) {
+#pragma unroll
+      for (int s = 0; s < kDepth; ++s) {
+        if (g + s < ng) step(f[s], g + s);
+        load(f[s], min(g + s + kDepth, ng - 1));
+      }
     }
   }
 
@@ -286,9 +299,9 @@ __global__ __launch_bounds__(kWave * kMaxChunks) void attn_merge(AttnArgs a, int
 }
 
 int chunks_for(size_t batch, size_t len_bound) {
-  // about 128 keys (256 KB of an fp16 cache at D = 512) per workgroup, and at least 2 workgroups
-  // per CU when the batch alone gives fewer
-  long c = static_cast<long>((len_bound + 127) / 128);
+  // about GSVK_ATTN_KEYS_PER_WG keys (128: 256 KB of an fp16 cache at D = 512) per workgroup, and
+  // at least 2 workgroups per CU when the batch alone gives fewer
+  long c = static_cast<long>((len_bound + GSVK_ATTN_KEYS_PER_WG - 1) / GSVK_ATTN_KEYS_PER_WG);
   const long min_c = (512 + static_cast<long>(batch) - 1) / static_cast<long>(batch);
   if (len_bound > 256) c = std::max(c, min_c);
   return static_cast<int>(std::max(1L, std::min<long>(c, kMaxChunks)));

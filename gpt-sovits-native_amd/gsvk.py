@@ -789,3 +789,50 @@ def t2s_model_from_gsv(g, dev="cuda", stream=None):
              dims=dict(d_model=int(mm["hidden_dim"]), ffn=int(mm["linear_units"]),
                        vocab=int(mm["vocab_size"]), n_layer=n_layer))
     return m, (a16, a32)
+
+
+SOVITS_UPS_U = (10, 8, 2, 2, 2)    # Generator upsample rates (dec.hpp:55)
+SOVITS_RES_K = (3, 7, 11)          # ResBlock1 kernel sizes (dec.hpp:67)
+SOVITS_RES_DIL = (1, 3, 5)         # convs1 dilations (dec.hpp:57)
+
+
+def sovits_decoder_from_gsv(g, z, ge, out, round_x=False, graph=True, dev="cuda", stream=None):
+    """A SovitsDecoder over the Generator weights of a sovits .gsv, by the names Generator::load
+    reads (dec.hpp:54-75): conv_pre, cond, ups.{i}, resblocks.{3 i + j}.convs{1,2}.{m}, conv_post.
+    Each weight comes as load_tensor_f16 takes it (sovits_types.hpp:76-87): the tensor's fp16 copy
+    when the file has one, else its fp32 values rounded to fp16 (to nearest even) on the device;
+    biases are fp32 (absent: zeros, as for conv_post). Channel counts and kernel sizes come from
+    the tensors' shapes, strides and dilations are the model's. Returns (decoder, arenas)."""
+    a16, t16 = g.upload(F16, dev, stream)
+    a32, t32 = g.upload(F32, dev, stream)
+
+    def w16(name):
+        if name in t16:
+            return t16[name]
+        if name not in t32:
+            raise GsvkError(f"sovits_decoder_from_gsv: missing tensor {name}", E_FORMAT)
+        return t32[name].half()
+
+    def b32(name):
+        return t32.get(name)
+
+    pre = Conv1d(w16("dec.conv_pre.weight"), b32("dec.conv_pre.bias"))
+    cond = None
+    if "dec.cond.weight" in t16 or "dec.cond.weight" in t32:
+        cw = w16("dec.cond.weight")
+        cond = (cw.reshape(cw.shape[0], -1).contiguous(), b32("dec.cond.bias"))
+    stages = []
+    for i, u in enumerate(SOVITS_UPS_U):
+        ups = ConvT1d(w16(f"dec.ups.{i}.weight"), b32(f"dec.ups.{i}.bias"), u)
+        blocks = []
+        for j in range(len(SOVITS_RES_K)):
+            p = f"dec.resblocks.{3 * i + j}."
+            blocks.append(ResBlock1([w16(f"{p}convs1.{m}.weight") for m in range(3)],
+                                    [b32(f"{p}convs1.{m}.bias") for m in range(3)],
+                                    [w16(f"{p}convs2.{m}.weight") for m in range(3)],
+                                    [b32(f"{p}convs2.{m}.bias") for m in range(3)],
+                                    SOVITS_RES_DIL))
+        stages.append(GeneratorStage(ups, blocks))
+    post = Conv1d(w16("dec.conv_post.weight"), b32("dec.conv_post.bias"))
+    dec = SovitsDecoder(pre, cond, stages, post, z, ge, out, round_x=round_x, graph=graph)
+    return dec, (a16, a32)

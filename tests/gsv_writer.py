@@ -16,9 +16,10 @@ def _up(n):
     return (n + ALIGN - 1) // ALIGN * ALIGN
 
 
-def gsv_bytes(name, tensors, model_config=None, slim=()):
+def gsv_bytes(name, tensors, model_config=None, slim=(), no16=()):
     """tensors: dict name -> numpy array (float32 or float16 source). slim: names written with an
-    fp16 copy only (f32 bytes 0). Returns the file as bytes."""
+    fp16 copy only (f32 bytes 0). no16: names written without an fp16 copy whatever their size (the
+    converter's weight-norm products, convert.py:75-82). Returns the file as bytes."""
     cfg = json.dumps({"meta": {"model": name, "converter": "convert.py GSV1"},
                       "model_config": model_config}, ensure_ascii=False, sort_keys=True).encode()
     nm = name.encode()
@@ -33,7 +34,7 @@ def gsv_bytes(name, tensors, model_config=None, slim=()):
     has16 = False
     for e in layout:
         k, v = e[0], e[1]
-        if v.size >= FP16_MIN_ELEMS or k in slim:
+        if (v.size >= FP16_MIN_ELEMS and k not in no16) or k in slim:
             e[4], e[5] = pos, 2 * v.size
             pos += _up(e[5])
             has16 = True
@@ -83,3 +84,27 @@ def t2s_tensors(D=128, H=4, FF=256, L=2, V=50, PV=40, seed=0):
     cfg = {"model": {"hidden_dim": D, "embedding_dim": D, "head": H, "n_layer": L,
                      "linear_units": FF, "vocab_size": V, "phoneme_vocab_size": PV, "EOS": V - 1}}
     return t, cfg
+
+
+def sovits_dec_tensors(c_z=16, c0=64, g_in=32, seed=0):
+    """A SoVITS decoder (Generator) with the tensor names Generator::load reads (dec.hpp:54-75), c0
+    channels after conv_pre (the model's: 768), the model's strides, kernels and dilations; fp32
+    weights whose fp16 copies the loader uses when present."""
+    r = np.random.default_rng(seed)
+    w = lambda co, ci, k: (r.standard_normal((co, ci, k)) / np.sqrt(ci * k)).astype(np.float32)
+    b = lambda n: (0.05 * r.standard_normal(n)).astype(np.float32)
+    t = {"dec.conv_pre.weight": w(c0, c_z, 7), "dec.conv_pre.bias": b(c0),
+         "dec.cond.weight": w(c0, g_in, 1), "dec.cond.bias": b(c0)}
+    c = c0
+    for i, (u, k) in enumerate(zip((10, 8, 2, 2, 2), (20, 16, 8, 2, 2))):
+        t[f"dec.ups.{i}.weight"] = (r.standard_normal((c, c // 2, k)) /
+                                   np.sqrt(c * k / u)).astype(np.float32)
+        t[f"dec.ups.{i}.bias"] = b(c // 2)
+        c //= 2
+        for j, kr in enumerate((3, 7, 11)):
+            for m in range(3):
+                for conv in ("convs1", "convs2"):
+                    t[f"dec.resblocks.{3 * i + j}.{conv}.{m}.weight"] = w(c, c, kr)
+                    t[f"dec.resblocks.{3 * i + j}.{conv}.{m}.bias"] = b(c)
+    t["dec.conv_post.weight"] = w(1, c, 7)
+    return t

@@ -8,7 +8,7 @@ import torch
 import gsvk
 import oracle as O
 from gpu_util import F16, F32, host, say
-from gsv_writer import gsv_bytes, t2s_tensors
+from gsv_writer import gsv_bytes, sovits_dec_tensors, t2s_tensors
 from test_gpu_t2s_decode import compare, oracle_step
 
 pytestmark = pytest.mark.gpu
@@ -79,3 +79,46 @@ def test_decode_step_from_gsv_matches_oracle(tmp_path):
             k_cache=caches[l][0].copy(), v_cache=caches[l][1].copy()))
     x_want, lg_want = oracle_step(mh, io_h)
     compare(host(iod["x"], F16), host(iod["logits"], F32), x_want, lg_want, "from .gsv")
+
+
+def test_sovits_decoder_from_gsv_matches_oracle(tmp_path):
+    """The decoder bound to a sovits .gsv by Generator::load's names (dec.hpp:54-75). The upsampler
+    and ResBlock weights are written without an fp16 copy, as the converter writes weight-norm
+    products (convert.py:75-82), so the loader rounds their fp32 values to fp16 on the device;
+    conv_pre, cond and conv_post come from their fp16 copies. The oracle chain runs on the same
+    fp16 weights (numpy's round to nearest even): within the decoder test's 1e-4."""
+    from test_gpu_sovits_decoder import oracle_decoder
+    c_z, c0, g_in, frames = 16, 64, 32, 8
+    t = sovits_dec_tensors(c_z, c0, g_in, seed=11)
+    no16 = [k for k in t if k.startswith(("dec.ups.", "dec.resblocks.")) and k.endswith(".weight")]
+    p = tmp_path / "s2.gsv"
+    p.write_bytes(gsv_bytes("sovits_v2ProPlus", t, None, no16=no16))
+    g = gsvk.GsvFile(str(p))
+    assert all(g.tensors[k]["f16_nbytes"] == 0 for k in no16)
+    assert g.tensors["dec.conv_pre.weight"]["f16_nbytes"] > 0
+    h16 = lambda k: t[k].astype(np.float16)
+    m = {"pre": (h16("dec.conv_pre.weight"), t["dec.conv_pre.bias"]),
+         "cond": (h16("dec.cond.weight"), t["dec.cond.bias"]), "post": h16("dec.conv_post.weight"),
+         "stages": []}
+    for i in range(5):
+        rbs = []
+        for j in range(3):
+            q = f"dec.resblocks.{3 * i + j}."
+            rbs.append(([h16(f"{q}convs1.{k}.weight") for k in range(3)],
+                        [t[f"{q}convs1.{k}.bias"] for k in range(3)],
+                        [h16(f"{q}convs2.{k}.weight") for k in range(3)],
+                        [t[f"{q}convs2.{k}.bias"] for k in range(3)]))
+        m["stages"].append(((h16(f"dec.ups.{i}.weight"), t[f"dec.ups.{i}.bias"]), rbs))
+    r = np.random.default_rng(12)
+    z = r.standard_normal((c_z, frames)).astype(np.float32)
+    ge = r.standard_normal(g_in).astype(np.float32)
+    want = oracle_decoder(m, z, ge)
+    out = torch.full((frames * 640,), float("nan"), device="cuda")
+    dec, arenas = gsvk.sovits_decoder_from_gsv(g, torch.from_numpy(z).cuda(),
+                                               torch.from_numpy(ge).cuda(), out)
+    dec.run()
+    torch.cuda.synchronize()
+    got = host(out, F32)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
+    say(f"sovits decoder from .gsv: max |d| {err:.2e}")
+    assert np.isfinite(got).all() and err <= 1e-4
