@@ -1,8 +1,8 @@
 /*
  * gsvk_oracle.c — CPU restatement of the reference's fused-layer arithmetic (see gsvk_oracle.h).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the timed CPU baseline. It is never
- * linked into, loaded by or called from the product library.
+ * TEST INFRASTRUCTURE ONLY: the results the HIP kernels are compared with and the timed CPU
+ * baseline. It is never linked into, loaded by or called from the product library.
  *
  * Build: gcc -O3 -mavx2 -mfma -ffp-contract=off (oracle/Makefile). With contraction off, an fma
  * happens exactly where this file writes fma()/fmaf(), which is where AppleClang's default

@@ -1,8 +1,8 @@
 /*
  * gsvk_oracle.h — CPU restatement of the reference's fused-layer arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker the HIP kernels are compared against and the timed
- * CPU baseline; the product library never links, loads or calls it. Only tests/, the smoke check
+ * TEST INFRASTRUCTURE ONLY. The HIP kernels are compared against these results, and this is the
+ * timed CPU baseline; the product library never links, loads or calls it. Only tests/, the smoke check
  * and the benchmark's CPU-baseline leg may use it.
  *
  * Each function follows the reference's operation order (cited per function in gsvk_oracle.c).

@@ -1,7 +1,8 @@
 """numpy/ctypes front of the CPU oracle (liboracle.so, oracle/gsvk_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: used by tests/, the smoke check and the CPU-baseline leg of bench.py as
-the checker. The product (libgsvk.so) never imports or calls it.
+the reference results the GPU kernels are compared with. The product (libgsvk.so) never imports
+or calls it.
 
 Arrays are host numpy arrays holding the *storage* representation: float32 for dtype F32, uint16
 bit patterns for F16 / BF16 (F16 may also be given as numpy float16).

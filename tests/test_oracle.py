@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker.
+"""Pins the CPU oracle before the GPU kernels are compared against it.
 
 Every oracle function is checked against the reference's own golden vectors where they exist
 (tests/golden/*.f32 are the reference's tests/kern_golden files, unmodified) and otherwise against
