@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
@@ -276,5 +277,22 @@ inline size_t span_bytes(size_t rows, size_t n, size_t ld, size_t esz) {
 }
 
 int launch_status();  // GSVK_OK, or GSVK_E_HIP after a failed launch (reads hipGetLastError)
+
+constexpr int kMaxDevices = 64;
+
+// Allow `bytes` of dynamic LDS (above the 64 KiB default) for kernel `fn` on the current device:
+// once per kernel and device, `done` being that kernel's flags (setting it twice from racing first
+// calls is harmless). False when the device cannot be queried or the runtime refuses.
+inline bool allow_dynamic_lds(const void* fn, size_t bytes,
+                              std::atomic<bool> (&done)[kMaxDevices]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  if (done[dev].load(std::memory_order_acquire)) return true;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(bytes)) != hipSuccess)
+    return false;
+  done[dev].store(true, std::memory_order_release);
+  return true;
+}
 
 }  // namespace gsvk

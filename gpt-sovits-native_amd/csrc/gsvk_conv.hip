@@ -508,10 +508,8 @@ int launch_tiles(const ConvArgs& a, hipStream_t st) {
   constexpr size_t lds = lds_bytes<XM, NT, NO, HMAX, FS>();
   auto kern = conv1d_mfma<XM, NT, NO, HMAX, FS>;
   if constexpr (lds > 64 * 1024) {
-    static const bool opted = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  static_cast<int>(lds)) == hipSuccess;
-    if (!opted) return GSVK_E_HIP;
+    static std::atomic<bool> lds_ok[kMaxDevices];
+    if (!allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds, lds_ok)) return GSVK_E_HIP;
   }
   const long npos = a.up ? a.T + 1 : a.T;  // a phase of a transposed convolution: <= T + 1
   const long gx = (npos + kWaves * FS * NT - 1) / (kWaves * FS * NT);

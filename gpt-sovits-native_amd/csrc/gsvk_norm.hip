@@ -489,8 +489,6 @@ int launch_ln(const LnArgs& a, bool vec_ok, hipStream_t st) {
   return launch_status();
 }
 
-constexpr int kMaxDevices = 64;
-
 // Compute units of the current device (cached per device; 256 on MI355X). A racing first call
 // stores the same value twice.
 int device_cus() {
@@ -506,35 +504,30 @@ int device_cus() {
   return n;
 }
 
+// False (nothing launched) when the runtime refuses the LDS the tile needs.
 template <int DT, int CPT, bool NT>
-void launch_gn_cpt(const GnArgs& a, hipStream_t st) {
+bool launch_gn_cpt(const GnArgs& a, hipStream_t st) {
   constexpr size_t lds = static_cast<size_t>(CPT) * kGnBlock * 16;  // 16-128 KiB of the 160 KiB
-  // Dynamic LDS above 64 KiB must be allowed once per kernel and device (idempotent, so two
-  // threads racing on the first call both just set it).
-  static std::atomic<bool> attr_set[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices &&
-      !attr_set[dev].load(std::memory_order_acquire)) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gn_gelu_vec<DT, CPT, NT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    attr_set[dev].store(true, std::memory_order_release);
-  }
+  static std::atomic<bool> lds_ok[kMaxDevices];
+  if (lds > 64 * 1024 &&
+      !allow_dynamic_lds(reinterpret_cast<const void*>(&gn_gelu_vec<DT, CPT, NT>), lds, lds_ok))
+    return false;
   // one workgroup per CU (two when the staging buffer leaves room for a second one)
   const long slots = device_cus() * (lds <= 64 * 1024 ? 2 : 1);
   const dim3 grid(static_cast<unsigned>(a.channels < slots ? a.channels : slots));
   hipLaunchKernelGGL((gn_gelu_vec<DT, CPT, NT>), grid, dim3(kGnBlock), lds, st, a);
+  return true;
 }
 
 template <int DT, bool NT>
 bool launch_gn_vec(const GnArgs& a, hipStream_t st) {
   constexpr int V = Store<DT>::VEC;
   const long nb = a.T / V + 1;  // upper bound on body chunks
-  if (nb <= 1L * kGnBlock) launch_gn_cpt<DT, 1, NT>(a, st);
-  else if (nb <= 2L * kGnBlock) launch_gn_cpt<DT, 2, NT>(a, st);
-  else if (nb <= 4L * kGnBlock) launch_gn_cpt<DT, 4, NT>(a, st);
-  else if (nb <= 8L * kGnBlock) launch_gn_cpt<DT, 8, NT>(a, st);
-  else return false;
-  return true;
+  if (nb <= 1L * kGnBlock) return launch_gn_cpt<DT, 1, NT>(a, st);
+  if (nb <= 2L * kGnBlock) return launch_gn_cpt<DT, 2, NT>(a, st);
+  if (nb <= 4L * kGnBlock) return launch_gn_cpt<DT, 4, NT>(a, st);
+  if (nb <= 8L * kGnBlock) return launch_gn_cpt<DT, 8, NT>(a, st);
+  return false;
 }
 
 template <int DT>
