@@ -61,6 +61,7 @@ struct ConvArgs {
   int epi;
   float slope;
   bool vec;
+  bool xact;  // x read as lrelu(x, slope)
   int up;     // 0: Conv1d; u: transposed convolution with stride u (phase r = blockIdx.z)
   long Tout;  // transposed: output columns T u
   int pad_t;  // transposed: (k - u) / 2
@@ -314,7 +315,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float xv = DT == GSVK_F32 ? __builtin_bit_cast(float, raw[u][j]) : h2f(raw[u][j]);
-        const float v = tok && ch0 + j < a.cin ? xv : 0.f;
+        float v = tok && ch0 + j < a.cin ? xv : 0.f;
+        if (a.xact) v = lrelu_ref(v, a.slope);  // the input pre-activation (0 stays 0)
         hi[j] = static_cast<_Float16>(v);
         if constexpr (P == 2) {  // an infinite x leaves inf - inf: its remainder is 0
           const float rest = v - static_cast<float>(hi[j]);
@@ -598,6 +600,8 @@ namespace {
 int conv_entry(ConvArgs a, int dtype, int round_x, size_t T, size_t Tout, size_t wb,
                hipStream_t st) {
   if (dtype != GSVK_F32 && dtype != GSVK_F16) return GSVK_E_DTYPE;
+  a.xact = (a.epi & GSVK_CONV_X_LRELU) != 0;
+  a.epi &= ~GSVK_CONV_X_LRELU;
   if (a.epi < GSVK_CONV_EPI_BIAS || a.epi > GSVK_CONV_EPI_TANH) return GSVK_E_DTYPE;
   const bool reads_res = a.epi == GSVK_CONV_EPI_RES_LRELU || a.epi == GSVK_CONV_EPI_RES;
   const bool has_cur = reads_res || a.epi == GSVK_CONV_EPI_DUAL;

@@ -18,6 +18,7 @@ ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_LEAKY_RELU = 0, 1, 2, 3
 OK, E_NULL, E_SIZE, E_DTYPE, E_ALIAS, E_ARG, E_HIP, E_FORMAT, E_IO = 0, -1, -2, -3, -4, -5, -6, -7, -8
 CONV_EPI_BIAS, CONV_EPI_LRELU, CONV_EPI_RES_LRELU, CONV_EPI_RES, CONV_EPI_DUAL, CONV_EPI_TANH = \
     0, 1, 2, 3, 4, 5
+CONV_X_LRELU = 0x100  # OR-ed into epi: the convolution reads lrelu(x, slope)
 
 # Every exported symbol of the C ABI with (restype, argtypes).
 _vp, _sz, _i, _f, _d = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_double
@@ -204,7 +205,7 @@ class Conv1d:
     def forward(self, x, y=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None, round_x=False,
                 stream=None, res=None):
         import torch
-        if y is None and epi != CONV_EPI_RES:
+        if y is None and (epi & ~CONV_X_LRELU) != CONV_EPI_RES:
             y = torch.empty(self.out_c, x.shape[1], dtype=x.dtype, device=x.device)
         conv1d(x, self.wp, self.out_c, self.k, y, self.b, self.dilation, epi, slope, cur, round_x,
                stream, res=res)
@@ -252,7 +253,7 @@ class ConvT1d:
     def forward(self, x, y=None, epi=CONV_EPI_BIAS, slope=0.1, cur=None, round_x=False,
                 stream=None, res=None):
         import torch
-        if y is None and epi != CONV_EPI_RES:
+        if y is None and (epi & ~CONV_X_LRELU) != CONV_EPI_RES:
             y = torch.empty(self.out_c, x.shape[1] * self.stride_u, dtype=x.dtype, device=x.device)
         convt1d(x, self.wp, self.out_c, self.k, self.stride_u, y, self.b, epi, slope, cur, round_x,
                 stream, res=res)
@@ -271,14 +272,16 @@ class ResBlock1:
 class GeneratorStage:
     """One stage of the reference's Generator::forward (dec.hpp:283-336) on the GPU, with every
     element-wise pass fused into a neighbouring kernel:
-      y = ups(x), t_in = lrelu(y, 0.1)            one launch (CONV_EPI_DUAL); x arrives already
-                                                  LeakyReLU'd (the previous stage's branch mean,
-                                                  dec.hpp:284)
+      y = ups(x)                                  x arrives already LeakyReLU'd (the previous
+                                                  stage's branch mean, dec.hpp:284)
       for each ResBlock j: cur_j = y; for each pair m:
-          t_a = lrelu(convs1[m](t_in))            conv + leaky_relu_io (dec.hpp:323-324)
-          cur_j += convs2[m](t_a); t_in = lrelu(cur_j)   conv + add_inplace + next leaky_relu_write
-                                                  (the first pair reads y as its residual and
-                                                  writes cur_j: no copy of y)
+          t_a = lrelu(convs1[m](lrelu(cur_j)))    leaky_relu_write (dec.hpp:322) applied as the
+                                                  conv reads its input (CONV_X_LRELU), the
+                                                  leaky_relu_io after it (dec.hpp:323-324) in its
+                                                  store: no t_in tensor
+          cur_j += convs2[m](t_a)                 conv + add_inplace (dec.hpp:325-326); the first
+                                                  pair reads y as its residual and writes cur_j:
+                                                  no copy of y
       out = lrelu(mean_j cur_j, slope_next)       mul_write / add_scaled_inplace + the next stage's
                                                   leaky_relu_io (dec.hpp:328-336, 284 or 342)
     Launches: 1 upsampler, 18 convolutions, 1 branch mean."""
@@ -293,23 +296,21 @@ class GeneratorStage:
         key = (C, T, dtype, device)
         if self._buf is None or self._buf[0] != key:
             mk = lambda: torch.empty(C, T, dtype=dtype, device=device)
-            self._buf = (key, mk(), mk(), mk(), mk(), [mk() for _ in self.resblocks])
+            self._buf = (key, mk(), mk(), [mk() for _ in self.resblocks])
         return self._buf[1:]
 
     def forward(self, x, out, slope_next=0.1, round_x=False, stream=None):
-        y, t_in0, t_in, t_a, curs = self._buffers(self.ups.out_c, x.shape[1] * self.ups.stride_u,
-                                                  x.dtype, x.device)
-        self.ups.forward(x, y, epi=CONV_EPI_DUAL, slope=0.1, cur=t_in0, round_x=round_x,
-                         stream=stream)
+        y, t_a, curs = self._buffers(self.ups.out_c, x.shape[1] * self.ups.stride_u, x.dtype,
+                                     x.device)
+        self.ups.forward(x, y, round_x=round_x, stream=stream)
         for rb, cur in zip(self.resblocks, curs):
-            src, res = t_in0, y
-            for m, (c1, c2) in enumerate(zip(rb.convs1, rb.convs2)):
-                c1.forward(src, t_a, epi=CONV_EPI_LRELU, slope=0.1, round_x=round_x, stream=stream)
-                last = m + 1 == len(rb.convs2)
-                c2.forward(t_a, None if last else t_in,
-                           epi=CONV_EPI_RES if last else CONV_EPI_RES_LRELU, slope=0.1, cur=cur,
-                           res=res, round_x=round_x, stream=stream)
-                src, res = t_in, None
+            src, res = y, y
+            for c1, c2 in zip(rb.convs1, rb.convs2):
+                c1.forward(src, t_a, epi=CONV_EPI_LRELU | CONV_X_LRELU, slope=0.1, round_x=round_x,
+                           stream=stream)
+                c2.forward(t_a, None, epi=CONV_EPI_RES, cur=cur, res=res, round_x=round_x,
+                           stream=stream)
+                src, res = cur, None
         resblock_branch_mean(curs, None, out, True, slope_next, stream=stream)
         return out
 

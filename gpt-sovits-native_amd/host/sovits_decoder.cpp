@@ -14,11 +14,12 @@ constexpr size_t kAlign = 256;  // bytes: alignment of every workspace region
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout: the folded bias (c0 floats), then 8 activation slots of `slot` elements of the
+// Workspace layout: the folded bias (c0 floats), then 6 activation slots of `slot` elements of the
 // activation dtype each: X (stage input, then the stage output), Y (upsampler output, the first
-// residual), TIN0 (lrelu(Y)), TIN (the next pair's LeakyReLU input), TA (the pair's middle
-// activation) and CUR0..CUR2 (the three branch accumulators).
-enum Slot { kX, kY, kTin0, kTin, kTa, kCur0, kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS };
+// residual), TA (the pair's middle activation) and CUR0..CUR2 (the three branch accumulators).
+// The pairs' LeakyReLU inputs are not stored: the first conv of a pair reads lrelu(cur) as it
+// loads (GSVK_CONV_X_LRELU).
+enum Slot { kX, kY, kTa, kCur0, kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS };
 
 struct Layout {
   size_t vec_bytes = 0;   // bytes of the folded bias (c0 floats, rounded up)
@@ -112,31 +113,29 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
   for (size_t s = 0; s < d->n_stages; ++s) {
     const gsvk_sovits_stage& S = d->stage[s];
     const size_t C = S.c_out, Tu = T * S.ups_u;
-    // y = ups(x), t_in0 = lrelu(y)  (dec.hpp:285; the first pair's leaky_relu_write, dec.hpp:322)
-    if ((rc = gsvk_convt1d(dt, rx, slot[kX], T, S.ups_w, S.ups_b, GSVK_CONV_EPI_DUAL, slope,
-                           slot[kTin0], nullptr, Tu, slot[kY], Tu, S.c_in, C, T, S.ups_k, S.ups_u,
-                           st)))
+    // y = ups(x)  (dec.hpp:285)
+    if ((rc = gsvk_convt1d(dt, rx, slot[kX], T, S.ups_w, S.ups_b, GSVK_CONV_EPI_BIAS, 0.f, nullptr,
+                           nullptr, 0, slot[kY], Tu, S.c_in, C, T, S.ups_k, S.ups_u, st)))
       return rc;
     T = Tu;
     const void* curs[GSVK_SOVITS_RESBLOCKS];
     for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS; ++j) {
       void* cur = slot[kCur0 + j];
       curs[j] = cur;
-      const void* src = slot[kTin0];
-      const void* res = slot[kY];  // cur_j starts as a copy of y (dec.hpp:316): read it in place
+      const void* src = slot[kY];  // cur_j starts as a copy of y (dec.hpp:316): read it in place
+      const void* res = slot[kY];
       for (size_t m = 0; m < GSVK_SOVITS_PAIRS; ++m) {
-        // t_a = lrelu(convs1[m](t_in))  (dec.hpp:323-324)
-        if ((rc = gsvk_conv1d(dt, rx, src, T, S.w1[j][m], S.b1[j][m], GSVK_CONV_EPI_LRELU, slope,
-                              nullptr, nullptr, 0, slot[kTa], T, C, C, T, S.res_k[j], S.res_dil[m],
-                              st)))
+        // t_a = lrelu(convs1[m](lrelu(cur_j)))  (dec.hpp:322-324: leaky_relu_write as the
+        // convolution reads its input, leaky_relu_io in its store)
+        if ((rc = gsvk_conv1d(dt, rx, src, T, S.w1[j][m], S.b1[j][m],
+                              GSVK_CONV_EPI_LRELU | GSVK_CONV_X_LRELU, slope, nullptr, nullptr, 0,
+                              slot[kTa], T, C, C, T, S.res_k[j], S.res_dil[m], st)))
           return rc;
-        // cur_j = res + convs2[m](t_a) (dec.hpp:325-326); t_in = lrelu(cur_j) for the next pair
-        const bool last = m + 1 == GSVK_SOVITS_PAIRS;
-        if ((rc = gsvk_conv1d(dt, rx, slot[kTa], T, S.w2[j][m], S.b2[j][m],
-                              last ? GSVK_CONV_EPI_RES : GSVK_CONV_EPI_RES_LRELU, slope, cur, res,
-                              T, last ? nullptr : slot[kTin], T, C, C, T, S.res_k[j], 1, st)))
+        // cur_j = res + convs2[m](t_a)  (dec.hpp:325-326)
+        if ((rc = gsvk_conv1d(dt, rx, slot[kTa], T, S.w2[j][m], S.b2[j][m], GSVK_CONV_EPI_RES, slope,
+                              cur, res, T, nullptr, T, C, C, T, S.res_k[j], 1, st)))
           return rc;
-        src = slot[kTin];
+        src = cur;
         res = nullptr;  // in place from the second pair on
       }
     }

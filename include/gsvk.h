@@ -54,6 +54,10 @@ typedef enum gsvk_conv_epi {
   GSVK_CONV_EPI_DUAL = 4,       /* y = conv + bias and cur = lrelu(y)  upsampler + the first pair's
                                    leaky_relu_write (dec.hpp:285, 322) */
   GSVK_CONV_EPI_TANH = 5,       /* y = tanh(conv + bias)              conv_post then tanh (dec.hpp:343-344) */
+  /* Flag OR-ed into epi: the convolution reads lrelu(x, slope) instead of x (the same slope as
+     the epilogue's), i.e. leaky_relu_write into t_in then the conv (dec.hpp:322-323) in one pass
+     without t_in. */
+  GSVK_CONV_X_LRELU = 0x100,
 } gsvk_conv_epi;
 
 typedef enum gsvk_status {
@@ -164,7 +168,10 @@ size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t 
  *   pad = (k - 1) * dilation / 2, x = 0 outside [0, T); the output has T columns.
  *   epi (gsvk_conv_epi): BIAS y = v; LRELU y = lrelu(v, slope); RES_LRELU cur = r + v, y =
  *   lrelu(cur, slope) (from the fp32 sum); RES cur = r + v (y may be NULL); DUAL y = v, cur =
- *   lrelu(v, slope); TANH y = tanhf(v). For RES_LRELU / RES the residual r is read from `res`
+ *   lrelu(v, slope); TANH y = tanhf(v). With GSVK_CONV_X_LRELU OR-ed into epi, every x value is
+ *   replaced by lrelu(x, slope) as it is read (x itself unchanged; the sum then runs on that value:
+ *   exact for F32, rounded to fp16 with round_x or F16 storage, as a stored lrelu(x) would be).
+ *   For RES_LRELU / RES the residual r is read from `res`
  *   (row stride ldc) or, when res is NULL or equal to cur, from cur itself (in place): a branch's
  *   first pair can then add onto the stage input without copying it into cur first.
  * Replaces Conv1d::forward (src/sovits/conv1d.hpp:109-194: im2col, sgemm, add_bias) and, fused

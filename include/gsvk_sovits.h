@@ -9,9 +9,9 @@
  *                                            (dec.hpp:275-279) folded into its output
  *   x    = lrelu(conv_pre(z) + bias, 0.1)    (dec.hpp:268, 275-279, 284)          1 launch
  *   per stage s (dec.hpp:283-336):                                               20 launches
- *     y = ups(x), t_in = lrelu(y, 0.1)                                  (DUAL epilogue)
- *     per ResBlock j, pair m: t_a = lrelu(convs1[m](t_in)); cur_j = (m ? cur_j : y) +
- *                             convs2[m](t_a); t_in = lrelu(cur_j)       (LRELU / RES_LRELU / RES)
+ *     y = ups(x)
+ *     per ResBlock j, pair m: t_a = lrelu(convs1[m](lrelu(c))), c = m ? cur_j : y   (X_LRELU input,
+ *                             LRELU epilogue); cur_j = c + convs2[m](t_a)           (RES epilogue)
  *     x = lrelu(sum_j cur_j * (1/3), s < last ? 0.1 : 0.01)             (branch mean, dec.hpp:342)
  *   out  = tanh(conv_post(x))                [1, T out]    (dec.hpp:343-344)       1 launch
  *

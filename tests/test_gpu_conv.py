@@ -385,3 +385,36 @@ def test_wide_tiles_transposed():
     geometry, narrowed)."""
     check_t(F32, 128, 64, 12289, 16, 8, seed=530)
     check_t(F32, 128, 64, 12289, 16, 8, epi=gsvk.CONV_EPI_RES_LRELU, seed=531)
+
+
+@pytest.mark.parametrize("dt,round_x", [(F32, False), (F32, True), (F16, False)])
+def test_x_lrelu_input_equals_materialized_lrelu(dt, round_x):
+    """GSVK_CONV_X_LRELU reads lrelu(x, slope) as the convolution loads x: bit for bit the same as
+    materialising lrelu(x) first (gsvk_leaky_relu, one rounding to the storage type) and convolving
+    that, for the convolution (both tile shapes' grids) and the transposed convolution; x itself is
+    left unchanged."""
+    r = rng(600 + dt + 2 * round_x)
+    for C, T, k, dil in ((48, 3000, 7, 3), (64, 98305, 3, 1)):
+        x, w, b, _ = make(r, C, C, T, k, dt)
+        xd = dev(x, dt)
+        x0 = xd.clone()
+        conv = gsvk.Conv1d(dev(w, F16), devf(b), dil)
+        ya = conv.forward(xd, epi=gsvk.CONV_EPI_LRELU | gsvk.CONV_X_LRELU, slope=0.1,
+                          round_x=round_x)
+        xl = torch.empty_like(xd)
+        gsvk.leaky_relu(xd, xl, 0.1)
+        yb = conv.forward(xl, epi=gsvk.CONV_EPI_LRELU, slope=0.1, round_x=round_x)
+        torch.cuda.synchronize()
+        assert torch.equal(xd.view(torch.int16), x0.view(torch.int16))
+        assert torch.equal(ya.view(torch.int16), yb.view(torch.int16)), f"{C}x{T}"
+    cin, cout, T, k, u = 96, 48, 700, 8, 2
+    x = O.to_storage(dt, r.standard_normal((cin, T)).astype(np.float32))
+    w = (r.standard_normal((cin, cout, k)) / np.sqrt(cin * k / u)).astype(np.float16)
+    xd = dev(x, dt)
+    up = gsvk.ConvT1d(dev(w.view(np.uint16), F16), None, u)
+    ya = up.forward(xd, epi=gsvk.CONV_EPI_BIAS | gsvk.CONV_X_LRELU, slope=0.1, round_x=round_x)
+    xl = torch.empty_like(xd)
+    gsvk.leaky_relu(xd, xl, 0.1)
+    yb = up.forward(xl, round_x=round_x)
+    torch.cuda.synchronize()
+    assert torch.equal(ya.view(torch.int16), yb.view(torch.int16))
