@@ -164,3 +164,40 @@ def test_embed_large_bit_exact(rows):
                   pos=torch.from_numpy(pos).cuda())
     sync()
     assert_bitexact(out_dt, host(OUT, out_dt), want, "large embed")
+
+
+def test_embed_long_call_rows_split_by_position():
+    """Calls past 256 MiB of output (the non-temporal path): every row written once, bit for bit,
+    including text rows (mm + bias), invalid ids / positions (NaN rows and the error flag) and
+    implicit positions."""
+    r = rng(41)
+    D, rows = 512, 262147
+    pe = gsvk.pe_table(2048, D)
+    tab = (0.02 * randn(r, (732, D))).astype(np.float16).view(np.uint16)
+    ids = r.integers(0, 732, rows).astype(np.int64)
+    pos = r.integers(0, 2048, rows).astype(np.int64)
+    ids[[5, 70000, rows - 1]] = [732, -1, 9999]        # out-of-range ids
+    pos[[6, 131072, rows - 2]] = [2048, -3, 1 << 40]   # out-of-range positions
+    mm = O.to_storage(F16, randn(r, (rows, D), 1.0))
+    bias = randn(r, D, 0.02)
+    want, bad = O.embed_pe(F16, F16, tab, ids, pe, 0.9, pos=pos, mm=mm, bias=bias)
+    assert bad == 6
+    OUT = torch.empty((rows, D), dtype=torch.float16, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    gsvk.embed_pe(dev(tab, F16), torch.from_numpy(ids).cuda(), devf(pe), 0.9, OUT,
+                  pos=torch.from_numpy(pos).cuda(), mm=dev(mm, F16), bias=devf(bias), err=err)
+    sync()
+    assert int(err.item()) == 1
+    assert_bitexact(F16, host(OUT, F16), want, "long embed, text rows")
+    del OUT, want, mm
+    # implicit positions pos0 + r over 2^20 + 1 rows of 64 fp32 columns
+    D, rows, pos0 = 64, (1 << 20) + 1, 3
+    pe = gsvk.pe_table(rows + pos0, D)
+    tab = (0.02 * randn(r, (1025, D))).astype(np.float16).view(np.uint16)
+    ids = r.integers(0, 1025, rows).astype(np.int64)
+    want, bad = O.embed_pe(F32, F16, tab, ids, pe, 0.7, pos0=pos0)
+    assert bad == 0
+    OUT = torch.empty((rows, D), dtype=torch.float32, device="cuda")
+    gsvk.embed_pe(dev(tab, F16), torch.from_numpy(ids).cuda(), devf(pe), 0.7, OUT, pos0=pos0)
+    sync()
+    assert_bitexact(F32, host(OUT, F32), want, "long embed, implicit positions")
