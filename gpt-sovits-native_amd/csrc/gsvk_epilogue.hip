@@ -14,6 +14,8 @@
 // file is built with -ffp-contract=off, so no multiply-add is fused unless written as fmaf).
 #include <cmath>
 
+#include <algorithm>
+
 #include "gsvk_common.hpp"
 
 namespace gsvk {
@@ -484,6 +486,27 @@ void launch_scaled_add(const EwArgs& a, hipStream_t st) {
   else launch_scaled_add_nt<DT, false>(a, st);
 }
 
+// fp32 -> fp16 storage, round to nearest even (subnormals kept, overflow to inf, NaN stays NaN):
+// kern::f32_to_f16 (gemv_fmlal.cpp:23-35, vcvt_f16_f32). 8 elements per thread per step from 32
+// aligned bytes (vec), else one.
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ x,
+                                                         uint16_t* __restrict__ y, long n, int vec) {
+  const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+  const long t0 = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (vec) {
+    const long n8 = n / 8;
+    for (long i = t0; i < n8; i += stride) {
+      const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
+      const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+      reinterpret_cast<uint4*>(y)[i] =
+          uint4{f2h2(a.x, a.y), f2h2(a.z, a.w), f2h2(b.x, b.y), f2h2(b.z, b.w)};
+    }
+    for (long i = n8 * 8 + t0; i < n; i += stride) y[i] = static_cast<uint16_t>(f2h(x[i]));
+  } else {
+    for (long i = t0; i < n; i += stride) y[i] = static_cast<uint16_t>(f2h(x[i]));
+  }
+}
+
 }  // namespace
 }  // namespace gsvk
 
@@ -648,5 +671,17 @@ extern "C" int gsvk_scaled_add(int dtype, const void* acc, const void* src, void
   } else {
     launch_scalar_dt(dtype, a, 3, st);
   }
+  return launch_status();
+}
+
+extern "C" int gsvk_f32_to_f16(const float* x, uint16_t* y, size_t n, void* stream) {
+  if (!x || !y) return GSVK_E_NULL;
+  if (n == 0 || n > (1ul << 40)) return GSVK_E_SIZE;
+  if (overlaps(y, n * 2, x, n * 4)) return GSVK_E_ALIAS;
+  if (reinterpret_cast<uintptr_t>(x) % 4 || reinterpret_cast<uintptr_t>(y) % 2) return GSVK_E_ARG;
+  const int vec = aligned16(x) && aligned16(y);
+  const long blocks = std::min<long>((static_cast<long>(n) / 8 + 255) / 256 + 1, 8192);
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, y, static_cast<long>(n), vec);
   return launch_status();
 }

@@ -47,6 +47,7 @@ SIGNATURES = {
     "gsvk_resblock_branch_mean": (_i, [_i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i, _vp, _sz,
                                        _i, _f, _vp]),
     "gsvk_scaled_add": (_i, [_i, _vp, _vp, _vp, _sz, _f, _vp]),
+    "gsvk_f32_to_f16": (_i, [_vp, _vp, _sz, _vp]),
     "gsvk_embed_pe": (_i, [_i, _i, _i, _vp, _sz, _vp, _vp, _i64, _vp, _sz, _f, _vp, _vp, _vp, _sz,
                            _sz, _vp, _vp]),
     "gsvk_pe_table": (_i, [_vp, _sz, _sz]),
@@ -483,6 +484,15 @@ def scaled_add(acc, src, out, scale, stream=None):
                                                            _stream(stream)))
 
 
+def f32_to_f16(x, y=None, stream=None):
+    """fp16 copy of an fp32 device tensor, round to nearest even (kern::f32_to_f16)."""
+    import torch
+    if y is None:
+        y = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    _check("gsvk_f32_to_f16", lib().gsvk_f32_to_f16(_ptr(x), _ptr(y), x.numel(), _stream(stream)))
+    return y
+
+
 def embed_pe(table, ids, pe, alpha, out, pos=None, pos0=0, mm=None, bias=None, err=None,
              stream=None):
     import torch
@@ -801,7 +811,7 @@ def sovits_decoder_from_gsv(g, z, ge, out, round_x=False, graph=True, dev="cuda"
     """A SovitsDecoder over the Generator weights of a sovits .gsv, by the names Generator::load
     reads (dec.hpp:54-75): conv_pre, cond, ups.{i}, resblocks.{3 i + j}.convs{1,2}.{m}, conv_post.
     Each weight comes as load_tensor_f16 takes it (sovits_types.hpp:76-87): the tensor's fp16 copy
-    when the file has one, else its fp32 values rounded to fp16 (to nearest even) on the device;
+    when the file has one, else its fp32 values rounded to fp16 on the device (gsvk_f32_to_f16);
     biases are fp32 (absent: zeros, as for conv_post). Channel counts and kernel sizes come from
     the tensors' shapes, strides and dilations are the model's. Returns (decoder, arenas)."""
     a16, t16 = g.upload(F16, dev, stream)
@@ -812,7 +822,7 @@ def sovits_decoder_from_gsv(g, z, ge, out, round_x=False, graph=True, dev="cuda"
             return t16[name]
         if name not in t32:
             raise GsvkError(f"sovits_decoder_from_gsv: missing tensor {name}", E_FORMAT)
-        return t32[name].half()
+        return f32_to_f16(t32[name], stream=stream)
 
     def b32(name):
         return t32.get(name)

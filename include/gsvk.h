@@ -277,6 +277,14 @@ int gsvk_scaled_add(int dtype, const void* acc, const void* src, void* out, size
                     void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * fp32 -> fp16 storage: y[k] = fp16(x[k]) rounded to nearest even (subnormals kept, overflow to
+ * inf, NaN stays NaN), bit-exact. Replaces kern::f32_to_f16 (src/kern/gemv_fmlal.cpp:23-35), the
+ * conversion load_tensor_f16 applies to a weight stored without an fp16 copy
+ * (src/sovits/sovits_types.hpp:76-87). x and y must not overlap.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_f32_to_f16(const float* x, uint16_t* y, size_t n, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Token-embedding gather fused with the scaled sinusoidal positional add, bit-exact.
  *   p = pos ? pos[r] : pos0 + r
  *   e = float(table[id_r, :])                           (exact upcast of f16 / bf16 / f32 rows)

@@ -227,6 +227,16 @@ def test_embed_validation(gsvk_lib):
     assert call(outp=C + 16) == gsvk.E_ALIAS     # writes over the PE table
 
 
+def test_f32_to_f16_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_f32_to_f16
+    assert f(None, 0x1000, 8, None) == gsvk.E_NULL
+    assert f(0x1000, None, 8, None) == gsvk.E_NULL
+    assert f(0x1000, 0x8000, 0, None) == gsvk.E_SIZE
+    assert f(0x1000, 0x1010, 8, None) == gsvk.E_ALIAS     # y inside x's 32 bytes
+    assert f(0x1002, 0x8000, 8, None) == gsvk.E_ARG       # x not 4-byte aligned
+    assert f(0x1000, 0x8001, 8, None) == gsvk.E_ARG       # y not 2-byte aligned
+
+
 def test_t2s_step_validation(gsvk_lib):
     out = ctypes.c_void_p()
     assert gsvk_lib.gsvk_t2s_step_create(None, ctypes.byref(out)) == gsvk.E_NULL
@@ -352,3 +362,13 @@ void engine_like(float* x, const float* g, const float* b, float* ff, float* cur
     if r.returncode != 0 and "No such file" in r.stderr and "hipcc" in r.stderr:
         pytest.skip("hipcc not available")
     assert r.returncode == 0, r.stderr[-2000:]
+
+
+def test_sovits_run_example_usage():
+    """The C++ mirror's example program is built and rejects a wrong command line before touching
+    the GPU (exit status 2, usage on stderr)."""
+    exe = os.path.join(ROOT, "gpt-sovits-native_amd", "sovits_run")
+    if not os.path.exists(exe):
+        pytest.skip("sovits_run not built")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stderr

@@ -122,3 +122,40 @@ def test_sovits_decoder_from_gsv_matches_oracle(tmp_path):
     err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
     say(f"sovits decoder from .gsv: max |d| {err:.2e}")
     assert np.isfinite(got).all() and err <= 1e-4
+
+
+def test_cpp_generator_mirror_matches_python_decoder(tmp_path):
+    """The C++ host mirror (gsv::sovits::Generator in host/gsvk/sovits.hpp, driven by the
+    sovits_run example in its own process) loads the same .gsv by Generator::load's names
+    (dec.hpp:54-75) and runs the same launches as the Python binding's decoder: bit-identical."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(gsvk.__file__), "sovits_run")
+    assert os.path.exists(exe), "sovits_run not built (make -C gpt-sovits-native_amd)"
+    c_z, c0, g_in, frames = 16, 64, 32, 9
+    t = sovits_dec_tensors(c_z, c0, g_in, seed=21)
+    no16 = [k for k in t if k.startswith("dec.resblocks.") and k.endswith(".weight")]
+    p = tmp_path / "s2.gsv"
+    p.write_bytes(gsv_bytes("sovits_v2ProPlus", t, None, no16=no16))
+    r = np.random.default_rng(22)
+    z = r.standard_normal((c_z, frames)).astype(np.float32)
+    ge = r.standard_normal(g_in).astype(np.float32)
+    z.tofile(tmp_path / "z.f32")
+    ge.tofile(tmp_path / "ge.f32")
+    say(f"sovits_run: c0 {c0} frames {frames}")
+    res = subprocess.run([exe, str(p), str(tmp_path / "z.f32"), str(frames),
+                          str(tmp_path / "ge.f32"), str(tmp_path / "out.f32")],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr[-2000:]
+    got = np.fromfile(tmp_path / "out.f32", dtype=np.float32)
+    assert got.shape == (frames * 640,)
+
+    g = gsvk.GsvFile(str(p))
+    out = torch.full((frames * 640,), float("nan"), device="cuda")
+    dec, arenas = gsvk.sovits_decoder_from_gsv(g, torch.from_numpy(z).cuda(),
+                                               torch.from_numpy(ge).cuda(), out, graph=False)
+    dec.run()
+    torch.cuda.synchronize()
+    want = host(out, F32)
+    assert np.isfinite(got).all()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

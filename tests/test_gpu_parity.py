@@ -466,3 +466,26 @@ def test_f16_store_rounds_subnormal_ties_to_even():
     got = host(OUT, F16)[0, :vals.size]
     bad = np.flatnonzero(got != want)
     assert bad.size == 0, (vals[bad[:5]], got[bad[:5]], want[bad[:5]])
+
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (8, 0), (1001, 0), (4099, 1), (1 << 20, 0)])
+def test_f32_to_f16_bit_exact(n, offset):
+    """gsvk_f32_to_f16 (kern::f32_to_f16, gemv_fmlal.cpp:23-35) against numpy's round-to-nearest-
+    even cast, bit for bit: ties, subnormals, overflow to inf, infinities and NaN; vector body and
+    tail, and an output off the 16-byte alignment (element path)."""
+    r = rng(700 + n)
+    x = (r.standard_normal(n) * 10.0 ** r.uniform(-9, 5, n)).astype(np.float32)
+    special = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -70000.0, 2.0 ** -24, 2.0 ** -25,
+                        3 * 2.0 ** -26, 1e-8, np.inf, -np.inf, np.nan, 1.0 + 2.0 ** -11,
+                        1.0 + 3 * 2.0 ** -11, -(2.0 ** -14) * 0.75], dtype=np.float32)
+    x[:min(n, special.size)] = special[:min(n, special.size)]
+    want = x.astype(np.float16).view(np.uint16)
+    xd = devf(x)
+    buf = torch.zeros(n + offset, dtype=torch.float16, device="cuda")
+    y = buf[offset:]
+    gsvk.f32_to_f16(xd, y)
+    sync()
+    got = y.cpu().view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(np.isnan(got.view(np.float16)), nan)
+    assert np.array_equal(got[~nan], want[~nan])
