@@ -30,6 +30,7 @@
 // hi = f16(x) and lo = f16(x - hi) through two MFMAs: x - hi is exact and lo holds the next 11
 // bits, so hi + lo equals x to about 2^-22 relative (|x| < 65504).
 #include <algorithm>
+#include <cmath>
 
 #include "gsvk_common.hpp"
 
@@ -55,6 +56,14 @@ struct GvArgs {
   int act;
   float slope;
   bool vec_store;
+  // LayerNorm prologue (the LN instantiations): x holds the pre-norm rows, the products use
+  // h = LN(x) (gamma / beta may be null: ones / zeros), and column-block 0 stores h to ln_y.
+  const float* ln_g = nullptr;
+  const float* ln_b = nullptr;
+  void* ln_y = nullptr;
+  long ldh = 0;
+  float ln_eps = 0.f;
+  double inv_n = 0.0;  // 1.0 / K, computed on the host
 };
 
 __device__ __forceinline__ float act_rt(int act, float v, float slope) {
@@ -150,6 +159,8 @@ template <int XM, int MF, int NF>
 struct Raw {
   u32x4 w[NF][2];
   u32x4 x[MF][x_insts<XM>()];
+  u32x4 g[XM == kXF16 ? 2 : 1], b[XM == kXF16 ? 2 : 1];  // LN: gamma / beta of the lane's k
+  long kb;                                                // LN: the block (for the h store)
   bool okw, okx;
 };
 
@@ -160,7 +171,7 @@ constexpr int stage_halves() {
   return (NF + MF * (XM == kXSplit ? 2 : 1)) * 16 * kRowHalves;
 }
 
-template <int XM, int YDT, int MF, int NF, int WK, int D, bool TAIL>
+template <int XM, int YDT, int MF, int NF, int WK, int D, bool TAIL, bool LN>
 __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
   constexpr int T = MF * NF;  // 16 x 16 output tiles of the workgroup
   constexpr int SH = stage_halves<XM, MF, NF>();
@@ -206,6 +217,7 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
           static_cast<size_t>(min(m0 + 16 * i + (16 / XQ) * q + lane / XLPR, a.M - 1)) * a.ldx;
 
   auto load = [&](Raw<XM, MF, NF>& r, long kb) {
+    r.kb = kb;
     const long kw = kb * 64 + (lane % 8) * 8;  // 8 halves per lane
     r.okw = !TAIL || kw < a.K;
     const size_t kcw = static_cast<size_t>(r.okw ? kw : a.K - 8);
@@ -230,6 +242,86 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
         for (int q = 0; q < 4; ++q)
           r.x[i][q] = ld16<false>(static_cast<const float*>(a.x) + xrow[i][q] + kcx);
     }
+    if constexpr (LN) {
+      // the lane's 8 (16-bit x) or 4 (fp32 x) k of this block, clamped like the x loads
+      const size_t kc = XM == kXF16 ? kcw
+                                    : static_cast<size_t>(!TAIL || kb * 64 + (lane % 16) * 4 < a.K
+                                                              ? kb * 64 + (lane % 16) * 4
+                                                              : a.K - 4);
+#pragma unroll
+      for (int q = 0; q < (XM == kXF16 ? 2 : 1); ++q) {
+        r.g[q] = ld16<false>(param_or(a.ln_g, kc + 4 * q, kOnes8));
+        r.b[q] = ld16<false>(param_or(a.ln_b, kc + 4 * q, kZeros8));
+      }
+    }
+  };
+
+  // LayerNorm prologue (LN). The host launches it only when every wave's k blocks fit in its D
+  // load slots, so the activations of the workgroup's 16 MF rows over all of K are in registers
+  // once the first loads land: the statistics come from them, with no second read. Per row:
+  // each lane sums its in-range values in k order, the lanes that share the row add up with DPP,
+  // and the per-wave partials are added in wave order through LDS; mean = float(sum * (1/K)) in
+  // double, then the centred second moment the same way, rstd = rsq(var + eps): ln_rows_tile's
+  // formulas (csrc/gsvk_norm.hip) in another summation order.
+  __shared__ float ln_part[LN ? WK * 16 * MF : 1];
+  float lmean[MF][XQ], lrstd[MF][XQ];
+  const bool store_h = LN && a.ln_y != nullptr && blockIdx.x == 0;
+  auto row_sum = [&](float v) {  // over the XLPR consecutive lanes that hold one row
+    v += dpp_f32<0xB1>(v);       // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);       // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);      // row_half_mirror: 8 lanes
+    if constexpr (XLPR == 16) v += dpp_f32<0x140>(v);  // row_mirror: 16 lanes
+    return v;
+  };
+  // pass 0: sum of x; pass 1: sum of (x - mean)^2. Lanes past K and blocks past the wave's range
+  // add nothing.
+  auto ln_pass = [&](const Raw<XM, MF, NF>(&f)[D], int pass, float (&out)[MF][XQ]) {
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) {
+        float p = 0.f;
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+          if (kb0 + s < kb1 && f[s].okx) {
+            float v[XQ == 2 ? 8 : 4];
+            if constexpr (XM == kXF16) Store<GSVK_F16>::unpack(f[s].x[i][q], v);
+            else Store<GSVK_F32>::unpack(f[s].x[i][q], v);
+#pragma unroll
+            for (int k = 0; k < (XQ == 2 ? 8 : 4); ++k) {
+              if (pass == 0) {
+                p += v[k];
+              } else {
+                const float d = v[k] - lmean[i][q];
+                p = __builtin_fmaf(d, d, p);
+              }
+            }
+          }
+        }
+        p = row_sum(p);
+        if (lane % XLPR == 0) ln_part[wave * 16 * MF + 16 * i + (16 / XQ) * q + lane / XLPR] = p;
+      }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) {
+        const int rr = 16 * i + (16 / XQ) * q + lane / XLPR;
+        float t = ln_part[rr];
+#pragma unroll
+        for (int w = 1; w < WK; ++w) t += ln_part[w * 16 * MF + rr];
+        out[i][q] = static_cast<float>(static_cast<double>(t) * a.inv_n);
+      }
+    __syncthreads();  // the partials area is reused by the next pass
+  };
+  auto ln_prologue = [&](const Raw<XM, MF, NF>(&f)[D]) {
+    ln_pass(f, 0, lmean);
+    float var[MF][XQ];
+    ln_pass(f, 1, var);
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) lrstd[i][q] = __builtin_amdgcn_rsqf(var[i][q] + a.ln_eps);
   };
 
   _Float16* st_w = reinterpret_cast<_Float16*>(smem) + wave * SH;
@@ -248,15 +340,45 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < 2; ++q) {
+          u32x4 v = r.x[i][q];
+          if constexpr (LN) {
+            float h[8], o[8];
+            Store<GSVK_F16>::unpack(v, h);
+            const f4v g0 = __builtin_bit_cast(f4v, r.g[0]), g1 = __builtin_bit_cast(f4v, r.g[1]);
+            const f4v b0 = __builtin_bit_cast(f4v, r.b[0]), b1 = __builtin_bit_cast(f4v, r.b[1]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              o[k] = __builtin_fmaf((h[k] - lmean[i][q]) * lrstd[i][q], k < 4 ? g0[k] : g1[k - 4],
+                                    k < 4 ? b0[k] : b1[k - 4]);
+            v = Store<GSVK_F16>::pack(o);
+            const long row = m0 + 16 * i + 8 * q + lane / 8;
+            if (store_h && r.okx && row < a.M)
+              st16<false>(static_cast<uint16_t*>(a.ln_y) + static_cast<size_t>(row) * a.ldh +
+                              r.kb * 64 + (lane % 8) * 8,
+                          v);
+          }
           *reinterpret_cast<u32x4*>(st_x + (i * 16 + 8 * q + lane / 8) * kRowHalves +
-                                    (lane % 8) * 8) = r.okx ? r.x[i][q] : zero;
+                                    (lane % 8) * 8) = r.okx ? v : zero;
+        }
     } else {
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f4v f = __builtin_bit_cast(f4v, r.okx ? r.x[i][q] : zero);
+          f4v f = __builtin_bit_cast(f4v, r.x[i][q]);
+          if constexpr (LN) {
+            const f4v g = __builtin_bit_cast(f4v, r.g[0]), b = __builtin_bit_cast(f4v, r.b[0]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              f[k] = __builtin_fmaf((f[k] - lmean[i][q]) * lrstd[i][q], g[k], b[k]);
+            const long row = m0 + 16 * i + 4 * q + lane / 16;
+            if (store_h && r.okx && row < a.M)
+              st16<false>(static_cast<float*>(a.ln_y) + static_cast<size_t>(row) * a.ldh +
+                              r.kb * 64 + (lane % 16) * 4,
+                          __builtin_bit_cast(u32x4, f));
+          }
+          if (!r.okx) f = __builtin_bit_cast(f4v, zero);
           const h4 hi = __builtin_convertvector(f, h4);
           const int off = (i * 16 + 4 * q + lane / 16) * kRowHalves + (lane % 16) * 4;
           *reinterpret_cast<h4*>(st_x + off) = hi;
@@ -310,11 +432,20 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
   // Rolling prefetch: D k blocks of global loads in flight. Block indices past the wave's range
   // are clamped to its last block (an in-bounds reload whose result is not used), so no load sits
   // under a branch.
-  if (kb0 < kb1) {
-    Raw<XM, MF, NF> f[D];
-    const long nr = (kb1 - kb0 + D - 1) / D;
+  Raw<XM, MF, NF> f[D];
+  if constexpr (LN) {
+    // All of the wave's blocks (at most D), then the statistics. A wave with no blocks
+    // (kb0 == kb1 == nkb) loads the last block and never uses it.
 #pragma unroll
-    for (int s = 0; s < D; ++s) load(f[s], min(kb0 + s, kb1 - 1));
+    for (int s = 0; s < D; ++s) load(f[s], max(0L, min(kb0 + s, kb1 - 1)));
+    ln_prologue(f);
+  }
+  if (kb0 < kb1) {
+    const long nr = (kb1 - kb0 + D - 1) / D;
+    if constexpr (!LN) {
+#pragma unroll
+      for (int s = 0; s < D; ++s) load(f[s], min(kb0 + s, kb1 - 1));
+    }
     for (long r = 0; r + 1 < nr; ++r) {
 #pragma unroll
       for (int s = 0; s < D; ++s) {
@@ -397,21 +528,24 @@ __global__ __launch_bounds__(256) void gemv_generic(GvArgs a) {
 
 // ---- launch plan ---------------------------------------------------------------------------------
 
-template <int XM, int YDT, int MF, int NF, int WK, int D>
+template <int XM, int YDT, int MF, int NF, int WK, int D, bool LN>
 void launch_tiles(const GvArgs& a, hipStream_t st) {
   const long gx = (a.N + 16 * NF - 1) / (16 * NF);
   const long gy = (a.M + 16 * MF - 1) / (16 * MF);
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
   // K a multiple of 64 (every decode shape) needs no zeroing of a partial last k block.
   if (a.K % 64 == 0)
-    hipLaunchKernelGGL((gemv_mfma<XM, YDT, MF, NF, WK, D, false>), grid, dim3(kWave * WK), 0, st, a);
+    hipLaunchKernelGGL((gemv_mfma<XM, YDT, MF, NF, WK, D, false, LN>), grid, dim3(kWave * WK), 0,
+                       st, a);
   else
-    hipLaunchKernelGGL((gemv_mfma<XM, YDT, MF, NF, WK, D, true>), grid, dim3(kWave * WK), 0, st, a);
+    hipLaunchKernelGGL((gemv_mfma<XM, YDT, MF, NF, WK, D, true, LN>), grid, dim3(kWave * WK), 0,
+                       st, a);
 }
 
-template <int XM, int YDT>
+// LN (the LayerNorm prologue) is only launched tiled: the host checks the tile conditions first.
+template <int XM, int YDT, bool LN>
 void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
-  if (!tiled) {
+  if (!tiled && !LN) {
     const long blocks = std::min<long>((a.M * a.N + 255) / 256, 4096);
     hipLaunchKernelGGL((gemv_generic<XM, YDT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        st, a);
@@ -424,22 +558,36 @@ void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
   // K over 4 or 8 waves with two k blocks each in flight (measured best on MI355X at B = 64 for
   // K = 512 and 2048).
   if (tiles >= 16384) {
-    if (nkb > 16) return launch_tiles<XM, YDT, 4, 4, 2, 2>(a, st);
-    return launch_tiles<XM, YDT, 4, 2, 4, 2>(a, st);
+    if (nkb > 16) return launch_tiles<XM, YDT, 4, 4, 2, 2, LN>(a, st);
+    return launch_tiles<XM, YDT, 4, 2, 4, 2, LN>(a, st);
   }
-  if (nkb >= 16) return launch_tiles<XM, YDT, 1, 1, 8, 2>(a, st);
-  if (nkb >= 8) return launch_tiles<XM, YDT, 1, 1, 4, 2>(a, st);
-  if (nkb >= 4) return launch_tiles<XM, YDT, 1, 1, 4, 1>(a, st);
-  if (nkb >= 2) return launch_tiles<XM, YDT, 1, 1, 2, 1>(a, st);
-  launch_tiles<XM, YDT, 1, 1, 1, 1>(a, st);
+  if (nkb >= 16) return launch_tiles<XM, YDT, 1, 1, 8, 2, LN>(a, st);
+  if (nkb >= 8) return launch_tiles<XM, YDT, 1, 1, 4, 2, LN>(a, st);
+  if (nkb >= 4) return launch_tiles<XM, YDT, 1, 1, 4, 1, LN>(a, st);
+  if (nkb >= 2) return launch_tiles<XM, YDT, 1, 1, 2, 1, LN>(a, st);
+  launch_tiles<XM, YDT, 1, 1, 1, 1, LN>(a, st);
 }
 
-template <int XM>
+// Whether launch_plan's choice for this shape gives every wave at most D k blocks (all of them in
+// registers at once), which the LayerNorm prologue needs. Mirrors launch_plan's thresholds.
+bool ln_resident(long M, long N, long K) {
+  const long nkb = (K + 63) / 64;
+  const long tiles = (N + 15) / 16 * ((M + 15) / 16);
+  if (tiles >= 16384) return false;
+  long wk = 1, d = 1;
+  if (nkb >= 16) wk = 8, d = 2;
+  else if (nkb >= 8) wk = 4, d = 2;
+  else if (nkb >= 4) wk = 4, d = 1;
+  else if (nkb >= 2) wk = 2, d = 1;
+  return (nkb + wk - 1) / wk <= d;
+}
+
+template <int XM, bool LN = false>
 void launch_xm(int ydt, const GvArgs& a, bool tiled, hipStream_t st) {
   switch (ydt) {
-    case GSVK_F32: return launch_plan<XM, GSVK_F32>(a, tiled, st);
-    case GSVK_F16: return launch_plan<XM, GSVK_F16>(a, tiled, st);
-    default: return launch_plan<XM, GSVK_BF16>(a, tiled, st);
+    case GSVK_F32: return launch_plan<XM, GSVK_F32, LN>(a, tiled, st);
+    case GSVK_F16: return launch_plan<XM, GSVK_F16, LN>(a, tiled, st);
+    default: return launch_plan<XM, GSVK_BF16, LN>(a, tiled, st);
   }
 }
 
@@ -480,6 +628,70 @@ extern "C" int gsvk_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ld
     case kXF16: launch_xm<kXF16>(y_dtype, a, tiled, st); break;
     case kXRound: launch_xm<kXRound>(y_dtype, a, tiled, st); break;
     default: launch_xm<kXSplit>(y_dtype, a, tiled, st); break;
+  }
+  return launch_status();
+}
+
+extern "C" int gsvk_gemv_f16w_ln(int x_dtype, int round_x, const void* z, size_t ldz,
+                                 const float* gamma, const float* beta, double eps, void* h,
+                                 size_t ldh, const uint16_t* w, const float* bias, int act,
+                                 float slope, const void* residual, int y_dtype, void* y,
+                                 size_t ldy, size_t rows, size_t out, size_t in, void* stream) {
+  if (x_dtype != GSVK_F32 && x_dtype != GSVK_F16) return GSVK_E_DTYPE;
+  if (!valid_dtype(y_dtype)) return GSVK_E_DTYPE;
+  if (act < GSVK_ACT_NONE || act > GSVK_ACT_LEAKY_RELU) return GSVK_E_DTYPE;
+  if (!z || !h || !w || !y) return GSVK_E_NULL;
+  if (rows == 0 || out == 0 || in == 0 || ldz < in || ldh < in || ldy < out) return GSVK_E_SIZE;
+  if (rows > static_cast<size_t>(kMaxRowGroups) * 16 || out > (1ul << 31) || in > (1ul << 30) ||
+      ldz > (1ul << 40) || ldh > (1ul << 40) || ldy > (1ul << 40))
+    return GSVK_E_SIZE;
+  if (!(eps >= 0.0) || !std::isfinite(eps)) return GSVK_E_ARG;
+  const size_t xsz = dtype_size(x_dtype), ysz = dtype_size(y_dtype);
+  const size_t zbytes = span_bytes(rows, in, ldz, xsz), hbytes = span_bytes(rows, in, ldh, xsz);
+  const size_t ybytes = span_bytes(rows, out, ldy, ysz);
+  // Other workgroups still read z while column block 0 writes h, and every one reads h's
+  // parameters and the weights: h overlaps none of them, nor y.
+  if (overlaps(h, hbytes, z, zbytes) || overlaps(h, hbytes, w, out * in * 2) ||
+      overlaps(h, hbytes, gamma, gamma ? in * 4 : 0) || overlaps(h, hbytes, beta, beta ? in * 4 : 0))
+    return GSVK_E_ALIAS;
+  if (overlaps(y, ybytes, z, zbytes) || overlaps(y, ybytes, h, hbytes) ||
+      overlaps(y, ybytes, w, out * in * 2) || overlaps(y, ybytes, bias, bias ? out * 4 : 0))
+    return GSVK_E_ALIAS;
+  if (residual && residual != y && overlaps(y, ybytes, residual, ybytes)) return GSVK_E_ALIAS;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // The fused form needs the matrix-core tiles (16-byte rows of z and h, K % 8 == 0, 16-byte
+  // parameter vectors) and a launch plan whose waves hold all their k blocks at once (K up to
+  // 1024 at decode batch sizes). Otherwise: the two launches it stands for.
+  const bool fused = in % 8 == 0 && ln_resident(static_cast<long>(rows), static_cast<long>(out),
+                                                static_cast<long>(in)) &&
+                     aligned16(w) && aligned16(z) && aligned16(h) && (ldz * xsz) % 16 == 0 &&
+                     (ldh * xsz) % 16 == 0 && (!gamma || aligned16(gamma)) &&
+                     (!beta || aligned16(beta));
+  if (!fused) {
+    if (ldz != ldh) return GSVK_E_ARG;  // the LayerNorm launch takes one row stride
+    const int rc = gsvk_add_layernorm(x_dtype, z, nullptr, nullptr, gamma, beta, h, rows, in, ldz,
+                                      eps, stream);
+    if (rc) return rc;
+    return gsvk_gemv_f16w(x_dtype, round_x, h, ldh, w, bias, act, slope, residual, y_dtype, y, ldy,
+                          rows, out, in, stream);
+  }
+  GvArgs a{z, w, bias, residual, y, static_cast<long>(rows), static_cast<long>(out),
+           static_cast<long>(in), static_cast<long>(ldz), static_cast<long>(ldy), act, slope,
+           false};
+  a.ln_g = gamma;
+  a.ln_b = beta;
+  a.ln_y = h;
+  a.ldh = static_cast<long>(ldh);
+  a.ln_eps = static_cast<float>(eps);
+  a.inv_n = 1.0 / static_cast<double>(in);
+  const size_t yalign = y_dtype == GSVK_F32 ? 16 : 8;
+  a.vec_store = ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % yalign == 0;
+  const int xm = x_dtype == GSVK_F16 ? kXF16 : (round_x ? kXRound : kXSplit);
+  switch (xm) {
+    case kXF16: launch_xm<kXF16, true>(y_dtype, a, true, st); break;
+    case kXRound: launch_xm<kXRound, true>(y_dtype, a, true, st); break;
+    default: launch_xm<kXSplit, true>(y_dtype, a, true, st); break;
   }
   return launch_status();
 }

@@ -30,6 +30,8 @@ SIGNATURES = {
     "gsvk_bias_act": (_i, [_i, _i, _vp, _vp, _vp, _sz, _sz, _sz, _f, _vp]),
     "gsvk_gemv_f16w": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _i, _vp, _sz, _sz, _sz, _sz,
                             _vp]),
+    "gsvk_gemv_f16w_ln": (_i, [_i, _i, _vp, _sz, _vp, _vp, _d, _vp, _sz, _vp, _vp, _i, _f, _vp, _i,
+                               _vp, _sz, _sz, _sz, _sz, _vp]),
     "gsvk_decode_attention": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz,
                                    _sz, _vp, _sz, _vp, _vp]),
     "gsvk_decode_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
@@ -163,6 +165,23 @@ def gemv_f16w(x, w, y, bias=None, act=ACT_NONE, slope=0.0, residual=None, round_
                   lib().gsvk_gemv_f16w(dtype_code(x), int(round_x), _ptr(x), ldx, _ptr(w),
                                        _ptr(bias), act, slope, _ptr(residual), dtype_code(y),
                                        _ptr(y), ldy, rows, n_out, n_in, _stream(stream)))
+
+
+def gemv_f16w_ln(z, gamma, beta, eps, h, w, y, bias=None, act=ACT_NONE, slope=0.0, residual=None,
+                 round_x=True, stream=None):
+    """h[r] = LN(z[r]) (gamma / beta may be None) and y[r] = act(w @ h[r] + bias) (+ residual[r]) in
+    one launch; z, h [rows, in] of one dtype, y / residual [rows, out] sharing y's row stride."""
+    rows, n_in, ldz = _rows(z)
+    _, _, ldh = _rows(h)
+    n_out = w.shape[0]
+    _, _, ldy = _rows(y)
+    assert residual is None or residual.data_ptr() == y.data_ptr() or _rows(residual)[2] == ldy, \
+        "residual shares y's row stride"
+    return _check("gsvk_gemv_f16w_ln",
+                  lib().gsvk_gemv_f16w_ln(dtype_code(z), int(round_x), _ptr(z), ldz, _ptr(gamma),
+                                          _ptr(beta), float(eps), _ptr(h), ldh, _ptr(w), _ptr(bias),
+                                          act, slope, _ptr(residual), dtype_code(y), _ptr(y), ldy,
+                                          rows, n_out, n_in, _stream(stream)))
 
 
 def conv1d_pack(w, stream=None):

@@ -61,11 +61,19 @@ int issue_decode(const gsvk_t2s_decode_desc* d, void* st) {
                          d->pos, 0, d->pe, d->max_pos, d->alpha, nullptr, nullptr, d->x, B, D,
                          d->err, st);
   if (rc) return rc;
+  // Each post-LN is folded into the GEMV that reads its output (gsvk_gemv_f16w_ln): norm1 into
+  // W1, norm2 into the next layer's QKV or, after the last layer, the logits.
   for (size_t l = 0; l < d->layers; ++l) {
     const gsvk_t2s_layer& L = d->layer[l];
-    if ((rc = gsvk_gemv_f16w(dt, 1, d->x, D, L.wqkv, L.bqkv, GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32,
-                             d->qkv, 3 * D, B, 3 * D, D, st)))
-      return rc;
+    if (l == 0) {
+      rc = gsvk_gemv_f16w(dt, 1, d->x, D, L.wqkv, L.bqkv, GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32,
+                          d->qkv, 3 * D, B, 3 * D, D, st);
+    } else {  // x = norm2_{l-1}(z), qkv = W_qkv x + b  (t2s_engine.cpp:1119, 1044-1049)
+      const gsvk_t2s_layer& P = d->layer[l - 1];
+      rc = gsvk_gemv_f16w_ln(dt, 1, d->z, D, P.n2g, P.n2b, d->eps, d->x, D, L.wqkv, L.bqkv,
+                             GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32, d->qkv, 3 * D, B, 3 * D, D, st);
+    }
+    if (rc) return rc;
     if ((rc = gsvk_decode_attention(d->kv_dtype, dt, d->qkv, 3 * D, L.k_cache, L.v_cache,
                                     d->max_len, d->kv_pos, d->attn, D, B, H, D / H, d->len_bound,
                                     d->workspace, d->workspace_bytes, d->err, st)))
@@ -73,23 +81,21 @@ int issue_decode(const gsvk_t2s_decode_desc* d, void* st) {
     if ((rc = gsvk_gemv_f16w(dt, 1, d->attn, D, L.wout, L.bout, GSVK_ACT_NONE, 0.f, d->x, dt, d->z,
                              D, B, D, D, st)))
       return rc;
-    if ((rc = gsvk_add_layernorm(dt, d->z, nullptr, nullptr, L.n1g, L.n1b, d->h, B, D, D, d->eps,
-                                 st)))
-      return rc;
-    if ((rc = gsvk_gemv_f16w(dt, 1, d->h, D, L.w1, L.b1, GSVK_ACT_RELU, 0.f, nullptr, dt, d->ff, FF,
-                             B, FF, D, st)))
+    // h = norm1(z), ff = relu(W1 h + b1)  (t2s_engine.cpp:1097, 1105-1112)
+    if ((rc = gsvk_gemv_f16w_ln(dt, 1, d->z, D, L.n1g, L.n1b, d->eps, d->h, D, L.w1, L.b1,
+                                GSVK_ACT_RELU, 0.f, nullptr, dt, d->ff, FF, B, FF, D, st)))
       return rc;
     if ((rc = gsvk_gemv_f16w(dt, 1, d->ff, FF, L.w2, L.b2, GSVK_ACT_NONE, 0.f, d->h, dt, d->z, D, B,
                              D, FF, st)))
       return rc;
-    if ((rc = gsvk_add_layernorm(dt, d->z, nullptr, nullptr, L.n2g, L.n2b, d->x, B, D, D, d->eps,
-                                 st)))
-      return rc;
   }
-  if (d->w_logits)
-    return gsvk_gemv_f16w(dt, 1, d->x, D, d->w_logits, nullptr, GSVK_ACT_NONE, 0.f, nullptr,
-                          GSVK_F32, d->logits, d->vocab, B, d->vocab, D, st);
-  return GSVK_OK;
+  const gsvk_t2s_layer& last = d->layer[d->layers - 1];
+  if (d->w_logits)  // x = norm2(z), logits = W_logits x
+    return gsvk_gemv_f16w_ln(dt, 1, d->z, D, last.n2g, last.n2b, d->eps, d->x, D, d->w_logits,
+                             nullptr, GSVK_ACT_NONE, 0.f, nullptr, GSVK_F32, d->logits, d->vocab, B,
+                             d->vocab, D, st);
+  return gsvk_add_layernorm(dt, d->z, nullptr, nullptr, last.n2g, last.n2b, d->x, B, D, D, d->eps,
+                            st);
 }
 
 int count_decode_launches(const gsvk_t2s_decode_desc* d) {
@@ -99,7 +105,9 @@ int count_decode_launches(const gsvk_t2s_decode_desc* d) {
                      d->workspace &&
                      d->workspace_bytes >= gsvk_decode_attention_workspace_bytes(
                                                d->batch, d->heads, d->d_model / d->heads, lb);
-  return static_cast<int>(1 + d->layers * (merge ? 8 : 7) + (d->w_logits ? 1 : 0));
+  // gather; per layer QKV (+ norm2 of the layer before), attention (+ merge), out-proj,
+  // W1 (+ norm1), W2; then the logits (+ the last norm2) or the last norm2 alone
+  return static_cast<int>(1 + d->layers * (merge ? 6 : 5) + 1);
 }
 
 }  // namespace

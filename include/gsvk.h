@@ -131,6 +131,29 @@ int gsvk_gemv_f16w(int x_dtype, int round_x, const void* x, size_t ldx, const ui
                    void* y, size_t ldy, size_t rows, size_t out, size_t in, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * LayerNorm folded into the GEMV that consumes it:
+ *   h[r, :] = LN(z[r, :]; gamma, beta, eps)      as gsvk_add_layernorm(x_dtype, z, NULL, NULL,
+ *                                                gamma, beta, h, rows, in, ., eps)
+ *   y       = gsvk_gemv_f16w(x_dtype, round_x, h, ...)   on that h, with the same bits
+ * in one launch: every workgroup forms its rows' statistics from the activations it has loaded
+ * for the products, normalizes them as it stages them, and the first column block stores h. The
+ * statistics are summed in another order than gsvk_add_layernorm's: h agrees with it within the
+ * LayerNorm tolerance, not bit for bit. No reference function has this form; it is
+ * the post-LN of block_decode_impl followed by the GEMV that reads it: norm1 then W1
+ * (t2s_engine.cpp:1097-1110), norm2 then the next layer's QKV (1119, 1044) or the logits.
+ * The fused form needs every wave of the GEMV's launch plan to hold all its k blocks at once
+ * (in <= 128, 193..256, 449..512 or 961..1024 at decode batch sizes), in % 8 == 0 and 16-byte
+ * aligned rows and vectors; otherwise the call runs the two launches, with their exact results
+ * (then ldz == ldh is required: E_ARG).
+ * h is required and overlaps none of z, w, gamma, beta, y; y overlaps none of z, h, w, bias;
+ * residual == y is allowed. Same tolerance and determinism as gsvk_gemv_f16w.
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_gemv_f16w_ln(int x_dtype, int round_x, const void* z, size_t ldz, const float* gamma,
+                      const float* beta, double eps, void* h, size_t ldh, const uint16_t* w,
+                      const float* bias, int act, float slope, const void* residual, int y_dtype,
+                      void* y, size_t ldy, size_t rows, size_t out, size_t in, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * T2S decode attention with the KV append, B sequences at once.
  *   for each sequence b, p = pos[b]:
  *     k_cache[b, p, :] = k, v_cache[b, p, :] = v      (k, v = qkv[b, D:2D], qkv[b, 2D:3D], rounded

@@ -86,8 +86,11 @@ void gsvk_t2s_step_destroy(gsvk_t2s_step* step);
  * Activations x, h, z, attn, ff are stored in `dtype`; GEMVs round x to fp16 (gemv_fmlal) and
  * accumulate in fp32; the epilogues add in fp32 before the single rounding to `dtype`.
  * pos[b] is the PE position of the new token (P + idx), kv_pos[b] its cache slot (cur_len); the
- * step attends over kv_pos[b] + 1 keys. Per layer: 3 GEMV launches + 2 LayerNorms + the attention
- * (+ 1 chunk merge when len_bound > 256), plus the embedding and the logits GEMV.
+ * step attends over kv_pos[b] + 1 keys. Per layer: 4 GEMV launches and the attention (+ 1 chunk
+ * merge when len_bound > 256); LN1 runs inside the W1 GEMV and LN2 inside the next layer's QKV GEMV
+ * (gsvk_gemv_f16w_ln, within the LayerNorm tolerance of separate launches); plus the embedding
+ * and the logits GEMV
+ * with the last LN2 (a LayerNorm launch when there are no logits).
  * ------------------------------------------------------------------------------------------------ */
 typedef struct gsvk_t2s_layer {
   const uint16_t* wqkv; /* [3D, D] fp16 */

@@ -118,6 +118,32 @@ def test_gemv_validation(gsvk_lib):
     assert call(res=C + 4) == gsvk.E_ALIAS      # residual partly over y (res == y is allowed)
 
 
+def test_gemv_ln_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_gemv_f16w_ln
+    H = A + (1 << 24)  # h: a region of its own
+
+    def call(xdt=1, rx=1, z=A, ldz=64, g=None, b=None, eps=1e-5, h=H, ldh=64, w=B, bias=None,
+             act=0, res=None, ydt=0, y=C, ldy=32, rows=4, out=32, n_in=64):
+        return f(xdt, rx, z, ldz, g, b, eps, h, ldh, w, bias, act, 0.0, res, ydt, y, ldy, rows, out,
+                 n_in, None)
+
+    assert call(xdt=2) == gsvk.E_DTYPE
+    assert call(act=4) == gsvk.E_DTYPE
+    assert call(z=None) == gsvk.E_NULL
+    assert call(h=None) == gsvk.E_NULL          # the LayerNorm output is always written
+    assert call(rows=0) == gsvk.E_SIZE
+    assert call(ldh=63) == gsvk.E_SIZE
+    assert call(eps=-1.0) == gsvk.E_ARG
+    assert call(eps=float("nan")) == gsvk.E_ARG
+    assert call(h=A + 32) == gsvk.E_ALIAS       # h over z (other workgroups still read z)
+    assert call(h=B + 64) == gsvk.E_ALIAS       # h over the weights
+    assert call(g=H + 8) == gsvk.E_ALIAS        # gamma inside h
+    assert call(y=H + 16) == gsvk.E_ALIAS       # y over h
+    assert call(y=A + 64) == gsvk.E_ALIAS       # y over z
+    # two-launch form (in % 8 != 0) takes one row stride for z and h
+    assert call(n_in=60, ldz=64, ldh=72) == gsvk.E_ARG
+
+
 def test_attention_validation(gsvk_lib):
     f = gsvk_lib.gsvk_decode_attention
 

@@ -198,3 +198,80 @@ def test_gemv_rejects_bad_arguments():
                             Y.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_SIZE
     assert L.gsvk_gemv_f16w(F16, 1, None, 64, W.data_ptr(), None, 0, 0.0, None, F32,
                             Y.data_ptr(), 32, 4, 32, 64, None) == gsvk.E_NULL
+
+
+# ---- LayerNorm folded into the GEMV (gsvk_gemv_f16w_ln) ------------------------------------------
+
+LN_CASES = [
+    # rows, out, in, x_dt, round_x, y_dt, act, residual, affine
+    (64, 2048, 512, F16, True, F16, gsvk.ACT_RELU, False, True),    # norm1 -> W1, fp16 storage
+    (64, 1536, 512, F16, True, F32, gsvk.ACT_NONE, False, True),    # norm2 -> next QKV
+    (64, 1025, 512, F16, True, F32, gsvk.ACT_NONE, False, True),    # norm2 -> logits
+    (64, 2048, 512, F32, True, F32, gsvk.ACT_RELU, False, True),    # fp32 storage, x rounded
+    (37, 96, 472, F32, False, F32, gsvk.ACT_NONE, True, False),     # split mode, ragged, k tail
+    (21, 80, 200, F16, True, F16, gsvk.ACT_NONE, False, True),      # 16-bit x, k tail
+    (5, 24, 120, F32, True, F16, gsvk.ACT_NONE, False, True),       # two waves, k tail
+    (8, 40, 264, F32, True, F32, gsvk.ACT_NONE, False, True),       # two launches (2 blocks/wave)
+    (19, 64, 1024, F16, True, F16, gsvk.ACT_GELU_ERF, True, True),  # the largest fused K
+    (130, 40, 512, F16, True, F32, gsvk.ACT_NONE, False, True),     # several row blocks
+    (16, 48, 2048, F16, True, F32, gsvk.ACT_NONE, False, True),     # two launches (K > 1024)
+    (8, 40, 520, F32, True, F32, gsvk.ACT_NONE, False, True),       # two launches (K > 512 fp32)
+    (8, 40, 100, F32, True, F32, gsvk.ACT_NONE, False, True),       # two launches (K % 8 != 0)
+]
+
+
+def ln_fused(rows, n_out, n_in):
+    """Whether gsvk_gemv_f16w_ln runs as one launch: K % 8 == 0 and a launch plan whose waves hold
+    all their k blocks (the GEMV's thresholds: 64-wide blocks over 1, 2, 4, 4 or 8 waves)."""
+    nkb = (n_in + 63) // 64
+    if n_in % 8 or (n_out + 15) // 16 * ((rows + 15) // 16) >= 16384:
+        return False
+    wk, d = (8, 2) if nkb >= 16 else (4, 2) if nkb >= 8 else (4, 1) if nkb >= 4 else \
+        (2, 1) if nkb >= 2 else (1, 1)
+    return -(-nkb // wk) <= d
+
+
+@pytest.mark.parametrize("rows,n_out,n_in,x_dt,round_x,y_dt,act,use_res,affine", LN_CASES)
+def test_gemv_ln_equals_layernorm_then_gemv(rows, n_out, n_in, x_dt, round_x, y_dt, act, use_res,
+                                            affine):
+    """The fused launch against the oracle: h within the LayerNorm tolerance (its statistics are
+    summed in another order than gsvk_add_layernorm's), y = the oracle GEMV of that h; two calls
+    give the same bits. Every storage / rounding mode, ragged rows, a partial k block, absent
+    gamma / beta, and shapes that take the two-launch form (then equal to the two launches)."""
+    say(f"gemv_ln rows={rows} out={n_out} in={n_in} x={x_dt} round={round_x} y={y_dt} act={act}")
+    r = rng(500 + rows + n_out + n_in)
+    z = O.to_storage(x_dt, (3.0 * r.standard_normal((rows, n_in)) + 0.5).astype(np.float32))
+    g = (1.0 + 0.1 * r.standard_normal(n_in)).astype(np.float32) if affine else None
+    b = (0.1 * r.standard_normal(n_in)).astype(np.float32) if affine else None
+    w = weights(r, n_out, n_in)
+    bias = (0.02 * r.standard_normal(n_out)).astype(np.float32)
+    res = O.to_storage(y_dt, r.standard_normal((rows, n_out)).astype(np.float32)) if use_res \
+        else None
+    Z, W = dev(z, x_dt), dev(w, F16)
+    G, Bt = (devf(g), devf(b)) if affine else (None, None)
+    Bi = devf(bias)
+    ytype = dev(np.zeros(1, O.storage_dtype(y_dt)), y_dt).dtype
+    H1, H2 = torch.full_like(Z, 7), torch.full_like(Z, 7)
+    Y1 = torch.empty((rows, n_out), dtype=ytype, device="cuda")
+    Y2 = torch.empty_like(Y1)
+    R = dev(res, y_dt) if use_res else None
+    gsvk.gemv_f16w_ln(Z, G, Bt, 1e-5, H1, W, Y1, bias=Bi, act=act, residual=R, round_x=round_x)
+    gsvk.gemv_f16w_ln(Z, G, Bt, 1e-5, H2, W, Y2, bias=Bi, act=act, residual=R, round_x=round_x)
+    torch.cuda.synchronize()
+    h1, h2 = host(H1, x_dt), host(H2, x_dt)
+    y1, y2 = host(Y1, y_dt), host(Y2, y_dt)
+    assert np.array_equal(h1, h2) and np.array_equal(y1, y2), "two calls differ"
+    if not ln_fused(rows, n_out, n_in):  # the two-launch form: the same bits
+        gsvk.add_layernorm(Z, G, Bt, H2, 1e-5)
+        gsvk.gemv_f16w(H2, W, Y2, bias=Bi, act=act, residual=R, round_x=round_x)
+        torch.cuda.synchronize()
+        assert np.array_equal(h1, host(H2, x_dt)) and np.array_equal(y1, host(Y2, y_dt))
+    # and against the oracle: h within the LayerNorm tolerance, y = the oracle GEMV of that h
+    ones, zeros = np.ones(n_in, np.float32), np.zeros(n_in, np.float32)
+    want_h = O.to_f32(x_dt, O.add_layernorm(x_dt, z, g if affine else ones,
+                                            b if affine else zeros, 1e-5)).astype(np.float64)
+    got_h = O.to_f32(x_dt, h1).astype(np.float64)
+    tol_h = 2e-3 if x_dt == F16 else 1e-6 + 1e-5 * np.abs(want_h)
+    assert np.all(np.abs(got_h - want_h) <= tol_h), "h vs oracle LayerNorm"
+    want = O.gemv_f16w(x_dt, h1, w, y_dt, bias=bias, act=act, residual=res, round_x=round_x)
+    assert_gemv_close(y_dt, y1, want, act, "gemv_ln vs oracle GEMV")

@@ -108,7 +108,9 @@ def test_decode_step_matches_oracle_chain(graph, len_bound):
     md, iod = to_device(m, io, FF)
     x_want, lg_want = oracle_step(m, io)
     step = gsvk.T2SDecode(md, iod, len_bound=len_bound, graph=graph)
-    assert not graph or step.launches >= 1 + 7 * 2 + 1
+    # gather, 2 layers x (QKV, attention (+ merge), out-proj, W1 with norm1, W2), logits with
+    # the last norm2 (each norm2 / norm1 runs inside the GEMV after it)
+    assert not graph or step.launches in (1 + 5 * 2 + 1, 1 + 6 * 2 + 1)
     step.run()
     torch.cuda.synchronize()
     assert int(iod["err"].item()) == 0
