@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
   // and the per-wave partials are added in wave order through LDS; mean = float(sum * (1/K)) in
   // double, then the centred second moment the same way, rstd = rsq(var + eps): ln_rows_tile's
   // formulas (csrc/gsvk_norm.hip) in another summation order.
-  __shared__ float ln_part[LN ? WK * 16 * MF : 1];
+  __shared__ float ln_part[LN ? 2 * WK * 16 * MF : 1];  // one area per pass: two barriers in all
   float lmean[MF][XQ], lrstd[MF][XQ];
   const bool store_h = LN && a.ln_y != nullptr && blockIdx.x == 0;
   auto row_sum = [&](float v) {  // over the XLPR consecutive lanes that hold one row
@@ -299,20 +299,20 @@ __global__ __launch_bounds__(kWave * WK) void gemv_mfma(GvArgs a) {
           }
         }
         p = row_sum(p);
-        if (lane % XLPR == 0) ln_part[wave * 16 * MF + 16 * i + (16 / XQ) * q + lane / XLPR] = p;
+        if (lane % XLPR == 0)
+          ln_part[(pass * WK + wave) * 16 * MF + 16 * i + (16 / XQ) * q + lane / XLPR] = p;
       }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < MF; ++i)
 #pragma unroll
       for (int q = 0; q < XQ; ++q) {
-        const int rr = 16 * i + (16 / XQ) * q + lane / XLPR;
+        const int rr = pass * WK * 16 * MF + 16 * i + (16 / XQ) * q + lane / XLPR;
         float t = ln_part[rr];
 #pragma unroll
         for (int w = 1; w < WK; ++w) t += ln_part[w * 16 * MF + rr];
         out[i][q] = static_cast<float>(static_cast<double>(t) * a.inv_n);
       }
-    __syncthreads();  // the partials area is reused by the next pass
   };
   auto ln_prologue = [&](const Raw<XM, MF, NF>(&f)[D]) {
     ln_pass(f, 0, lmean);
