@@ -27,9 +27,6 @@ constexpr int kAttnWaves = 4;
 #ifndef GSVK_ATTN_DEPTH
 #define GSVK_ATTN_DEPTH 2
 #endif
-#ifndef GSVK_ATTN_KEYS_PER_WG
-#define GSVK_ATTN_KEYS_PER_WG 128
-#endif
 constexpr int kKeysPerGroup = GSVK_ATTN_KPG;  // keys per wave per pipeline step
 constexpr int kDepth = GSVK_ATTN_DEPTH;        // groups of loads in flight per wave
 constexpr int kMaxChunks = 16;
@@ -298,12 +295,20 @@ __global__ __launch_bounds__(kWave * kMaxChunks) void attn_merge(AttnArgs a, int
   store8<OUTT>(a.out, static_cast<size_t>(b) * a.ldo + 8 * lane, y);
 }
 
+// Key chunks per sequence. The workgroups of a launch stream their keys in step, so the grid is
+// sized to whole rounds of about two workgroups per CU: with B = 64 on 256 CUs, 8 chunks. Measured
+// on the whole T2S decode step (B = 64, 1088 and 2112 keys): 8 chunks ran 7% faster than 9 (2.25
+// workgroups per CU: a quarter-full last round) and 2% faster than 16. Contexts up to 256 keys
+// take one chunk per 128 keys, and no chunk is shorter than 64 keys.
 int chunks_for(size_t batch, size_t len_bound) {
-  // about GSVK_ATTN_KEYS_PER_WG keys (128: 256 KB of an fp16 cache at D = 512) per workgroup, and
-  // at least 2 workgroups per CU when the batch alone gives fewer
-  long c = static_cast<long>((len_bound + GSVK_ATTN_KEYS_PER_WG - 1) / GSVK_ATTN_KEYS_PER_WG);
-  const long min_c = (512 + static_cast<long>(batch) - 1) / static_cast<long>(batch);
-  if (len_bound > 256) c = std::max(c, min_c);
+  const long lb = static_cast<long>(len_bound), B = static_cast<long>(batch);
+  long c;
+  if (lb <= 256) {
+    c = (lb + 127) / 128;
+  } else {
+    c = (2L * device_cus() + B - 1) / B;
+    c = std::min(c, (lb + 63) / 64);
+  }
   return static_cast<int>(std::max(1L, std::min<long>(c, kMaxChunks)));
 }
 

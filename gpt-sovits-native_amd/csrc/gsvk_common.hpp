@@ -295,4 +295,19 @@ inline bool allow_dynamic_lds(const void* fn, size_t bytes,
   return true;
 }
 
+// Compute units of the current device (cached per device; 256 on MI355X). A racing first call
+// stores the same value twice.
+inline int device_cus() {
+  static std::atomic<int> cus[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 }  // namespace gsvk

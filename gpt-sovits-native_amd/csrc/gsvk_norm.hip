@@ -489,21 +489,6 @@ int launch_ln(const LnArgs& a, bool vec_ok, hipStream_t st) {
   return launch_status();
 }
 
-// Compute units of the current device (cached per device; 256 on MI355X). A racing first call
-// stores the same value twice.
-int device_cus() {
-  static std::atomic<int> cus[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
-  int n = cus[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 // False (nothing launched) when the runtime refuses the LDS the tile needs.
 template <int DT, int CPT, bool NT>
 bool launch_gn_cpt(const GnArgs& a, hipStream_t st) {

@@ -169,7 +169,8 @@ int gsvk_gemv_f16w_ln(int x_dtype, int round_x, const void* z, size_t ldz, const
  * reference's k16[j * D + h * HD + e]); out [batch, ldo >= D] of out_dtype. D = heads * head_dim
  * <= 512, head_dim a multiple of 8 with head_dim / 8 a power of two; rows 16-byte aligned.
  * len_bound: a host-side upper bound of pos[b] + 1 (e.g. the longest sequence so far) that sets how
- * many key chunks a sequence is split into (0 = max_len); results do not depend on it. With more
+ * many key chunks a sequence is split into (0 = max_len); results agree within the tolerance below
+ * whatever its value (the partition of the keys, so the rounding, follows it). With more
  * than one chunk the partial states go through `workspace` (gsvk_decode_attention_workspace_bytes
  * bytes, 16-byte aligned; no initialisation needed); with a NULL or smaller workspace every sequence
  * runs as one chunk. A position outside [0, max_len) (undefined in the reference) writes a NaN row,
