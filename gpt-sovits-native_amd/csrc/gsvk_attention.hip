@@ -22,7 +22,7 @@ namespace {
 
 constexpr int kAttnWaves = 4;
 #ifndef GSVK_ATTN_KPG
-#define GSVK_ATTN_KPG 4
+#define GSVK_ATTN_KPG 2
 #endif
 #ifndef GSVK_ATTN_DEPTH
 #define GSVK_ATTN_DEPTH 2
