@@ -114,6 +114,19 @@ inline void gemv_fmlal_rows(const uint16_t* w, const float* x, float* y, size_t 
               "gsv::kern::gemv_fmlal_rows");
 }
 
+// The post-LN of block_decode_impl followed by the GEMV that reads its output, in one launch:
+// h = layernorm(z; g, b, eps) (kern.hpp:25) is stored and y = act(W16 h + bias) (+ residual)
+// (norm1 then W1, t2s_engine.cpp:1097-1112; norm2 then the next QKV, 1119 / 1044). z, h
+// [rows, in] (h must not overlap z), y / residual [rows, out].
+inline void layernorm_gemv_fmlal_rows(const float* z, const float* g, const float* b, double eps,
+                                      float* h, const uint16_t* w, float* y, size_t rows,
+                                      size_t out, size_t in, const float* bias = nullptr,
+                                      int act = GSVK_ACT_NONE, const float* residual = nullptr) {
+  gsvk::check(gsvk_gemv_f16w_ln(GSVK_F32, 1, z, in, g, b, eps, h, in, w, bias, act, 0.f, residual,
+                                GSVK_F32, y, out, rows, out, in, gsvk::current_stream()),
+              "gsv::kern::layernorm_gemv_fmlal_rows");
+}
+
 }  // namespace gsv::kern
 
 namespace gsv::bert {

@@ -370,6 +370,8 @@ void engine_like(float* x, const float* g, const float* b, float* ff, float* cur
                              GSVK_ACT_RELU);
   gsv::kern::gemv_fmlal_rows(reinterpret_cast<const uint16_t*>(g), x, ff, 64, 2048, 512, b,
                              GSVK_ACT_RELU, x);
+  gsv::kern::layernorm_gemv_fmlal_rows(x, g, b, 1e-5, cur, reinterpret_cast<const uint16_t*>(g), ff,
+                                       64, 2048, 512, b, GSVK_ACT_RELU);
   gsv::sovits::Conv1d c1;
   c1.load(reinterpret_cast<const uint16_t*>(g), b, 192, 192, 11, 5);
   c1.forward(cur, tin, 40000, GSVK_CONV_EPI_LRELU, 0.1f);
