@@ -543,6 +543,26 @@ void launch_tiles(const GvArgs& a, hipStream_t st) {
 }
 
 // LN (the LayerNorm prologue) is only launched tiled: the host checks the tile conditions first.
+// The tile plan for a shape: 16 MF rows x 16 NF columns per workgroup, K over WK waves with D
+// k blocks in flight each.
+struct Plan {
+  int mf, nf, wk, d;
+};
+// A long weight stream (many 16 x 16 tiles): 64-row tiles, so the weights are re-read from L2
+// once per 64 rows, and 32 or 64 columns. Decode shapes: 16 x 16 tiles (the most workgroups),
+// K over 4 or 8 waves with two k blocks each in flight (measured best on MI355X at B = 64 for
+// K = 512 and 2048).
+Plan plan_for(long M, long N, long K) {
+  const long nkb = (K + 63) / 64;
+  const long tiles = (N + 15) / 16 * ((M + 15) / 16);
+  if (tiles >= 16384) return nkb > 16 ? Plan{4, 4, 2, 2} : Plan{4, 2, 4, 2};
+  if (nkb >= 16) return {1, 1, 8, 2};
+  if (nkb >= 8) return {1, 1, 4, 2};
+  if (nkb >= 4) return {1, 1, 4, 1};
+  if (nkb >= 2) return {1, 1, 2, 1};
+  return {1, 1, 1, 1};
+}
+
 template <int XM, int YDT, bool LN>
 void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
   if (!tiled && !LN) {
@@ -551,35 +571,26 @@ void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
                        st, a);
     return;
   }
-  const long nkb = (a.K + 63) / 64;
-  const long tiles = (a.N + 15) / 16 * ((a.M + 15) / 16);
-  // A long weight stream (many 16 x 16 tiles): 64-row tiles, so the weights are re-read from L2
-  // once per 64 rows, and 32 or 64 columns. Decode shapes: 16 x 16 tiles (the most workgroups),
-  // K over 4 or 8 waves with two k blocks each in flight (measured best on MI355X at B = 64 for
-  // K = 512 and 2048).
-  if (tiles >= 16384) {
-    if (nkb > 16) return launch_tiles<XM, YDT, 4, 4, 2, 2, LN>(a, st);
+  const Plan p = plan_for(a.M, a.N, a.K);
+  if (p.mf == 4) {
+    if (p.nf == 4) return launch_tiles<XM, YDT, 4, 4, 2, 2, LN>(a, st);
     return launch_tiles<XM, YDT, 4, 2, 4, 2, LN>(a, st);
   }
-  if (nkb >= 16) return launch_tiles<XM, YDT, 1, 1, 8, 2, LN>(a, st);
-  if (nkb >= 8) return launch_tiles<XM, YDT, 1, 1, 4, 2, LN>(a, st);
-  if (nkb >= 4) return launch_tiles<XM, YDT, 1, 1, 4, 1, LN>(a, st);
-  if (nkb >= 2) return launch_tiles<XM, YDT, 1, 1, 2, 1, LN>(a, st);
-  launch_tiles<XM, YDT, 1, 1, 1, 1, LN>(a, st);
+  switch (p.wk * 10 + p.d) {
+    case 82: return launch_tiles<XM, YDT, 1, 1, 8, 2, LN>(a, st);
+    case 42: return launch_tiles<XM, YDT, 1, 1, 4, 2, LN>(a, st);
+    case 41: return launch_tiles<XM, YDT, 1, 1, 4, 1, LN>(a, st);
+    case 21: return launch_tiles<XM, YDT, 1, 1, 2, 1, LN>(a, st);
+    default: return launch_tiles<XM, YDT, 1, 1, 1, 1, LN>(a, st);
+  }
 }
 
-// Whether launch_plan's choice for this shape gives every wave at most D k blocks (all of them in
-// registers at once), which the LayerNorm prologue needs. Mirrors launch_plan's thresholds.
+// Whether the plan for this shape gives every wave at most D k blocks (all of them in registers
+// at once), which the LayerNorm prologue needs; decode plans (16-row tiles) only.
 bool ln_resident(long M, long N, long K) {
+  const Plan p = plan_for(M, N, K);
   const long nkb = (K + 63) / 64;
-  const long tiles = (N + 15) / 16 * ((M + 15) / 16);
-  if (tiles >= 16384) return false;
-  long wk = 1, d = 1;
-  if (nkb >= 16) wk = 8, d = 2;
-  else if (nkb >= 8) wk = 4, d = 2;
-  else if (nkb >= 4) wk = 4, d = 1;
-  else if (nkb >= 2) wk = 2, d = 1;
-  return (nkb + wk - 1) / wk <= d;
+  return p.mf == 1 && (nkb + p.wk - 1) / p.wk <= p.d;
 }
 
 template <int XM, bool LN = false>
