@@ -580,7 +580,20 @@ int launch_plan(const ConvArgs& a, hipStream_t st) {
     const long groups = (npos + 255) / 256 * ((a.cout + 32 * nw - 1) / (32 * nw)) * (a.up ? a.up : 1);
     if (nw == 2 && groups >= 384) return launch_tiles<XM, 2, 2, 64, 32>(a, st);
   }
-  if (halo <= 64) return launch_no<XM, 2, 64>(a, no, st);
+  if (halo <= 64) {
+    // A grid of fewer than 512 workgroups (two per CU) leaves matrix cores idle: the 384-channel
+    // stage, its upsampler and conv_pre launch 48-240. There, two 16-row fragments per wave
+    // instead of three or four give 1.5-2x the workgroups; measured on the whole decoder graph
+    // (alternating on one box): exact 3955-4035 -> 3767-3852 us, round_x 3090-3106 -> 2981-2987,
+    // fp16 storage 2946-2959 -> 2864. Smaller time tiles instead (32 columns per workgroup) or
+    // both were slower.
+    const long npos = a.up ? a.T + 1 : a.T;
+    const long groups =
+        (npos + 127) / 128 * ((a.cout + 16 * no - 1) / (16 * no)) * (a.up ? a.up : 1);
+    if (groups < 512 && no > 2 && (a.cout + 31) / 32 * 32 <= a.opad)
+      return launch_no<XM, 2, 64>(a, 2, st);
+    return launch_no<XM, 2, 64>(a, no, st);
+  }
   return launch_no<XM, 1, kMaxHalo>(a, no, st);
 }
 
