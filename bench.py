@@ -4,18 +4,21 @@
 Headline workload (one "step"): the epilogue chain of one T2S decode step for B = 64 sequences,
 d_model 512, FFN 2048, 24 layers, fp16 storage / fp32 arithmetic — the decode-input gather +
 alpha*PE, then per layer residual+LayerNorm (norm1), bias+ReLU on the FFN activations, residual+
-LayerNorm (norm2): 73 launches, replayed as one HIP graph per step. `value` is the algorithmic
-bytes of a step (every input read once, every output written once, parameters once) divided by
-the measured step time, with all inputs resident in HBM.
+LayerNorm (norm2). The step runs as ONE kernel launch (gsvk_t2s_step_fused: one wave per
+sequence walks the row-local LayerNorm chain, the other waves run the ReLU tiles), replayed as a
+one-node HIP graph per step; the 73 per-op launches of the same step (one graph) are timed beside
+it. `value` is the algorithmic bytes of a step (every input read once, every output written once,
+parameters once) divided by the measured step time, with all inputs resident in HBM.
 
 Also reported (same JSON line):
-  roofline      the dominant kernel of the step (residual+LayerNorm [64,512]) — bytes per launch
-                over its average launch duration from HIP events, against 8 TB/s;
+  roofline      the step's kernel (t2s_step_fused) — bytes per launch over its device time per
+                launch from HIP events, against 8 TB/s; traffic from two rocprofv3 --pmc runs;
   cpu_baseline  the oracle's C restatement of the same step on the host cores;
+  whole_decode_step  the whole decode step (GEMVs, attention, epilogues) summary next to it;
   kernels       every fused kernel of the configurations at its stated shape (device time per launch
                 in a graph of back-to-back launches, inputs cache-resident) and as a replicated
                 batch of independent instances (> 0.4 GB moved, the 256 MB MALL cleared between
-                repetitions by reading a 512 MiB buffer), in GB/s and fraction of 8 TB/s;
+                repetitions by reading a 512 MiB buffer), in GB/s, rows/s and fraction of 8 TB/s;
   copy_GBps     a plain device-to-device copy of 1 GiB measured the same way (achievable-bandwidth
                 reference for the replicated figures);
   sovits_decoder  the SoVITS ResBlock epilogues at every decoder stage shape (reference 768-channel
@@ -27,7 +30,7 @@ Also reported (same JSON line):
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
        python bench.py --only KERNEL   (one kernel of the suite, for rocprofv3 runs)
-       python bench.py --pmc           (dominant kernel + a 256 MiB copy, for rocprofv3 --pmc runs)
+       python bench.py --pmc           (the step kernel + a 256 MiB copy, for rocprofv3 --pmc runs)
        python bench.py --whole-step 1024   (the whole decode step alone, for rocprofv3 runs)
        python bench.py --conv          (SoVITS convolutions per stage, stages and whole decoder)
        python bench.py --decoder       (Generator stages and the whole decoder graph alone)
@@ -195,10 +198,11 @@ def kernel_suite(torch, gsvk, dev, only=None):
         t = torch.empty(*shape, dtype=f32, device=dev).normal_(mean, std, generator=g)
         return t.to(dtype)
 
-    def run(name, cfg, stated, replicated, bytes_fn, count, rep_bytes_fn=None):
+    def run(name, cfg, stated, replicated, bytes_fn, count, rep_bytes_fn=None, rows=None):
         """stated / replicated: (setup -> launch fn) builders taking a replication factor.
         rep_bytes_fn: HBM-unique bytes of the replicated launch when they differ from
-        bytes_fn (the gather re-reads shared tables from cache)."""
+        bytes_fn (the gather re-reads shared tables from cache). rows: k -> rows one launch of k
+        instances produces (sequences, tokens or channel rows), for rows/s."""
         if only and only != name:
             return
         rec = {"kernel": name, "config": cfg}
@@ -206,7 +210,11 @@ def kernel_suite(torch, gsvk, dev, only=None):
         us1 = graph_us_per_launch(torch, fn1)
         rec["stated_shape"] = {"us_per_launch": round(us1, 3), "bytes": bytes_fn(1),
                                "GBps": round(bytes_fn(1) / us1 / 1e3, 1),
+                               "frac_of_peak": round(bytes_fn(1) / us1 / 1e3 / PEAK_GBS, 4),
                                "calls_per_config": count}
+        if rows:
+            rec["stated_shape"]["rows"] = rows(1)
+            rec["stated_shape"]["rows_per_s"] = round(rows(1) / us1 * 1e6, 0)
         del fn1
         rep, fnr = replicated()
         msr = measure_reps(torch, fnr, flush)
@@ -214,6 +222,9 @@ def kernel_suite(torch, gsvk, dev, only=None):
         gbs = rb / msr / 1e6
         rec["replicated"] = {"instances": rep, "bytes": rb, "us": round(msr * 1e3, 2),
                              "GBps": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        if rows:
+            rec["replicated"]["rows"] = rows(rep)
+            rec["replicated"]["rows_per_s"] = round(rows(rep) / msr * 1e3, 0)
         del fnr
         torch.cuda.empty_cache()
         out.append(rec)
@@ -240,7 +251,8 @@ def kernel_suite(torch, gsvk, dev, only=None):
         return (lambda: make(1), lambda: (rep, make(rep)), lambda k: bias_act_bytes(rows * k, n, 2))
 
     # config 1: residual + LayerNorm fp32 [256, 512]
-    run("residual_layernorm_f32_256x512", 1, *ln_case(256, 512, f32, 1e-5, False, True, 1024), 1)
+    run("residual_layernorm_f32_256x512", 1, *ln_case(256, 512, f32, 1e-5, False, True, 1024), 1,
+        rows=lambda k: 256 * k)
     # config 2: gather + PE prefill/decode, LN [64,512], bias+ReLU [64,2048]
     pe = torch.from_numpy(gsvk.pe_table(MAX_POS, D)).to(dev)
 
@@ -256,9 +268,36 @@ def kernel_suite(torch, gsvk, dev, only=None):
 
     def run_emb(name, rows, rep):
         st_, rp_, b_, ub_ = emb_case(rows, rep)
-        run(name, 2, st_, rp_, b_, 1, rep_bytes_fn=ub_)
+        run(name, 2, st_, rp_, b_, 1, rep_bytes_fn=ub_, rows=lambda k: rows * k)
 
     run_emb("embed_pe_prefill_1024x512", 1024, 512)
+
+    def prefill_case(rep):
+        """The stated prefill pattern: 512 phone ids from the [732, 512] table and 512 semantic ids
+        from the [1025, 512] table, both at positions 0..511 (pe_row(t) in row order,
+        t2s_engine.cpp:1778, 1784): one launch per table, positions implicit (pos0 = 0). The
+        replicated batch is `rep` such prompts, explicit positions t mod 512 per row; its HBM
+        floor counts ids, positions and output rows per row and the tables and the 512 PE rows
+        once."""
+        def make(k):
+            tp, ts = rn(732, D, std=0.02), rn(VOCAB, D, std=0.02)
+            ip = torch.randint(0, 732, (512 * k,), device=dev, generator=g)
+            isem = torch.randint(0, VOCAB, (512 * k,), device=dev, generator=g)
+            op = torch.empty(512 * k, D, dtype=f16, device=dev)
+            osem = torch.empty(512 * k, D, dtype=f16, device=dev)
+            if k == 1:
+                return lambda: (gsvk.embed_pe(tp, ip, pe, 0.93, op, pos0=0),
+                                gsvk.embed_pe(ts, isem, pe, 1.07, osem, pos0=0))
+            pos = torch.arange(512 * k, device=dev, dtype=torch.int64) % 512
+            return lambda: (gsvk.embed_pe(tp, ip, pe, 0.93, op, pos=pos),
+                            gsvk.embed_pe(ts, isem, pe, 1.07, osem, pos=pos))
+        per = lambda k: 1024 * k * (8 + 2 * D + 4 * D + 2 * D)
+        floor = lambda k: 1024 * k * (16 + 2 * D) + (732 + VOCAB) * D * 2 + 512 * D * 4
+        return (lambda: make(1), lambda: (rep, make(rep)), per, floor)
+
+    st_, rp_, b_, ub_ = prefill_case(512)
+    run("embed_pe_prefill_pos0_511_2x512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_,
+        rows=lambda k: 1024 * k)
     run_emb("embed_pe_decode_64x512", 64, 8192)
 
     def text_case(rows, rep):
@@ -282,13 +321,16 @@ def kernel_suite(torch, gsvk, dev, only=None):
         return (lambda: make(1), lambda: (rep, make(rep)), per_row, floor)
 
     st_, rp_, b_, ub_ = text_case(512, 1024)
-    run("embed_pe_text_rows_512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_)
-    run("residual_layernorm_f16_64x512", 2, *ln_case(64, 512, f16, 1e-5, True, True, 8192), 48)
-    run("bias_relu_f16_64x2048", 2, *ba_case(64, 2048, gsvk.ACT_RELU, 4096), 24)
+    run("embed_pe_text_rows_512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_, rows=lambda k: 512 * k)
+    run("residual_layernorm_f16_64x512", 2, *ln_case(64, 512, f16, 1e-5, True, True, 8192), 48,
+        rows=lambda k: 64 * k)
+    run("bias_relu_f16_64x2048", 2, *ba_case(64, 2048, gsvk.ACT_RELU, 4096), 24,
+        rows=lambda k: 64 * k)
     # config 3: bias + GELU [512, 4096], residual + LN(1024, eps 1e-12)
-    run("bias_gelu_f16_512x4096", 3, *ba_case(512, 4096, gsvk.ACT_GELU_ERF, 128), 1)
+    run("bias_gelu_f16_512x4096", 3, *ba_case(512, 4096, gsvk.ACT_GELU_ERF, 128), 1,
+        rows=lambda k: 512 * k)
     run("residual_layernorm_f16_512x1024_eps1e-12", 3,
-        *ln_case(512, 1024, f16, 1e-12, False, True, 512), 24)
+        *ln_case(512, 1024, f16, 1e-12, False, True, 512), 24, rows=lambda k: 512 * k)
     # config 4: GroupNorm + GELU [512, 31999] fp32, LN(768), bias + GELU [499, 3072]
 
     def gn_case(rep):
@@ -299,9 +341,11 @@ def kernel_suite(torch, gsvk, dev, only=None):
             return lambda: gsvk.groupnorm_gelu(x, gm, bt, y, 1e-5)
         return (lambda: make(1), lambda: (rep, make(rep)), lambda k: gn_bytes(512 * k, 31999, 4))
 
-    run("groupnorm_gelu_f32_512x31999", 4, *gn_case(8), 1)
-    run("residual_layernorm_f16_499x768", 4, *ln_case(499, 768, f16, 1e-5, True, True, 512), 24)
-    run("bias_gelu_f16_499x3072", 4, *ba_case(499, 3072, gsvk.ACT_GELU_ERF, 192), 12)
+    run("groupnorm_gelu_f32_512x31999", 4, *gn_case(8), 1, rows=lambda k: 512 * k)
+    run("residual_layernorm_f16_499x768", 4, *ln_case(499, 768, f16, 1e-5, True, True, 512), 24,
+        rows=lambda k: 499 * k)
+    run("bias_gelu_f16_499x3072", 4, *ba_case(499, 3072, gsvk.ACT_GELU_ERF, 192), 12,
+        rows=lambda k: 499 * k)
 
     # config 5: SoVITS ResBlock epilogues at the largest stage [24, 320000]
     def sv_case(kind, dt, rep):
@@ -325,7 +369,8 @@ def kernel_suite(torch, gsvk, dev, only=None):
 
     for kind, count in (("K3", 1), ("K2", 6), ("K1", 9)):
         for dt, nm, rep in ((f32, "f32", 8), (f16, "f16", 16)):
-            run(f"sovits_{kind}_{nm}_24x320000", 5, *sv_case(kind, dt, rep), count)
+            run(f"sovits_{kind}_{nm}_24x320000", 5, *sv_case(kind, dt, rep), count,
+                rows=lambda k: 24 * k)
 
     # T2S decode GEMVs with their fused epilogues, B = 64 rows (t2s_engine.cpp:1044-1116): the
     # stated shape cycles through 24 distinct weight matrices (one per layer, as a decode step
@@ -361,7 +406,8 @@ def kernel_suite(torch, gsvk, dev, only=None):
             ("w1_bias_relu", 2048, 512, gsvk.ACT_RELU, True, False, f16, 64, 24),
             ("w2_bias_residual", 512, 2048, gsvk.ACT_NONE, True, True, f16, 128, 24),
             ("logits_f32out", 1025, 512, gsvk.ACT_NONE, False, False, f32, 128, 1)):
-        run(f"gemv_{name}_64x{N}x{K}", 2, *gemv_case(N, K, act, ub, ur, ydt, rep), count)
+        run(f"gemv_{name}_64x{N}x{K}", 2, *gemv_case(N, K, act, ub, ur, ydt, rep), count,
+            rows=lambda k: B)
 
     # T2S decode attention with the KV append (t2s_engine.cpp:1051-1087): B = 64 sequences, 16 heads
     # of 32, fp16 caches, every sequence at position L - 1. One call already streams 2 B L D cache
@@ -377,7 +423,7 @@ def kernel_suite(torch, gsvk, dev, only=None):
         nbytes = lambda k: 2 * B * Ln * k * D * 2 + B * 3 * D * 4 + B * D * 2
         return (lambda: make(1), lambda: (rep, make(rep)), nbytes)
 
-    run("decode_attention_f16kv_64x1024x512", 2, *attn_case(1024, 2), 24)
+    run("decode_attention_f16kv_64x1024x512", 2, *attn_case(1024, 2), 24, rows=lambda k: B)
     return out
 
 
@@ -659,6 +705,26 @@ def cpu_model():
     return "unknown"
 
 
+def cpu_topology():
+    """Logical CPUs this process may run on, and the physical cores behind them (from
+    /proc/cpuinfo: distinct (physical id, core id) pairs), so `cores` can be read either way."""
+    logical = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    pairs, phys, core = set(), None, None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("physical id"):
+                phys = line.split(":", 1)[1].strip()
+            elif line.startswith("core id"):
+                core = line.split(":", 1)[1].strip()
+            elif not line.strip() and core is not None:
+                pairs.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    return {"logical_cpus_allowed": logical, "hardware_threads": os.cpu_count(),
+            "physical_cores_on_host": len(pairs) or None}
+
+
 def cpu_baseline(torch, bufs, rep_s=0.3, reps=9):
     """The oracle's restatement of the same decode step on host copies of the same buffers, with
     the reference's bench convention (src/kern/bench_harness.hpp:8-13): 2 warm-up steps, then the
@@ -789,26 +855,32 @@ def copy_bandwidth(torch, dev, nbytes=1 << 30):
 
 
 PMC_COPY_BYTES = 256 << 20
-PMC_LAUNCHES = 100
+PMC_LAUNCHES = 30
+PMC_KERNEL = "t2s_step_fused"
 
 
 def pmc_workload(torch, gsvk, bufs):
     """For `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`: PMC_LAUNCHES launches of the step's
-    dominant kernel (residual+LN [64,512] f16, bias + residual) and 10 plain copies of
-    PMC_COPY_BYTES (the calibration: its counters per dispatch against its known bytes)."""
-    L0, _, _ = step_ops(gsvk, bufs)
+    kernel (t2s_step_fused, the whole decode-step epilogue chain), each after a 512 MiB read that
+    clears the MALL (so the step's inputs come from HBM, as in a decode loop where the GEMVs
+    stream 150 MB of weights between steps), and 10 plain copies of PMC_COPY_BYTES (the
+    calibration: its counters per dispatch against its known bytes)."""
+    step = gsvk.T2SStep(bufs, eps=1e-5, graph=False, fused=True)
+    flush = Flusher(torch, bufs["x"].device)
     for _ in range(PMC_LAUNCHES):
-        L0()
+        flush()
+        step.run()
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=bufs["x"].device)
     dst = torch.empty_like(src)
     for _ in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"pmc workload: {PMC_LAUNCHES} x residual+LN [64,512] f16, 10 x copy {PMC_COPY_BYTES} B")
+    log(f"pmc workload: {PMC_LAUNCHES} x {PMC_KERNEL} (MALL cleared before each), "
+        f"10 x copy {PMC_COPY_BYTES} B")
 
 
 def measure_traffic(timeout_s=150):
-    """HBM-side traffic of one launch of the dominant kernel: two `rocprofv3 --pmc` child runs of
+    """HBM-side traffic of one launch of the step's kernel: two `rocprofv3 --pmc` child runs of
     this script's --pmc workload (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what
     the same counter reads for the PMC_COPY_BYTES copy in that workload. Returns (dict, None) or
     (None, reason)."""
@@ -837,7 +909,7 @@ def measure_traffic(timeout_s=150):
                 if r["Counter_Name"] != ctr:
                     continue
                 v = float(r["Counter_Value"])
-                if "ln_rows_tile" in r["Kernel_Name"]:
+                if PMC_KERNEL in r["Kernel_Name"]:
                     ln.append(v)
                 elif "copyBuffer" in r["Kernel_Name"] or "copy" in r["Kernel_Name"].lower():
                     cp.append(v)
@@ -863,7 +935,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run one kernel of the suite and exit")
     ap.add_argument("--pmc", action="store_true",
-                    help="run the dominant kernel and a plain copy only (for rocprofv3 --pmc)")
+                    help="run the step kernel and a plain copy only (for rocprofv3 --pmc)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
     ap.add_argument("--conv", action="store_true",
@@ -906,21 +978,36 @@ def main():
     if a.pmc:
         pmc_workload(torch, gsvk, bufs)
         return
-    step = gsvk.T2SStep(bufs, eps=1e-5, graph=True)
     nbytes = step_bytes()
-    for _ in range(a.warmup):
-        step.run()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(a.steps):
-        step.run()
-    e.record()
-    e.synchronize()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / a.steps
+
+    def time_step(st):
+        for _ in range(a.warmup):
+            st.run()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(a.steps):
+            st.run()
+        e.record()
+        e.synchronize()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / a.steps
+
+    # The step as one launch (gsvk_t2s_step_fused), launched directly per step: the headline.
+    # The same launch recorded as a one-node graph is timed beside it.
+    step = gsvk.T2SStep(bufs, eps=1e-5, graph=False, fused=True)
+    ms = time_step(step)
     assert int(bufs["err"].item()) == 0
-    log(f"decode step (graph, {step.launches} launches): {ms * 1e3:.2f} us")
+    log(f"decode step (one fused launch): {ms * 1e3:.2f} us")
+    step_g = gsvk.T2SStep(bufs, eps=1e-5, graph=True, fused=True)
+    ms_g = time_step(step_g)
+    step_g.close()
+    log(f"decode step (one fused launch as a one-node graph): {ms_g * 1e3:.2f} us")
+    # The same step as the 73 per-op launches (one graph), for comparison.
+    step73 = gsvk.T2SStep(bufs, eps=1e-5, graph=True)
+    ms73 = time_step(step73)
+    log(f"decode step (graph, {step73.launches} launches): {ms73 * 1e3:.2f} us")
+    step73.close()
 
     # per-op breakdown at the step's shapes: graphs of 48 back-to-back launches of each op
     L0, R0, E0 = step_ops(gsvk, bufs)
@@ -931,15 +1018,20 @@ def main():
         gr = graph_of(torch, fn, 48)
         us = time_loop(torch, gr.replay, 20) * 1e3 / 48
         per_op[name] = {"us_per_launch": round(us, 3), "launches_per_step": cnt, "bytes": byt,
-                        "GBps": round(byt / us / 1e3, 1)}
+                        "GBps": round(byt / us / 1e3, 1),
+                        "rows_per_s": round(B / us * 1e6, 0)}
         del gr
-    dom = max(per_op, key=lambda k: per_op[k]["us_per_launch"] * per_op[k]["launches_per_step"])
-    d = per_op[dom]
-    ach = d["bytes"] / d["us_per_launch"] / 1e3
-    roofline = {"kernel": f"{dom} [{B},{D if dom != 'bias_relu' else FF}] f16",
+
+    # Roofline of the step's one kernel (t2s_step_fused): the step's algorithmic bytes over its
+    # device time per launch, HIP events around a graph of 32 back-to-back launches on the launch
+    # stream.
+    us_fused = graph_us_per_launch(torch, step.run, launches=32, replays=20)
+    ach = nbytes / us_fused / 1e3
+    roofline = {"kernel": f"t2s_step_fused [B={B}, D={D}, FF={FF}, {LAYERS} layers] f16",
                 "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_GBS, 5), "traffic": None,
-                "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_launch"]}
+                "bytes_per_launch": nbytes, "us_per_launch": round(us_fused, 3),
+                "rows_per_s": round(B * (1 + 3 * LAYERS) / us_fused * 1e6, 0)}
 
     if not a.no_traffic:
         tr, why = measure_traffic()
@@ -961,9 +1053,10 @@ def main():
                          f"{LAYERS} layers, fp16 storage) of the oracle's C restatement, rows split "
                          f"over {tall} threads; 2 warm-up steps",
                "us_per_step": round(best["s_per_step"] * 1e6, 1), "cv": round(best["cv"], 4),
+               "rows_per_s": round(B * (1 + 3 * LAYERS) / best["s_per_step"], 0),
                "single_thread_us_per_step": round(res[1]["s_per_step"] * 1e6, 1),
                "single_thread_cv": round(res[1]["cv"], 4),
-               "cpu_model": cpu_model(), "hardware_threads": os.cpu_count()}
+               "cpu_model": cpu_model(), **cpu_topology(), "threads_used": tall}
 
     kernels = copy_gbs = decoder = full = conv = None
     if not a.no_kernels:
@@ -983,6 +1076,11 @@ def main():
             log(f"  CPU (oracle, 1 thread): decode step {nt['t2s_whole_decode_step']['us_per_step']:.0f}"
                 f" us, conv 192x40000 k11 {nt['sovits_conv_192x40000_k11_d5']['us']:.0f} us")
 
+    whole = None
+    if full:
+        whole = {f"kv{r['kv_len']}": {"us_per_step": r["us_per_step"],
+                                      "tokens_per_s": r["tokens_per_s"],
+                                      "frac_of_peak": r["frac_of_peak"]} for r in full}
     line = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 5),
@@ -990,10 +1088,16 @@ def main():
         "data": "synthetic (seeded normal activations / parameters, uniform ids and positions)",
         "config": {"workload": "t2s_decode_step_epilogues", "batch": B, "d_model": D, "ffn": FF,
                    "layers": LAYERS, "storage": "f16", "launches_per_step": step.launches,
-                   "bytes_per_step": nbytes, "us_per_step": round(ms * 1e3, 3),
-                   "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_GBS, 5), "graph": True},
+                   "fused": True, "bytes_per_step": nbytes, "us_per_step": round(ms * 1e3, 3),
+                   "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_GBS, 5),
+                   "rows_per_s": round(B * (1 + 3 * LAYERS) / ms * 1e3, 0),
+                   "tokens_per_s": round(B / ms * 1e3, 0), "graph": False,
+                   "one_node_graph_us_per_step": round(ms_g * 1e3, 3),
+                   "per_op_graph_us_per_step": round(ms73 * 1e3, 3),
+                   "per_op_graph_launches": 1 + 3 * LAYERS},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "whole_decode_step": whole,
         "per_op": per_op,
         "copy_GBps": copy_gbs,
         "kernels": kernels,

@@ -181,6 +181,13 @@ __global__ __launch_bounds__(kWave * kAttnWaves) void attn_chunk(AttnArgs a) {
           vr[u][i] = vn[i];
         }
       }
+      // A padded slot (k >= k1) re-read row k1 - 1, which in the chunk holding pos is the row
+      // the append is writing: possibly stale bits, Inf or NaN. Its score is -inf (p = 0), and
+      // its values are zeroed too, since 0 * Inf / NaN would poison o.
+      if (k >= k1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vr[u][i] = 0.f;
+      }
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[i], kr[i], d);
@@ -342,15 +349,20 @@ extern "C" size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t hea
   (void)heads;
   (void)head_dim;
   if (batch == 0) return 0;
-  return part_bytes(batch, chunks_for(batch, len_bound));
+  // len_bound 0 (the launch then uses max_len, which this query does not see): size for the
+  // longest context, an upper bound of what any max_len needs.
+  return part_bytes(batch, chunks_for(batch, len_bound ? len_bound : (1ul << 31)));
 }
 
-extern "C" int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* qkv, size_t ldq,
-                                     void* k_cache, void* v_cache, size_t max_len,
-                                     const int64_t* pos, void* out, size_t ldo, size_t batch,
-                                     size_t heads, size_t head_dim, size_t len_bound,
-                                     void* workspace, size_t workspace_bytes, int32_t* err,
-                                     void* stream) {
+namespace gsvk {
+
+// The whole call after the workspace decision. need_ws: the caller's workspace must hold the
+// chunk states (the no-allocation form); otherwise a missing or short workspace means one chunk.
+__attribute__((visibility("hidden"))) int attention_call(
+                   int kv_dtype, int out_dtype, const float* qkv, size_t ldq, void* k_cache,
+                   void* v_cache, size_t max_len, const int64_t* pos, void* out, size_t ldo,
+                   size_t batch, size_t heads, size_t head_dim, size_t len_bound, void* workspace,
+                   size_t workspace_bytes, bool need_ws, int32_t* err, void* stream) {
   if (!valid_dtype(kv_dtype) || !valid_dtype(out_dtype)) return GSVK_E_DTYPE;
   if (!qkv || !k_cache || !v_cache || !pos || !out) return GSVK_E_NULL;
   const size_t D = heads * head_dim;
@@ -373,6 +385,7 @@ extern "C" int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* q
     return GSVK_E_ARG;
 
   int C = chunks_for(batch, len_bound ? len_bound : max_len);
+  if (need_ws && part_bytes(batch, C) > workspace_bytes) return GSVK_E_SIZE;
   if (C > 1 && (!workspace || workspace_bytes < part_bytes(batch, C) || !aligned16(workspace)))
     C = 1;  // without the workspace every sequence runs as one chunk
   if (C > 1 && (overlaps(workspace, part_bytes(batch, C), out, obytes) ||
@@ -391,3 +404,17 @@ extern "C" int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* q
   }
   return launch_status();
 }
+
+}  // namespace gsvk
+
+extern "C" int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* qkv, size_t ldq,
+                                     void* k_cache, void* v_cache, size_t max_len,
+                                     const int64_t* pos, void* out, size_t ldo, size_t batch,
+                                     size_t heads, size_t head_dim, size_t len_bound,
+                                     void* workspace, size_t workspace_bytes, int32_t* err,
+                                     void* stream) {
+  return attention_call(kv_dtype, out_dtype, qkv, ldq, k_cache, v_cache, max_len, pos, out, ldo,
+                        batch, heads, head_dim, len_bound, workspace, workspace_bytes, false, err,
+                        stream);
+}
+

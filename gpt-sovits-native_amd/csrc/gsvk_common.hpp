@@ -211,13 +211,23 @@ constexpr size_t kStreamBytes = size_t(256) << 20;
 
 // ---- wave64 reductions -------------------------------------------------------------------------
 // Inside each 16-lane DPP row: quad_perm xor-1, quad_perm xor-2, row_half_mirror, row_mirror give
-// every lane its row's sum; ds_swizzle (xor 16) folds rows pairwise inside each 32-lane half and
-// two readlanes fold the halves. The result is wave-uniform and bitwise identical on every lane.
+// every lane its row's sum r_k (bitwise the same on all 16 lanes: each step adds a pair in either
+// order). Then row_bcast:15 adds row k's lane 15 into row k + 1 (rows 1 and 3 only) and
+// row_bcast:31 adds lane 31 into rows 2 and 3, so lane 63 holds (r3 + r2) + (r1 + r0), read once
+// with v_readlane. The result is wave-uniform; the two broadcasts replace an LDS swizzle and a
+// second readlane on the critical path of every row reduction (the sum is the same bits as
+// (r0 + r1) + (r2 + r3): fp32 addition is commutative).
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// DPP move restricted to ROW_MASK rows; the other rows get 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_rows_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xf, false));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -225,10 +235,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f32<0x141>(v);  // row_half_mirror
   v += dpp_f32<0x140>(v);  // row_mirror
-  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-  const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-  return lo + hi;
+  v += dpp_rows_f32<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_rows_f32<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ double wave_sum(double v) {

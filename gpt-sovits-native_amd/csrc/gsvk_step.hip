@@ -1,0 +1,432 @@
+// gsvk_step.hip — the epilogue chain of one T2S decode step as ONE launch (gfx950).
+//
+// The chain (include/gsvk_t2s.h; block_decode_impl, t2s_engine.cpp:1096-1119, and the decode input,
+// 1866-1869) for B sequences is:
+//   x = audio_emb[id] + alpha * pe[pos]
+//   per layer l:  h = LN1((attn_out[l] + bout) + x);  ff[l] = relu(ff[l] + b1);
+//                 x = LN2((ffn_out[l] + b2) + h)
+// Every dependency of the LayerNorm chain stays inside one row: row b of layer l + 1 needs only row b
+// of layer l. So wave b walks the whole chain of sequence b with its row in VGPRs (the gather, then
+// 2 x layers LayerNorms), storing every h and x exactly as the per-op launches do, while the other
+// waves of the same launch stream the ReLU tiles of all layers (they depend on nothing in the chain).
+// No wave waits for another and there is no barrier: the 1 + 3 x layers launches of the graph form
+// become one dispatch, and its duration is the chain's critical path (2 x layers dependent row
+// reductions) instead of 73 launch latencies.
+//
+// The chain wave prefetches the next layers' inputs (attn_out / ffn_out rows and the six parameter
+// vectors) two layers ahead into a register ring, so HBM latency is paid once, not per LayerNorm.
+// Its row reductions are DPP only (gsvk_common.hpp wave_sum): no LDS round trip per LayerNorm.
+//
+// Numerics: the same operations in the same order as ln_rows_tile (gsvk_norm.hip), bias_act_tile
+// (gsvk_epilogue.hip) and embed_pe_vec (gsvk_embed.hip) with the same lane partition, and each
+// stored h / x is re-read as its rounded storage value (unpack of the packed store), so the fused
+// step is bitwise identical to the per-op launches.
+#include <cmath>
+
+#include "gsvk_common.hpp"
+#include "gsvk_t2s.h"
+
+namespace gsvk {
+namespace {
+
+constexpr int kMaxStepLayers = 32;  // the layer records travel in the kernel arguments
+constexpr int kReluRows = 4;        // rows per ReLU wave (the bias chunk is reused across them)
+
+struct StepLayer {
+  const void* attn_out;
+  const float* bout;
+  const float* n1g;
+  const float* n1b;
+  void* ff;
+  const float* b1;
+  const void* ffn_out;
+  const float* b2;
+  const float* n2g;
+  const float* n2b;
+};
+
+struct StepArgs {
+  const void* table;
+  const void* ids;
+  const int64_t* pos;
+  const float* pe;
+  int32_t* err;
+  void* x;
+  void* h;
+  long vocab, max_pos, B, D, FF;
+  long relu_waves_per_layer;  // ceil(B / kReluRows) * ceil(FF chunks / 64)
+  int relu_col_tiles;         // ceil(FF chunks / 64)
+  double inv_n;               // 1 / D, computed on the host
+  float eps;
+  float alpha;
+  int ids32;
+  int tab_dt;
+  int layers;
+  StepLayer L[kMaxStepLayers];
+};
+
+// V consecutive elements of a row of storage type T at element index i, as fp32 (the table may have
+// another storage type than the activations, so 8, 16 or 32 bytes).
+template <int T, int V>
+__device__ __forceinline__ void load_elems(const void* p, size_t i, float (&v)[V]) {
+  if constexpr (T == GSVK_F32) {
+#pragma unroll
+    for (int k = 0; k < V; k += 4) {
+      float q[4];
+      Store<GSVK_F32>::load(p, i + k, q);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[k + j] = q[j];
+    }
+  } else if constexpr (V == 8) {
+    Store<T>::load(p, i, v);
+  } else {  // four 16-bit values: one 8-byte load
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = Store<T>::up(w.x & 0xffffu);
+    v[1] = Store<T>::up(w.x >> 16);
+    v[2] = Store<T>::up(w.y & 0xffffu);
+    v[3] = Store<T>::up(w.y >> 16);
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void load_param(const float* p, size_t i, const float* fill,
+                                           float (&v)[V]) {
+  const float* q = param_or(p, i, fill);
+#pragma unroll
+  for (int k = 0; k < V; k += 4) load_f32x4(q, k, &v[k]);
+}
+
+// One layer's inputs for this lane's CPL chunks, in flight until the layer runs.
+template <int DT, int CPL>
+struct LayerIn {
+  static constexpr int V = Store<DT>::VEC;
+  u32x4 att[CPL], ffo[CPL];
+  float bo[CPL][V], g1[CPL][V], be1[CPL][V], b2[CPL][V], g2[CPL][V], be2[CPL][V];
+};
+
+template <int DT, int CPL>
+__device__ __forceinline__ void load_layer(const StepArgs& a, const StepLayer& L, size_t row_off,
+                                           const int (&idx)[CPL], LayerIn<DT, CPL>& f) {
+  constexpr int V = Store<DT>::VEC;
+  constexpr size_t kEsz = DT == GSVK_F32 ? 4 : 2;
+  (void)a;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const size_t e = row_off + static_cast<size_t>(idx[c]) * V;
+    f.att[c] = ld16<false>(static_cast<const char*>(L.attn_out) + e * kEsz);
+    f.ffo[c] = ld16<false>(static_cast<const char*>(L.ffn_out) + e * kEsz);
+  }
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const size_t i = static_cast<size_t>(idx[c]) * V;
+    load_param(L.bout, i, kZeros8, f.bo[c]);
+    load_param(L.n1g, i, kOnes8, f.g1[c]);
+    load_param(L.n1b, i, kZeros8, f.be1[c]);
+    load_param(L.b2, i, kZeros8, f.b2[c]);
+    load_param(L.n2g, i, kOnes8, f.g2[c]);
+    load_param(L.n2b, i, kZeros8, f.be2[c]);
+  }
+}
+
+// y = LN((in + bias) + res) over one row held by the wave, the operation order of ln_rows_tile:
+// per-lane sum in (chunk, element) order, wave_sum, mean = float(double(sum) / n), centred second
+// moment by fmaf, rstd = rsq(var + eps), y = fmaf((v - mean) rstd, g, b). Stores y and returns its
+// rounded storage value in `yr` (what the next LayerNorm reads back as its residual).
+template <int DT, int CPL, bool FULL>
+__device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL],
+                                       const float (&bias)[CPL][Store<DT>::VEC],
+                                       const float (&res)[CPL][Store<DT>::VEC],
+                                       const float (&g)[CPL][Store<DT>::VEC],
+                                       const float (&b)[CPL][Store<DT>::VEC],
+                                       const bool (&on)[CPL], void* y, size_t row_off,
+                                       const int (&idx)[CPL], float (&yr)[CPL][Store<DT>::VEC]) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  float v[CPL][V];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    if (FULL || on[c]) {
+      S::unpack(in[c], v[c]);
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + bias[c][k];
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + res[c][k];
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += v[c][k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[c][k] = 0.f;
+    }
+  }
+  const float sum = wave_sum(s);
+  const float mean = static_cast<float>(static_cast<double>(sum) * a.inv_n);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    if (FULL || on[c]) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const float d = v[c][k] - mean;
+        q = __builtin_fmaf(d, d, q);
+      }
+    }
+  }
+  const float sq = wave_sum(q);
+  const float var = static_cast<float>(static_cast<double>(sq) * a.inv_n);
+  const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    float o[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) o[k] = __builtin_fmaf((v[c][k] - mean) * rstd, g[c][k], b[c][k]);
+    const u32x4 packed = S::pack(o);
+    if (FULL || on[c])
+      st16<false>(static_cast<char*>(y) + (row_off + static_cast<size_t>(idx[c]) * V) *
+                                              (DT == GSVK_F32 ? 4 : 2),
+                  packed);
+    S::unpack(packed, yr[c]);
+  }
+}
+
+// The chain of sequence b: gather + alpha*PE, then LN1 / LN2 of every layer. FULL: every lane
+// holds CPL whole chunks (D = 64 * CPL * VEC), so no store needs a guard.
+//
+// The layer loop runs in pairs with no condition inside: layer l sits in ring slot l % 2 and the
+// slot is refilled with layer l + 2 (clamped to the last layer: an in-bounds reread whose values
+// are never used) right after it runs. With no branch between the loads and their uses, the
+// compiler's wait before each layer covers only that layer's loads (the other slot's loads stay in
+// flight); an odd last layer runs after the loop from slot 0.
+template <int DT, int CPL, bool FULL>
+__device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  const int lane = threadIdx.x;
+  const int nch = static_cast<int>(a.D / V);
+  int idx[CPL];
+  bool on[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int i = lane + c * kWave;
+    on[c] = FULL || i < nch;
+    idx[c] = on[c] ? i : nch - 1;  // clamped: loads stay unconditional, stores are guarded
+  }
+  const size_t row_off = static_cast<size_t>(b) * static_cast<size_t>(a.D);
+
+  // Decode input (embed_pe_vec's arithmetic): x = fmaf(alpha, pe[pos], e[id]). Both index words are
+  // read unconditionally (int32 ids read word b twice) so no branch separates the loads.
+  const uint32_t* idw = static_cast<const uint32_t*>(a.ids);
+  const size_t w0 = a.ids32 ? static_cast<size_t>(b) : 2 * static_cast<size_t>(b);
+  const uint32_t id_lo = idw[w0], id_hi = idw[a.ids32 ? w0 : w0 + 1];
+  const int64_t p = a.pos[b];
+
+  // Layers 0 and 1 are in flight while the gather resolves its id.
+  const int L = a.layers;
+  LayerIn<DT, CPL> f[2];
+  load_layer<DT, CPL>(a, a.L[0], row_off, idx, f[0]);
+  load_layer<DT, CPL>(a, a.L[L > 1 ? 1 : 0], row_off, idx, f[1]);
+
+  const int64_t id = a.ids32 ? static_cast<int64_t>(static_cast<int32_t>(id_lo))
+                             : static_cast<int64_t>((static_cast<uint64_t>(id_hi) << 32) | id_lo);
+  const bool ok = id >= 0 && id < a.vocab && p >= 0 && p < a.max_pos;
+  const size_t trow = static_cast<size_t>(ok ? id : 0) * static_cast<size_t>(a.D);
+  const size_t prow = static_cast<size_t>(ok ? p : 0) * static_cast<size_t>(a.D);
+  float xr[CPL][V];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const size_t i = static_cast<size_t>(idx[c]) * V;
+    float e[V], pe[V], o[V];
+    switch (a.tab_dt) {  // wave-uniform
+      case GSVK_F32: load_elems<GSVK_F32, V>(a.table, trow + i, e); break;
+      case GSVK_F16: load_elems<GSVK_F16, V>(a.table, trow + i, e); break;
+      default: load_elems<GSVK_BF16, V>(a.table, trow + i, e); break;
+    }
+    load_elems<GSVK_F32, V>(a.pe, prow + i, pe);
+#pragma unroll
+    for (int k = 0; k < V; ++k) o[k] = ok ? __builtin_fmaf(a.alpha, pe[k], e[k]) : __builtin_nanf("");
+    const u32x4 packed = S::pack(o);
+    if (FULL || on[c])
+      st16<false>(static_cast<char*>(a.x) + (row_off + i) * (DT == GSVK_F32 ? 4 : 2), packed);
+    S::unpack(packed, xr[c]);
+  }
+  if (!ok && lane == 0 && a.err) *a.err = 1;
+
+  float hr[CPL][V];
+  auto layer = [&](LayerIn<DT, CPL>& fi) {
+    ln_row<DT, CPL, FULL>(a, fi.att, fi.bo, xr, fi.g1, fi.be1, on, a.h, row_off, idx, hr);
+    ln_row<DT, CPL, FULL>(a, fi.ffo, fi.b2, hr, fi.g2, fi.be2, on, a.x, row_off, idx, xr);
+  };
+  // sched_barrier(0) keeps the scheduler from hoisting the next layer's arithmetic (and so its
+  // loads' waits) into the current layer's reductions: measured, that put a wait on loads issued
+  // half a layer earlier into every LayerNorm.
+  for (int l = 0; l + 1 < L; l += 2) {
+    layer(f[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_layer<DT, CPL>(a, a.L[l + 2 < L ? l + 2 : L - 1], row_off, idx, f[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    layer(f[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_layer<DT, CPL>(a, a.L[l + 3 < L ? l + 3 : L - 1], row_off, idx, f[1]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (L & 1) layer(f[0]);
+}
+
+// ReLU wave w of the launch: layer w / waves_per_layer, rows r0 .. r0 + kReluRows - 1, one column
+// tile of 64 chunks. bias_act_tile's arithmetic: relu(x + b1) in place.
+template <int DT>
+__device__ __forceinline__ void relu_tile(const StepArgs& a, long w) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  const long l = w / a.relu_waves_per_layer;
+  const long rem = w - l * a.relu_waves_per_layer;
+  const long rg = rem / a.relu_col_tiles, ct = rem - rg * a.relu_col_tiles;
+  const long nch = a.FF / V;
+  const long c = ct * kWave + threadIdx.x;
+  if (c >= nch) return;
+  const StepLayer& L = a.L[l];
+  float bi[V];
+  load_param(L.b1, static_cast<size_t>(c) * V, kZeros8, bi);
+  const long r0 = rg * kReluRows;
+  float v[kReluRows][V];
+#pragma unroll
+  for (int u = 0; u < kReluRows; ++u) {
+    const long r = r0 + u < a.B ? r0 + u : a.B - 1;
+    S::load(L.ff, static_cast<size_t>(r) * a.FF + c * V, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kReluRows; ++u) {
+    if (r0 + u < a.B) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[u][k] = relu_ref(v[u][k] + bi[k]);
+      S::store(L.ff, static_cast<size_t>(r0 + u) * a.FF + c * V, v[u]);
+    }
+  }
+}
+
+// Workgroups 0 .. B-1 (dispatched first) run the chains at raised wave priority, so a ReLU wave
+// sharing their SIMD does not delay the critical path; the rest run the ReLU tiles.
+template <int DT, int CPL, bool FULL>
+__global__ __launch_bounds__(kWave) void t2s_step_fused(StepArgs a) {
+  const long blk = blockIdx.x;
+  if (blk < a.B) {
+    __builtin_amdgcn_s_setprio(3);
+    chain_row<DT, CPL, FULL>(a, blk);
+  } else {
+    relu_tile<DT>(a, blk - a.B);
+  }
+}
+
+template <int DT>
+int launch_step(const StepArgs& a, hipStream_t st) {
+  constexpr int V = Store<DT>::VEC;
+  const long nch = a.D / V;
+  const unsigned grid = static_cast<unsigned>(a.B + a.layers * a.relu_waves_per_layer);
+  if (nch == kWave)
+    hipLaunchKernelGGL((t2s_step_fused<DT, 1, true>), dim3(grid), dim3(kWave), 0, st, a);
+  else if (nch < kWave)
+    hipLaunchKernelGGL((t2s_step_fused<DT, 1, false>), dim3(grid), dim3(kWave), 0, st, a);
+  else if (nch == 2 * kWave)
+    hipLaunchKernelGGL((t2s_step_fused<DT, 2, true>), dim3(grid), dim3(kWave), 0, st, a);
+  else
+    hipLaunchKernelGGL((t2s_step_fused<DT, 2, false>), dim3(grid), dim3(kWave), 0, st, a);
+  return launch_status();
+}
+
+bool a16(const void* p) { return !p || aligned16(p); }
+
+}  // namespace
+}  // namespace gsvk
+
+using namespace gsvk;
+
+extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
+  if (!d || !d->x || !d->h || !d->attn_out || !d->ff || !d->ffn_out || !d->audio_table ||
+      !d->ids || !d->pos || !d->pe)
+    return GSVK_E_NULL;
+  if (!valid_dtype(d->dtype) || !valid_dtype(d->table_dtype)) return GSVK_E_DTYPE;
+  if (d->index_type != GSVK_I64 && d->index_type != GSVK_I32) return GSVK_E_DTYPE;
+  if (d->batch == 0 || d->d_model == 0 || d->ffn == 0 || d->layers == 0 || d->vocab == 0 ||
+      d->max_pos == 0)
+    return GSVK_E_SIZE;
+  if (d->layers > static_cast<size_t>(kMaxStepLayers) || d->batch > (1ul << 20) ||
+      d->ffn > (1ul << 24) || d->vocab > (1ul << 40) || d->max_pos > (1ul << 40))
+    return GSVK_E_SIZE;
+  if (!(d->eps >= 0.0) || !std::isfinite(d->eps)) return GSVK_E_ARG;
+  const size_t V = d->dtype == GSVK_F32 ? 4 : 8;
+  // one wave holds a row: at most 2 chunks per lane (more would spill the prefetch ring); rows of
+  // whole 16-byte chunks
+  if (d->d_model % V || d->d_model / V > 2 * kWave || d->ffn % V) return GSVK_E_ARG;
+  for (size_t l = 0; l < d->layers; ++l)
+    if (!d->attn_out[l] || !d->ff[l] || !d->ffn_out[l]) return GSVK_E_NULL;
+
+  const size_t esz = dtype_size(d->dtype), B = d->batch, D = d->d_model, FF = d->ffn;
+  const size_t row_b = B * D * esz, ff_b = B * FF * esz, pb = D * 4;
+  // alignment: 16-byte rows everywhere (the per-op launches would take their vector paths)
+  bool al = a16(d->x) && a16(d->h) && a16(d->audio_table) && a16(d->pe);
+  auto at = [](const float* const* arr, size_t l) { return arr ? arr[l] : nullptr; };
+  for (size_t l = 0; l < d->layers && al; ++l)
+    al = a16(d->attn_out[l]) && a16(d->ff[l]) && a16(d->ffn_out[l]) && a16(at(d->bout, l)) &&
+         a16(at(d->n1g, l)) && a16(at(d->n1b, l)) && a16(at(d->b1, l)) && a16(at(d->b2, l)) &&
+         a16(at(d->n2g, l)) && a16(at(d->n2b, l));
+  if (!al) return GSVK_E_ARG;
+  // x and h are written by the chain and read by nothing else; each ff[l] is read and written in
+  // place by its own tiles only.
+  if (overlaps(d->x, row_b, d->h, row_b)) return GSVK_E_ALIAS;
+  const size_t isz = d->index_type == GSVK_I64 ? 8 : 4;
+  for (void* out : {d->x, d->h}) {
+    if (overlaps(out, row_b, d->audio_table, d->vocab * D * dtype_size(d->table_dtype)) ||
+        overlaps(out, row_b, d->ids, B * isz) || overlaps(out, row_b, d->pos, B * 8) ||
+        overlaps(out, row_b, d->pe, d->max_pos * D * 4) || overlaps(out, row_b, d->err, d->err ? 4 : 0))
+      return GSVK_E_ALIAS;
+    for (size_t l = 0; l < d->layers; ++l) {
+      if (overlaps(out, row_b, d->attn_out[l], row_b) || overlaps(out, row_b, d->ffn_out[l], row_b) ||
+          overlaps(out, row_b, d->ff[l], ff_b))
+        return GSVK_E_ALIAS;
+      for (const float* p : {at(d->bout, l), at(d->n1g, l), at(d->n1b, l), at(d->b2, l),
+                             at(d->n2g, l), at(d->n2b, l)})
+        if (overlaps(out, row_b, p, p ? pb : 0)) return GSVK_E_ALIAS;
+    }
+  }
+  for (size_t l = 0; l < d->layers; ++l)
+    for (size_t m = 0; m < d->layers; ++m) {
+      if ((m != l && overlaps(d->ff[l], ff_b, d->ff[m], ff_b)) ||
+          overlaps(d->ff[l], ff_b, d->attn_out[m], row_b) ||
+          overlaps(d->ff[l], ff_b, d->ffn_out[m], row_b) ||
+          overlaps(d->ff[l], ff_b, at(d->b1, m), at(d->b1, m) ? FF * 4 : 0))
+        return GSVK_E_ALIAS;
+    }
+
+  StepArgs a{};
+  a.table = d->audio_table;
+  a.ids = d->ids;
+  a.pos = d->pos;
+  a.pe = d->pe;
+  a.err = d->err;
+  a.x = d->x;
+  a.h = d->h;
+  a.vocab = static_cast<long>(d->vocab);
+  a.max_pos = static_cast<long>(d->max_pos);
+  a.B = static_cast<long>(B);
+  a.D = static_cast<long>(D);
+  a.FF = static_cast<long>(FF);
+  const long ff_nch = static_cast<long>(FF / V);
+  a.relu_col_tiles = static_cast<int>((ff_nch + kWave - 1) / kWave);
+  a.relu_waves_per_layer = ((a.B + kReluRows - 1) / kReluRows) * a.relu_col_tiles;
+  a.inv_n = 1.0 / static_cast<double>(D);
+  a.eps = static_cast<float>(d->eps);
+  a.alpha = d->alpha;
+  a.ids32 = d->index_type == GSVK_I32;
+  a.tab_dt = d->table_dtype;
+  a.layers = static_cast<int>(d->layers);
+  for (size_t l = 0; l < d->layers; ++l)
+    a.L[l] = StepLayer{d->attn_out[l], at(d->bout, l), at(d->n1g, l), at(d->n1b, l), d->ff[l],
+                       at(d->b1, l),   d->ffn_out[l],  at(d->b2, l),  at(d->n2g, l), at(d->n2b, l)};
+  if (static_cast<size_t>(a.B + a.layers * a.relu_waves_per_layer) >= (1ul << 31)) return GSVK_E_SIZE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (d->dtype) {
+    case GSVK_F32: return launch_step<GSVK_F32>(a, st);
+    case GSVK_F16: return launch_step<GSVK_F16>(a, st);
+    default: return launch_step<GSVK_BF16>(a, st);
+  }
+}

@@ -58,6 +58,8 @@ SIGNATURES = {
     "gsvk_t2s_step_run": (_i, [_vp, _vp]),
     "gsvk_t2s_step_launches": (_i, [_vp]),
     "gsvk_t2s_step_destroy": (None, [_vp]),
+    "gsvk_t2s_step_fused": (_i, [_vp, _vp]),
+    "gsvk_t2s_step_create_fused": (_i, [_vp, ctypes.POINTER(_vp)]),
     "gsvk_t2s_decode_eager": (_i, [_vp, _vp]),
     "gsvk_gsv_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "gsvk_gsv_open_memory": (_i, [_vp, _sz, ctypes.POINTER(_vp)]),
@@ -549,9 +551,10 @@ class T2SStepDesc(ctypes.Structure):
 
 
 class T2SStep:
-    """Owns a gsvk_t2s_step (graph of one decode step's epilogue launches) over torch buffers."""
+    """Owns a gsvk_t2s_step (graph of one decode step's epilogue launches) over torch buffers.
+    fused=True: the whole step as one kernel launch (gsvk_t2s_step_fused), bitwise the same."""
 
-    def __init__(self, bufs, eps=1e-5, graph=True):
+    def __init__(self, bufs, eps=1e-5, graph=True, fused=False):
         import torch
         self.bufs = bufs  # keep tensors alive
         L = len(bufs["attn_out"])
@@ -584,22 +587,25 @@ class T2SStep:
             setattr(d, name, ctypes.cast(arr(name), ctypes.POINTER(_vp)))
         self.desc = d
         self.handle = None
+        self.fused = fused
         if graph:
             h = _vp()
-            _check("gsvk_t2s_step_create", lib().gsvk_t2s_step_create(ctypes.byref(d),
-                                                                      ctypes.byref(h)))
+            create = "gsvk_t2s_step_create_fused" if fused else "gsvk_t2s_step_create"
+            _check(create, getattr(lib(), create)(ctypes.byref(d), ctypes.byref(h)))
             self.handle = h
 
     @property
     def launches(self):
-        return lib().gsvk_t2s_step_launches(self.handle) if self.handle else 1 + 3 * self.desc.layers
+        if self.handle:
+            return lib().gsvk_t2s_step_launches(self.handle)
+        return 1 if self.fused else 1 + 3 * self.desc.layers
 
     def run(self, stream=None):
         if self.handle:
             return _check("gsvk_t2s_step_run", lib().gsvk_t2s_step_run(self.handle,
                                                                        _stream(stream)))
-        return _check("gsvk_t2s_step_eager", lib().gsvk_t2s_step_eager(ctypes.byref(self.desc),
-                                                                       _stream(stream)))
+        fn = "gsvk_t2s_step_fused" if self.fused else "gsvk_t2s_step_eager"
+        return _check(fn, getattr(lib(), fn)(ctypes.byref(self.desc), _stream(stream)))
 
     def close(self):
         if self.handle:

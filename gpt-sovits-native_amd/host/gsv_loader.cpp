@@ -87,8 +87,9 @@ int parse(gsvk_gsv* g) {
     uint64_t numel = 1;
     for (uint32_t d = 0; d < t.rank; ++d) {
       t.dims[d] = r.get<uint32_t>();
+      // checked before the multiply: numel <= 2^40 times a dim below 2^32 could wrap 64 bits
+      if (t.dims[d] != 0 && numel > kMaxNumel / t.dims[d]) return GSVK_E_FORMAT;
       numel *= t.dims[d];
-      if (numel > kMaxNumel) return GSVK_E_FORMAT;
     }
     t.numel = numel;
     t.src_dtype = r.get<uint16_t>();

@@ -173,6 +173,14 @@ extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_ste
                 static_cast<int>(1 + 3 * desc->layers), out);
 }
 
+extern "C" int gsvk_t2s_step_create_fused(const gsvk_t2s_step_desc* desc, gsvk_t2s_step** out) {
+  if (!out) return GSVK_E_NULL;
+  *out = nullptr;
+  if (!desc_ok(desc)) return GSVK_E_NULL;
+  // an unsupported shape fails inside the capture; record() then ends it and keeps no graph
+  return record([desc](hipStream_t st) { return gsvk_t2s_step_fused(desc, st); }, 1, out);
+}
+
 extern "C" int gsvk_t2s_decode_eager(const gsvk_t2s_decode_desc* desc, void* stream) {
   if (!decode_ok(desc)) return GSVK_E_NULL;
   return issue_decode(desc, stream);

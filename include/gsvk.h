@@ -173,8 +173,9 @@ int gsvk_gemv_f16w_ln(int x_dtype, int round_x, const void* z, size_t ldz, const
  * whatever its value (the partition of the keys, so the rounding, follows it). With more
  * than one chunk the partial states go through `workspace` (gsvk_decode_attention_workspace_bytes
  * bytes, 16-byte aligned; no initialisation needed); with a NULL or smaller workspace every sequence
- * runs as one chunk. A position outside [0, max_len) (undefined in the reference) writes a NaN row,
- * leaves the caches untouched and stores 1 into *err when err != NULL.
+ * runs as one chunk. Cache rows at and past pos[b] may hold any bits (stale, Inf, NaN): none of
+ * them enters the result. A position outside [0, max_len) (undefined in the reference) writes a
+ * NaN row, leaves the caches untouched and stores 1 into *err when err != NULL.
  * The softmax is formed online (running maximum, rescaled sums) in another order than the
  * reference's; results agree within fp32 rounding: |out - ref| <= 1e-5 * max(1, max |v|).
  * ------------------------------------------------------------------------------------------------ */
@@ -182,7 +183,8 @@ int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* qkv, size_t 
                           void* v_cache, size_t max_len, const int64_t* pos, void* out, size_t ldo,
                           size_t batch, size_t heads, size_t head_dim, size_t len_bound,
                           void* workspace, size_t workspace_bytes, int32_t* err, void* stream);
-/* Workspace bytes gsvk_decode_attention uses for these sizes (0: none). Host only. */
+/* Workspace bytes gsvk_decode_attention uses for these sizes (0: none). Host only. len_bound 0:
+ * the size for the longest context, an upper bound of what the call needs for any max_len. */
 size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t head_dim,
                                              size_t len_bound);
 

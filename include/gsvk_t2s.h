@@ -71,6 +71,20 @@ int gsvk_t2s_step_run(gsvk_t2s_step* step, void* stream);
 int gsvk_t2s_step_launches(const gsvk_t2s_step* step);
 void gsvk_t2s_step_destroy(gsvk_t2s_step* step);
 
+/* The same step as ONE kernel launch (no counterpart in the reference, which runs these loops
+ * one row at a time; replaces the 1 + 3*layers launches above). The LayerNorm chain is row-local
+ * (row b of layer l+1 reads only row b of layer l), so one wave walks the whole chain of one
+ * sequence while the other waves of the launch run the ReLU tiles. Results are bitwise those of
+ * gsvk_t2s_step_eager: every h and x is stored as the per-op launches store it (the final x and h
+ * are the last layer's), every ff[l] is updated in place.
+ * Limits: layers <= 32 (the layer pointers travel in the kernel arguments); d_model a multiple of
+ * 8 (4 for f32) and at most 1024 (f16 / bf16) or 512 (f32) elements; ffn a multiple of 8 (4);
+ * every pointer 16-byte aligned; x, h, ff[l] overlapping nothing else.
+ * GSVK_E_ARG / GSVK_E_SIZE when the shape is outside these limits (use the forms above). */
+int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* desc, void* stream);
+/* gsvk_t2s_step_fused recorded into a HIP graph (one node); run / launches / destroy as above. */
+int gsvk_t2s_step_create_fused(const gsvk_t2s_step_desc* desc, gsvk_t2s_step** out);
+
 /* ------------------------------------------------------------------------------------------------
  * The whole T2S decode step for B sequences: the same epilogue chain with the GEMVs and the
  * attention that feed it, as T2SEngine::generate runs one token (t2s_engine.cpp:1864-1885:

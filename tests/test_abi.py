@@ -270,6 +270,67 @@ def test_t2s_step_validation(gsvk_lib):
     assert gsvk_lib.gsvk_t2s_step_run(None, None) == gsvk.E_NULL
     assert gsvk_lib.gsvk_t2s_step_launches(None) == 0
     gsvk_lib.gsvk_t2s_step_destroy(None)
+    assert gsvk_lib.gsvk_t2s_step_fused(None, None) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_t2s_step_create_fused(None, ctypes.byref(out)) == gsvk.E_NULL
+
+
+def _step_desc(L=24, B=64, D=512, FF=2048, dt=gsvk.F16, base=0x10000000):
+    """A decode-step descriptor over fake, never dereferenced, disjoint 16-byte aligned device
+    addresses (16 MiB apart): the fused entry point must reject every variant below in validation."""
+    nxt = [base]
+
+    def addr():
+        nxt[0] += 1 << 24
+        return nxt[0]
+    keep = {}
+
+    def arr(name):
+        a = (ctypes.c_void_p * L)(*[addr() for _ in range(L)])
+        keep[name] = a
+        return ctypes.cast(a, ctypes.POINTER(ctypes.c_void_p))
+    d = gsvk.T2SStepDesc()
+    d.dtype, d.batch, d.d_model, d.ffn, d.layers, d.eps = dt, B, D, FF, L, 1e-5
+    d.audio_table, d.table_dtype, d.vocab = addr(), gsvk.F16, 1025
+    d.ids, d.index_type, d.pos, d.pe, d.max_pos, d.alpha = addr(), gsvk.I64, addr(), addr(), 2048, 0.9
+    d.err, d.x, d.h = addr(), addr(), addr()
+    for name in ("attn_out", "bout", "n1g", "n1b", "ff", "b1", "ffn_out", "b2", "n2g", "n2b"):
+        setattr(d, name, arr(name))
+    return d, keep
+
+
+def test_t2s_step_fused_validation(gsvk_lib):
+    f = lambda d: gsvk_lib.gsvk_t2s_step_fused(ctypes.byref(d), None)
+    d, k = _step_desc(L=33)
+    assert f(d) == gsvk.E_SIZE                       # more layers than the kernel arguments hold
+    d, k = _step_desc(D=1032)
+    assert f(d) == gsvk.E_ARG                        # 129 chunks: more than two per lane
+    d, k = _step_desc(D=516)
+    assert f(d) == gsvk.E_ARG                        # not whole 16-byte chunks
+    d, k = _step_desc(D=1024, dt=gsvk.F32)
+    assert f(d) == gsvk.E_ARG                        # f32 rows of more than 512
+    d, k = _step_desc(FF=2044)
+    assert f(d) == gsvk.E_ARG
+    d, k = _step_desc()
+    d.x = d.h + 64
+    assert f(d) == gsvk.E_ALIAS                      # x overlaps h
+    d, k = _step_desc()
+    d.h = k["attn_out"][3]
+    assert f(d) == gsvk.E_ALIAS                      # h is an input of layer 3
+    d, k = _step_desc()
+    k["ff"][5] = k["ff"][2] + 1024
+    assert f(d) == gsvk.E_ALIAS                      # two layers' FFN buffers overlap
+    d, k = _step_desc()
+    d.x = d.x + 8
+    assert f(d) == gsvk.E_ARG                        # x not 16-byte aligned
+    d, k = _step_desc()
+    d.index_type = 7
+    assert f(d) == gsvk.E_DTYPE
+    d, k = _step_desc()
+    d.eps = float("nan")
+    assert f(d) == gsvk.E_ARG
+    d, k = _step_desc()
+    d.ids = None
+    assert f(d) == gsvk.E_NULL
 
 
 def _decoder_desc(frames=500, c0=768, n_stages=5, fake=0x1000):

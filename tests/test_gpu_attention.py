@@ -37,9 +37,20 @@ def oracle_kv(kv_dt):
     return F32 if kv_dt == BF16 else kv_dt
 
 
-def case(B, H, HD, max_len, pos, kv_dt, out_dt, seed, len_bound=0, use_ws=True):
+def poison_rows(kc, pos, kv_dt):
+    """Fill cache rows pos[b] .. max_len - 1 of every sequence with NaN / +Inf / -Inf bit patterns
+    (rows the call may not read into its result: the appended row and everything after it)."""
+    pats = ([0x7E00, 0x7C00, 0xFC00] if kv_dt == F16 else
+            [0x7FC0, 0x7F80, 0xFF80] if kv_dt == BF16 else [0x7FC00000, 0x7F800000, 0xFF800000])
+    bits = kc.view(np.uint16 if kv_dt != F32 else np.uint32)
+    for b, p in enumerate(pos):
+        n = bits.shape[1] - p
+        bits[b, p:] = np.resize(np.asarray(pats, bits.dtype), (n, 1)).repeat(bits.shape[2], 1)
+
+
+def case(B, H, HD, max_len, pos, kv_dt, out_dt, seed, len_bound=0, use_ws=True, poison=False):
     say(f"attention B={B} H={H} HD={HD} max_len={max_len} kv={kv_dt} out={out_dt} "
-        f"len_bound={len_bound} ws={use_ws}")
+        f"len_bound={len_bound} ws={use_ws} poison={poison}")
     r = rng(seed)
     D = H * HD
     qkv = r.standard_normal((B, 3 * D)).astype(np.float32)
@@ -53,9 +64,12 @@ def case(B, H, HD, max_len, pos, kv_dt, out_dt, seed, len_bound=0, use_ws=True):
     kc = O.to_storage(kv_dt, k32)
     vc = O.to_storage(kv_dt, v32)
     pos = np.asarray(pos, dtype=np.int64)
+    if poison:
+        for a in (kc, vc):
+            poison_rows(a, pos, kv_dt)
     okv = oracle_kv(kv_dt)
-    kc_o = kc if okv == kv_dt else k32.copy()
-    vc_o = vc if okv == kv_dt else v32.copy()
+    kc_o = kc if okv == kv_dt else O.to_f32(kv_dt, kc)
+    vc_o = vc if okv == kv_dt else O.to_f32(kv_dt, vc)
     kc_o, vc_o = kc_o.copy(), vc_o.copy()
     want = O.decode_attention(okv, qkv, kc_o, vc_o, pos, H, HD)
     Q = torch.from_numpy(qkv).cuda()
@@ -66,7 +80,8 @@ def case(B, H, HD, max_len, pos, kv_dt, out_dt, seed, len_bound=0, use_ws=True):
     gsvk.decode_attention(Q, KC, VC, P, OUT, H, len_bound=len_bound, err=ERR, use_workspace=use_ws)
     torch.cuda.synchronize()
     got = O.to_f32(out_dt, host(OUT, out_dt))
-    vmax = np.abs(O.to_f32(kv_dt, vc)).reshape(B, -1).max(1)
+    vmax = np.array([np.abs(O.to_f32(kv_dt, vc[b, :p])).max() if p > 0 else 0.0
+                     for b, p in enumerate(np.clip(pos, 0, max_len))])
     tol = 1e-5 * np.maximum(1.0, vmax)[:, None]
     if out_dt != F32:
         tol = tol + step16(out_dt, want)
@@ -82,11 +97,13 @@ def case(B, H, HD, max_len, pos, kv_dt, out_dt, seed, len_bound=0, use_ws=True):
                           f"{bad[:3].tolist()}"
     # the append is exact; other rows untouched
     kc_g, vc_g = host(KC, kv_dt), host(VC, kv_dt)
+    u = lambda a: a.view(np.uint32) if a.dtype == np.float32 else a
     if okv == kv_dt:
-        assert np.array_equal(kc_g, kc_o) and np.array_equal(vc_g, vc_o), "cache rows differ"
+        assert np.array_equal(u(kc_g), u(kc_o)) and np.array_equal(u(vc_g), u(vc_o)), \
+            "cache rows differ"
     else:
-        assert np.array_equal(O.to_f32(kv_dt, kc_g), kc_o) and \
-            np.array_equal(O.to_f32(kv_dt, vc_g), vc_o), "cache rows differ"
+        assert np.array_equal(u(O.to_f32(kv_dt, kc_g)), u(kc_o)) and \
+            np.array_equal(u(O.to_f32(kv_dt, vc_g)), u(vc_o)), "cache rows differ"
     return got, int(ERR.item()), (Q, KC, VC, P, OUT)
 
 
@@ -130,6 +147,17 @@ def test_attention_deterministic():
     torch.cuda.synchronize()
     b = host(OUT, F32)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("kv_dt", [F16, F32, BF16])
+@pytest.mark.parametrize("len_bound,use_ws", [(0, False), (1100, True)])
+def test_attention_ignores_nonfinite_rows_past_pos(kv_dt, len_bound, use_ws):
+    """Rows at and past pos hold NaN / +-Inf: only rows < pos and the appended k / v enter the
+    result (a padded key slot of a wave re-reads the last row of its chunk, which for the chunk
+    holding pos is that row). Lengths cover odd key counts per wave, one key, and chunk borders."""
+    pos = [0, 1, 2, 3, 5, 7, 9, 17, 33, 64, 99, 130, 257, 513, 1023, 1099]
+    _, e, _ = case(len(pos), 16, 32, 1100, pos, kv_dt, F32, 8, len_bound, use_ws, poison=True)
+    assert e == 0
 
 
 def test_attention_rejects_bad_arguments():

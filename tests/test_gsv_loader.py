@@ -105,6 +105,24 @@ def test_rejects_malformed_directory():
     assert rc_of(patch(good, rank_off, "<H", 9)) == gsvk.E_FORMAT
 
 
+def test_rejects_dims_whose_product_wraps_64_bits():
+    """dims [2^20, 2^20, 2^24]: the running product passes 2^40 exactly, then the next multiply
+    would wrap 2^64 to 0 and a 0-byte segment would match. The bound is checked before the
+    multiply, so the header is rejected like any other numel above 2^40."""
+    good = gsv_bytes("t", {"x": np.ones((1, 1, 3), np.float32)})
+    assert rc_of(good) == 0
+    nl = struct.unpack_from("<H", good, 12)[0]
+    cl = struct.unpack_from("<I", good, 14 + nl)[0]
+    dims_off = 14 + nl + 4 + cl + 4 + 2 + 1 + 2
+    assert struct.unpack_from("<3I", good, dims_off) == (1, 1, 3)
+    b = bytearray(good)
+    struct.pack_into("<3I", b, dims_off, 1 << 20, 1 << 20, 1 << 24)
+    struct.pack_into("<Q", b, dims_off + 12 + 2 + 8, 0)      # f32 bytes 0 = the wrapped numel x 4
+    assert rc_of(bytes(b)) == gsvk.E_FORMAT
+    struct.pack_into("<3I", b, dims_off, 1 << 20, 1 << 20, 1)  # exactly 2^40 elements: the size
+    assert rc_of(bytes(b)) == gsvk.E_FORMAT                    # check (0 bytes) still rejects it
+
+
 def test_fp16_sizes_and_slim_files():
     big = {"w": np.ones((64, 64), np.float16), "b": np.ones(4, np.float32)}
     b = gsv_bytes("t", big)
