@@ -217,11 +217,16 @@ constexpr size_t kStreamBytes = size_t(256) << 20;
 // with v_readlane. The result is wave-uniform; the two broadcasts replace an LDS swizzle and a
 // second readlane on the critical path of every row reduction (the sum is the same bits as
 // (r0 + r1) + (r2 + r3): fp32 addition is commutative).
+// (v_permlane16/32_swap would keep the sum in VGPRs, but this compiler folds the two results of
+// a swap whose operands are the same value into one: it emitted s.x + s.x for s.x + s.y.)
 
+// Whole-row DPP move with bound_ctrl set: every lane has its source lane for these controls, so
+// the values are the plain move's, and the compiler can fold the move into the add that follows
+// (v_add_f32_dpp: one instruction per reduction step instead of two).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
   return __builtin_bit_cast(
-      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
 }
 // DPP move restricted to ROW_MASK rows; the other rows get 0.
 template <int CTRL, int ROW_MASK>
@@ -238,6 +243,28 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_rows_f32<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
   v += dpp_rows_f32<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Per-lane partial sums of one 16-byte chunk (4 or 8 values) as a balanced tree: depth 2-3
+// instead of a 3-7 long dependent chain (each dependent VALU step costs ~11 cycles on MI355X, and
+// the LayerNorm reductions sit on the critical path of latency-bound calls).
+template <int V>
+__device__ __forceinline__ float chunk_sum(const float (&v)[V]) {
+  static_assert(V == 4 || V == 8, "chunk of 4 or 8 values");
+  if constexpr (V == 4) return (v[0] + v[1]) + (v[2] + v[3]);
+  else return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+// Sum of (v - mean)^2 over one chunk: pairs fma(d1, d1, d0 * d0), then a tree of the pairs.
+template <int V>
+__device__ __forceinline__ float chunk_sumsq(const float (&v)[V], float mean) {
+  float q[V / 2];
+#pragma unroll
+  for (int k = 0; k < V / 2; ++k) {
+    const float d0 = v[2 * k] - mean, d1 = v[2 * k + 1] - mean;
+    q[k] = __builtin_fmaf(d1, d1, d0 * d0);
+  }
+  if constexpr (V == 4) return q[0] + q[1];
+  else return (q[0] + q[1]) + (q[2] + q[3]);
 }
 
 __device__ __forceinline__ double wave_sum(double v) {

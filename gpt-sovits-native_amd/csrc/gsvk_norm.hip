@@ -46,6 +46,8 @@ __device__ __forceinline__ float finish_rstd(float var, double eps) {
 // (one-shot grid). All x / residual chunks of the wave's R rows are loaded (packed) before any
 // arithmetic. The statistics are finalized with the host's 1/n and v_rsq_f32 (1 ulp): the latency
 // of a double-precision divide and square root sits on the critical path of every small call.
+// Per-lane partial sums are balanced trees per chunk (chunk_sum / chunk_sumsq), chunks added in
+// order: the order the one-launch decode step (gsvk_step.hip) repeats, so both give the same bits.
 template <int DT, int CPL, int R, bool NT, int BLOCK, bool HAS_RES>
 __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
   using S = Store<DT>;
@@ -127,8 +129,7 @@ __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
 #pragma unroll
           for (int k = 0; k < V; ++k) h[c][k] = h[c][k] + rv[k];
         }
-#pragma unroll
-        for (int k = 0; k < V; ++k) s += h[c][k];
+        s = c == 0 ? chunk_sum(h[c]) : s + chunk_sum(h[c]);
       } else {
 #pragma unroll
         for (int k = 0; k < V; ++k) h[c][k] = 0.f;
@@ -140,13 +141,7 @@ __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int idx = lane + c * kWave;
-      if (idx < nch) {
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-          const float d = h[c][k] - mean;
-          q = __builtin_fmaf(d, d, q);
-        }
-      }
+      if (idx < nch) q = c == 0 ? chunk_sumsq(h[c], mean) : q + chunk_sumsq(h[c], mean);
     }
     const float sq = wave_sum(q);
     const float var = static_cast<float>(static_cast<double>(sq) * a.inv_n);

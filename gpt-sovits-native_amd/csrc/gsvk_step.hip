@@ -14,7 +14,7 @@
 // reductions) instead of 73 launch latencies.
 //
 // The chain wave prefetches the next layers' inputs (attn_out / ffn_out rows and the six parameter
-// vectors) two layers ahead into a register ring, so HBM latency is paid once, not per LayerNorm.
+// vectors) three layers ahead into a register ring, so HBM latency is paid once, not per LayerNorm.
 // Its row reductions are DPP only (gsvk_common.hpp wave_sum): no LDS round trip per LayerNorm.
 //
 // Numerics: the same operations in the same order as ln_rows_tile (gsvk_norm.hip), bias_act_tile
@@ -57,6 +57,7 @@ struct StepArgs {
   long relu_waves_per_layer;  // ceil(B / kReluRows) * ceil(FF chunks / 64)
   int relu_col_tiles;         // ceil(FF chunks / 64)
   double inv_n;               // 1 / D, computed on the host
+  float inv_n_f;              // the same in fp32 (exact when D is a power of two)
   float eps;
   float alpha;
   int ids32;
@@ -105,11 +106,10 @@ struct LayerIn {
 };
 
 template <int DT, int CPL>
-__device__ __forceinline__ void load_layer(const StepArgs& a, const StepLayer& L, size_t row_off,
+__device__ __forceinline__ void load_layer(const StepLayer& L, size_t row_off,
                                            const int (&idx)[CPL], LayerIn<DT, CPL>& f) {
   constexpr int V = Store<DT>::VEC;
   constexpr size_t kEsz = DT == GSVK_F32 ? 4 : 2;
-  (void)a;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const size_t e = row_off + static_cast<size_t>(idx[c]) * V;
@@ -129,8 +129,8 @@ __device__ __forceinline__ void load_layer(const StepArgs& a, const StepLayer& L
 }
 
 // y = LN((in + bias) + res) over one row held by the wave, the operation order of ln_rows_tile:
-// per-lane sum in (chunk, element) order, wave_sum, mean = float(double(sum) / n), centred second
-// moment by fmaf, rstd = rsq(var + eps), y = fmaf((v - mean) rstd, g, b). Stores y and returns its
+// per-lane chunk trees added in chunk order, wave_sum, mean = float(double(sum) / n), centred
+// second moment (chunk_sumsq), rstd = rsq(var + eps), y = fmaf((v - mean) rstd, g, b). Stores y and returns its
 // rounded storage value in `yr` (what the next LayerNorm reads back as its residual).
 template <int DT, int CPL, bool FULL>
 __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL],
@@ -152,28 +152,24 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
       for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + bias[c][k];
 #pragma unroll
       for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + res[c][k];
-#pragma unroll
-      for (int k = 0; k < V; ++k) s += v[c][k];
+      s = c == 0 ? chunk_sum(v[c]) : s + chunk_sum(v[c]);
     } else {
 #pragma unroll
       for (int k = 0; k < V; ++k) v[c][k] = 0.f;
     }
   }
-  const float sum = wave_sum(s);
-  const float mean = static_cast<float>(static_cast<double>(sum) * a.inv_n);
+  // With FULL rows n = 64 * CPL * VEC is a power of two, so scaling by 1/n is exact in fp32 and
+  // commutes with every rounding of the sum: the lane partials are scaled before the reduction
+  // (one fewer dependent step after it), and the result is the same value as ln_rows_tile's
+  // float(double(sum) * (1/n)) without the double-precision latency.
+  const float mean = FULL ? wave_sum(s * a.inv_n_f)
+                          : static_cast<float>(static_cast<double>(wave_sum(s)) * a.inv_n);
   float q = 0.f;
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    if (FULL || on[c]) {
-#pragma unroll
-      for (int k = 0; k < V; ++k) {
-        const float d = v[c][k] - mean;
-        q = __builtin_fmaf(d, d, q);
-      }
-    }
-  }
-  const float sq = wave_sum(q);
-  const float var = static_cast<float>(static_cast<double>(sq) * a.inv_n);
+  for (int c = 0; c < CPL; ++c)
+    if (FULL || on[c]) q = c == 0 ? chunk_sumsq(v[c], mean) : q + chunk_sumsq(v[c], mean);
+  const float var = FULL ? wave_sum(q * a.inv_n_f)
+                         : static_cast<float>(static_cast<double>(wave_sum(q)) * a.inv_n);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
@@ -192,11 +188,11 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
 // The chain of sequence b: gather + alpha*PE, then LN1 / LN2 of every layer. FULL: every lane
 // holds CPL whole chunks (D = 64 * CPL * VEC), so no store needs a guard.
 //
-// The layer loop runs in pairs with no condition inside: layer l sits in ring slot l % 2 and the
-// slot is refilled with layer l + 2 (clamped to the last layer: an in-bounds reread whose values
+// The layer loop runs in threes with no condition inside: layer l sits in ring slot l % 3 and the
+// slot is refilled with layer l + 3 (clamped to the last layer: an in-bounds reread whose values
 // are never used) right after it runs. With no branch between the loads and their uses, the
-// compiler's wait before each layer covers only that layer's loads (the other slot's loads stay in
-// flight); an odd last layer runs after the loop from slot 0.
+// compiler's wait before each layer covers only that layer's loads (the other slots' loads stay in
+// flight); the last L mod 3 layers run after the loop from slots 0 and 1.
 template <int DT, int CPL, bool FULL>
 __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   using S = Store<DT>;
@@ -220,11 +216,12 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   const uint32_t id_lo = idw[w0], id_hi = idw[a.ids32 ? w0 : w0 + 1];
   const int64_t p = a.pos[b];
 
-  // Layers 0 and 1 are in flight while the gather resolves its id.
+  // Layers 0, 1 and 2 are in flight while the gather resolves its id.
   const int L = a.layers;
-  LayerIn<DT, CPL> f[2];
-  load_layer<DT, CPL>(a, a.L[0], row_off, idx, f[0]);
-  load_layer<DT, CPL>(a, a.L[L > 1 ? 1 : 0], row_off, idx, f[1]);
+  LayerIn<DT, CPL> f[3];
+  load_layer<DT, CPL>(a.L[0], row_off, idx, f[0]);
+  load_layer<DT, CPL>(a.L[L > 1 ? 1 : 0], row_off, idx, f[1]);
+  load_layer<DT, CPL>(a.L[L > 2 ? 2 : L - 1], row_off, idx, f[2]);
 
   const int64_t id = a.ids32 ? static_cast<int64_t>(static_cast<int32_t>(id_lo))
                              : static_cast<int64_t>((static_cast<uint64_t>(id_hi) << 32) | id_lo);
@@ -259,17 +256,28 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   // sched_barrier(0) keeps the scheduler from hoisting the next layer's arithmetic (and so its
   // loads' waits) into the current layer's reductions: measured, that put a wait on loads issued
   // half a layer earlier into every LayerNorm.
-  for (int l = 0; l + 1 < L; l += 2) {
+  // The layer records (ten pointers each, in the kernel arguments) are read into registers one
+  // layer before the refill that uses them: a record read right before its loads put a scalar-load
+  // round trip (the kernel-argument lines miss the scalar cache) in front of every refill.
+  StepLayer rec = a.L[L > 3 ? 3 : L - 1];
+  auto refill = [&](LayerIn<DT, CPL>& fi, int l) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_layer<DT, CPL>(rec, row_off, idx, fi);
+    rec = a.L[l + 1 < L ? l + 1 : L - 1];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int l = 0;
+  for (; l + 2 < L; l += 3) {
     layer(f[0]);
-    __builtin_amdgcn_sched_barrier(0);
-    load_layer<DT, CPL>(a, a.L[l + 2 < L ? l + 2 : L - 1], row_off, idx, f[0]);
-    __builtin_amdgcn_sched_barrier(0);
+    refill(f[0], l + 3);
     layer(f[1]);
-    __builtin_amdgcn_sched_barrier(0);
-    load_layer<DT, CPL>(a, a.L[l + 3 < L ? l + 3 : L - 1], row_off, idx, f[1]);
-    __builtin_amdgcn_sched_barrier(0);
+    refill(f[1], l + 4);
+    layer(f[2]);
+    refill(f[2], l + 5);
   }
-  if (L & 1) layer(f[0]);
+  // the last 1 or 2 layers (L mod 3), already in slots 0 and 1
+  if (l < L) layer(f[0]);
+  if (l + 1 < L) layer(f[1]);
 }
 
 // ReLU wave w of the launch: layer w / waves_per_layer, rows r0 .. r0 + kReluRows - 1, one column
@@ -414,6 +422,7 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
   a.relu_col_tiles = static_cast<int>((ff_nch + kWave - 1) / kWave);
   a.relu_waves_per_layer = ((a.B + kReluRows - 1) / kReluRows) * a.relu_col_tiles;
   a.inv_n = 1.0 / static_cast<double>(D);
+  a.inv_n_f = static_cast<float>(a.inv_n);
   a.eps = static_cast<float>(d->eps);
   a.alpha = d->alpha;
   a.ids32 = d->index_type == GSVK_I32;
