@@ -35,6 +35,8 @@ SIGNATURES = {
     "gsvk_decode_attention": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz,
                                    _sz, _vp, _sz, _vp, _vp]),
     "gsvk_decode_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
+    "gsvk_decode_attention_noalloc": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz,
+                                           _sz, _sz, _vp, _vp]),
     "gsvk_conv1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
                          _sz, _sz, _vp]),
     "gsvk_conv1d_packed_elems": (_sz, [_sz, _sz, _sz]),
@@ -468,6 +470,18 @@ def decode_attention(qkv, k_cache, v_cache, pos, out, heads, len_bound=0, err=No
                                               max_len, _ptr(pos), _ptr(out), _rows(out)[2], B,
                                               heads, hd, len_bound, ws, wsb, _ptr(err),
                                               _stream(stream)))
+
+
+def decode_attention_noalloc(qkv, k_cache, v_cache, pos, out, heads, len_bound=0, err=None,
+                             stream=None):
+    """decode_attention with the chunk states in the library's own device array (no workspace)."""
+    B = qkv.shape[0]
+    D = out.shape[-1]
+    return _check("gsvk_decode_attention_noalloc",
+                  lib().gsvk_decode_attention_noalloc(
+                      dtype_code(k_cache), dtype_code(out), _ptr(qkv), _rows(qkv)[2],
+                      _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], _ptr(pos), _ptr(out),
+                      _rows(out)[2], B, heads, D // heads, len_bound, _ptr(err), _stream(stream)))
 
 
 def groupnorm_gelu(x, gamma, beta, y, eps, apply_gelu=True, stream=None):

@@ -187,6 +187,19 @@ int gsvk_decode_attention(int kv_dtype, int out_dtype, const float* qkv, size_t 
  * the size for the longest context, an upper bound of what the call needs for any max_len. */
 size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t head_dim,
                                              size_t len_bound);
+/* gsvk_decode_attention without a workspace argument, for callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). No counterpart in the reference. The
+ * key-chunk states live in a 4 MiB device array owned by the library, one copy per GPU, kept until
+ * the process ends; the call allocates nothing. Every call on a GPU shares that copy, so calls in
+ * flight at once on one GPU (different streams) race on it. Same arguments (minus the workspace)
+ * and the same bits as gsvk_decode_attention with a workspace of
+ * gsvk_decode_attention_workspace_bytes. GSVK_E_SIZE when the chunk states would exceed 4 MiB
+ * (batch x chunks x 3 KiB: at most 1023 x 3 KiB on a 256-CU MI355X, so never there); GSVK_E_HIP
+ * when the array's device address cannot be looked up. */
+int gsvk_decode_attention_noalloc(int kv_dtype, int out_dtype, const float* qkv, size_t ldq,
+                                  void* k_cache, void* v_cache, size_t max_len, const int64_t* pos,
+                                  void* out, size_t ldo, size_t batch, size_t heads,
+                                  size_t head_dim, size_t len_bound, int32_t* err, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * SoVITS Conv1d, same padding with dilation, and the ResBlock passes that follow it.
