@@ -21,6 +21,8 @@ Also reported (same JSON line):
                 repetitions by reading a 512 MiB buffer), in GB/s, rows/s and fraction of 8 TB/s;
   copy_GBps     a plain device-to-device copy of 1 GiB measured the same way (achievable-bandwidth
                 reference for the replicated figures);
+  write_only_GBps  a 1 GiB write-only stream measured the same way (the ceiling of write-dominated
+                kernels such as the gather);
   sovits_decoder  the SoVITS ResBlock epilogues at every decoder stage shape (reference 768-channel
                 geometry and the 512-start geometry), with the per-stage launch counts summed into
                 epilogue microseconds per 10 s of audio;
@@ -271,6 +273,23 @@ def kernel_suite(torch, gsvk, dev, only=None):
         run(name, 2, st_, rp_, b_, 1, rep_bytes_fn=ub_, rows=lambda k: rows * k)
 
     run_emb("embed_pe_prefill_1024x512", 1024, 512)
+
+    def hot_case(rows, rep):
+        """The gather at the same granularity with every id 0 and every position 0: its table and
+        PE reads hit one 3 KiB working set in L1, so what remains is the id / position reads and
+        the 1 KiB row writes per wave. The ceiling of the gather's write path on this GPU."""
+        def make(k):
+            tab = rn(1, D, std=0.02)
+            ids = torch.zeros(rows * k, dtype=torch.int64, device=dev)
+            pos = torch.zeros(rows * k, dtype=torch.int64, device=dev)
+            o = torch.empty(rows * k, D, dtype=f16, device=dev)
+            return lambda: gsvk.embed_pe(tab, ids, pe, 0.93, o, pos=pos)
+        return (lambda: make(1), lambda: (rep, make(rep)), lambda k: embed_bytes(rows * k, D, 2, 2),
+                lambda k: rows * k * (8 + 8 + 2 * D) + D * 2 + D * 4)
+
+    st_, rp_, b_, ub_ = hot_case(1024, 512)
+    run("embed_pe_hot_row_ceiling_1024x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_,
+        rows=lambda k: 1024 * k)
 
     def prefill_case(rep):
         """The stated prefill pattern: 512 phone ids from the [732, 512] table and 512 semantic ids
@@ -854,6 +873,20 @@ def copy_bandwidth(torch, dev, nbytes=1 << 30):
     return round(gbs, 1)
 
 
+def write_bandwidth(torch, dev, nbytes=1 << 30):
+    """A write-only stream of 1 GiB (torch's fill kernel: 16-byte stores, nothing read), timed like
+    the replicated kernels: the achievable HBM write bandwidth, the ceiling of write-dominated
+    kernels such as the gather (1 KiB row written per 16 B of ids read; its table and PE reads are
+    served from the caches)."""
+    dst = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    ms = measure_reps(torch, lambda: dst.fill_(1.0), Flusher(torch, dev))
+    del dst
+    torch.cuda.empty_cache()
+    gbs = nbytes / ms / 1e6
+    log(f"  write-only 1 GiB: {gbs:.1f} GB/s ({100 * gbs / PEAK_GBS:.1f}%)")
+    return round(gbs, 1)
+
+
 PMC_COPY_BYTES = 256 << 20
 PMC_LAUNCHES = 30
 PMC_KERNEL = "t2s_step_fused"
@@ -957,6 +990,9 @@ def main():
     gsvk.lib()  # fails loudly when libgsvk.so is missing
     dev = torch.device("cuda:0")
 
+    if a.only == "write_bandwidth":
+        write_bandwidth(torch, dev)
+        return
     if a.only:
         kernel_suite(torch, gsvk, dev, only=a.only)
         return
@@ -1058,9 +1094,10 @@ def main():
                "single_thread_cv": round(res[1]["cv"], 4),
                "cpu_model": cpu_model(), **cpu_topology(), "threads_used": tall}
 
-    kernels = copy_gbs = decoder = full = conv = None
+    kernels = copy_gbs = write_gbs = decoder = full = conv = None
     if not a.no_kernels:
         copy_gbs = copy_bandwidth(torch, dev)
+        write_gbs = write_bandwidth(torch, dev)
         kernels = kernel_suite(torch, gsvk, dev)
         decoder = sovits_decoder(torch, gsvk, dev)
         full = [full_decode_step(torch, gsvk, dev, kv_len=n) for n in (1024, 2048)]
@@ -1100,6 +1137,7 @@ def main():
         "whole_decode_step": whole,
         "per_op": per_op,
         "copy_GBps": copy_gbs,
+        "write_only_GBps": write_gbs,
         "kernels": kernels,
         "sovits_decoder": decoder,
         "t2s_whole_decode_step": full,

@@ -166,6 +166,29 @@ def test_embed_large_bit_exact(rows):
     assert_bitexact(out_dt, host(OUT, out_dt), want, "large embed")
 
 
+def test_embed_many_rows_int32_ids_bf16_out_partial_lanes():
+    """The many-rows-per-wave path (>= 8192 rows) with int32 ids, a bf16 output, an fp32 table and
+    D = 200 (25 chunks: lanes past the row end idle), rows not a multiple of the 32 rows a wave
+    owns, and invalid ids / positions inside a wave's group."""
+    r = rng(43)
+    D, rows = 200, 9001
+    pe = gsvk.pe_table(2048, D)
+    tab = randn(r, (1025, D), 0.02)
+    ids = r.integers(0, 1025, rows).astype(np.int32)
+    pos = r.integers(0, 2048, rows).astype(np.int64)
+    ids[[0, 31, 8999]] = [1025, -7, 4000]
+    pos[[32, 9000]] = [-1, 2048]
+    want, bad = O.embed_pe(BF16, F32, tab, ids, pe, 1.3, pos=pos)
+    assert bad == 5
+    OUT = torch.empty((rows, D), dtype=torch.bfloat16, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    gsvk.embed_pe(devf(tab), torch.from_numpy(ids).cuda(), devf(pe), 1.3, OUT,
+                  pos=torch.from_numpy(pos).cuda(), err=err)
+    sync()
+    assert int(err.item()) == 1
+    assert_bitexact(BF16, host(OUT, BF16), want, "many-rows embed, int32 ids")
+
+
 def test_embed_long_call_rows_split_by_position():
     """Calls past 256 MiB of output (the non-temporal path): every row written once, bit for bit,
     including text rows (mm + bias), invalid ids / positions (NaN rows and the error flag) and
