@@ -238,6 +238,36 @@ __device__ __forceinline__ double block_sum(float v, double* red) {
   return t;
 }
 
+// ---- GroupNorm with one channel per 512-thread workgroup, the row resident in registers ----------
+// For rows of up to 512 * 16 chunks (32768 fp32 / 65536 16-bit elements): every workgroup loads
+// its whole channel row with all 16-byte loads in flight, reduces, and writes it back normalized,
+// two workgroups per CU. With as many workgroups as channels the hardware dispatcher starts the
+// next channel on a CU as soon as one finishes, so no in-kernel pipeline is needed, and at the
+// configuration's [512, 31999] every channel is resident at once: the call is one read of the
+// tensor, the reductions, and one write.
+constexpr int kGrBlock = 512;
+constexpr int kGrWaves = kGrBlock / kWave;
+
+// Workgroup barrier that orders LDS only (__syncthreads() would also wait for the thread's
+// outstanding global stores and loads).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ double block_sum512(float v, double* red) {
+  const float w_sum = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = static_cast<double>(w_sum);
+  lds_barrier();
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kGrWaves; ++i) t += red[i];
+  lds_barrier();
+  return t;
+}
+
 // A channel row as this thread sees it: head elements up to the first 128-byte boundary, nbody
 // 16-byte chunks (thread t owns chunks t, t + 1024, ...), then fewer than one chunk of tail
 // elements. Thread t also owns head element t (t < head) or tail element t - head (head <= t <
@@ -383,6 +413,96 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
   }
 }
 
+// One channel per workgroup. The row layout is gn_row's (head to the first 128-byte line, 16-byte
+// body chunks, tail), for 512 threads: thread t owns body chunks t, t + 512, ... and head / tail
+// element t. Chunks past the body load the body's last chunk and count as zero (every load is
+// unconditional, so all of them are in flight together). The statistics are gn_gelu_vec's: fp32
+// partial sums, wave sums in fp32, the block sum in double, the centred second moment corrected by
+// the fp32 mean's offset. Launch bounds of four waves per SIMD (at most 128 VGPRs) keep a second
+// channel resident on every CU.
+template <int DT, int CPT, bool NT>
+__global__ __launch_bounds__(kGrBlock, 4) void gn_gelu_row(GnArgs a) {
+  using S = Store<DT>;
+  constexpr int V = S::VEC;
+  constexpr int ESZ = DT == GSVK_F32 ? 4 : 2;
+  __shared__ double red[kGrWaves];
+  const long ch = blockIdx.x;
+  const size_t base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x) + base * ESZ;
+  long head = static_cast<long>(((128u - (addr & 127u)) & 127u) / ESZ);
+  if (head > a.T) head = a.T;
+  const long nbody = (a.T - head) / V;
+  const long tail = a.T - head - nbody * V;
+  const size_t body0 = base + head;
+  const int t = threadIdx.x;
+  const long e_idx = t < head ? t : (t < head + tail ? head + nbody * V + (t - head) : -1);
+  const char* xb = static_cast<const char*>(a.x) + body0 * ESZ;
+  const float g = *(a.gamma ? a.gamma + ch : kOnes8);
+  const float b = *(a.beta ? a.beta + ch : kZeros8);
+  u32x4 raw[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGrBlock;
+    raw[c] = ld16<NT>(xb + static_cast<size_t>(k < nbody ? k : nbody - 1) * 16);
+  }
+  const float e_raw = S::load1(a.x, base + (e_idx >= 0 ? e_idx : 0));
+  const float e = e_idx >= 0 ? e_raw : 0.f;
+  float s = e;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGrBlock;
+    float v[V];
+    S::unpack(raw[c], v);
+    float cs = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) cs += v[i];
+    s += k < nbody ? cs : 0.f;
+  }
+  const double mean_d = block_sum512(s, red) / static_cast<double>(a.T);
+  const float mean = static_cast<float>(mean_d);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGrBlock;
+    float v[V];
+    S::unpack(raw[c], v);
+    float cq = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float d = v[i] - mean;
+      cq = __builtin_fmaf(d, d, cq);
+    }
+    q += k < nbody ? cq : 0.f;
+  }
+  if (e_idx >= 0) {
+    const float d = e - mean;
+    q = __builtin_fmaf(d, d, q);
+  }
+  const double dm = mean_d - static_cast<double>(mean);
+  const double var = block_sum512(q, red) / static_cast<double>(a.T) - dm * dm;
+  const float rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
+  // Every thread has read all of its elements before any thread writes (the reductions above end
+  // in workgroup barriers), so y == x in place is safe.
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const long k = t + static_cast<long>(c) * kGrBlock;
+    if (k < nbody) {
+      float v[V], o[V];
+      S::unpack(raw[c], v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float y = __builtin_fmaf((v[i] - mean) * rstd, g, b);
+        o[i] = a.gelu ? gelu_erf(y) : y;
+      }
+      S::template store<NT>(a.y, body0 + static_cast<size_t>(k) * V, o);
+    }
+  }
+  if (e_idx >= 0) {
+    const float y = __builtin_fmaf((e - mean) * rstd, g, b);
+    S::store1(a.y, base + e_idx, a.gelu ? gelu_erf(y) : y);
+  }
+}
+
 // Any T / alignment: three strided sweeps over the channel row.
 template <int DT>
 __global__ __launch_bounds__(kGnBlock) void gn_gelu_generic(GnArgs a) {
@@ -510,9 +630,31 @@ bool launch_gn_vec(const GnArgs& a, hipStream_t st) {
   return false;
 }
 
+template <int DT, bool NT>
+void launch_gn_row(const GnArgs& a, long nb, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(a.channels));
+  if (nb <= 4L * kGrBlock)
+    hipLaunchKernelGGL((gn_gelu_row<DT, 4, NT>), grid, dim3(kGrBlock), 0, st, a);
+  else if (DT != GSVK_F32 || nb <= 8L * kGrBlock)
+    hipLaunchKernelGGL((gn_gelu_row<DT, 8, NT>), grid, dim3(kGrBlock), 0, st, a);
+  else if constexpr (DT == GSVK_F32)
+    hipLaunchKernelGGL((gn_gelu_row<DT, 16, NT>), grid, dim3(kGrBlock), 0, st, a);
+}
+
 template <int DT>
 int launch_gn(const GnArgs& a, bool vec_ok, hipStream_t st) {
-  const size_t bytes = 2 * static_cast<size_t>(a.channels) * a.T * (DT == GSVK_F32 ? 4 : 2);
+  constexpr long kEsz = DT == GSVK_F32 ? 4 : 2;
+  constexpr int V = Store<DT>::VEC;
+  const size_t bytes = 2 * static_cast<size_t>(a.channels) * a.T * kEsz;
+  const long nb = a.T / V + 1;  // upper bound on body chunks
+  // The resident-row kernel: rows of at least two 128-byte lines (its clamped loads need one whole
+  // body chunk) and at most 16 chunks per thread for fp32, 8 for 16-bit types (32768 elements;
+  // 16 chunks of packed 16-bit values do not fit 128 VGPRs with their fp32 temporaries).
+  if (vec_ok && a.T >= 2 * (128 / kEsz) && nb <= (DT == GSVK_F32 ? 16L : 8L) * kGrBlock) {
+    if (bytes >= kStreamBytes) launch_gn_row<DT, true>(a, nb, st);
+    else launch_gn_row<DT, false>(a, nb, st);
+    return launch_status();
+  }
   if (vec_ok) vec_ok = bytes >= kStreamBytes ? launch_gn_vec<DT, true>(a, st) : launch_gn_vec<DT, false>(a, st);
   if (!vec_ok)
     hipLaunchKernelGGL((gn_gelu_generic<DT>), dim3(static_cast<unsigned>(a.channels)), dim3(kGnBlock), 0, st, a);

@@ -230,7 +230,11 @@ def test_groupnorm_gelu_config4_matches_oracle(dt):
 
 @pytest.mark.parametrize("C,T,dt,gelu", [(7, 1, F32, True), (5, 3, F32, False), (3, 1000, BF16, True),
                                          (4, 65537, F32, True), (3, 100001, F16, True),
-                                         (6, 4097, F16, False)])
+                                         (6, 4097, F16, False),
+                                         # the shortest rows of the register path (two 128-byte
+                                         # lines) and the longest that take the generic one
+                                         (9, 64, F32, True), (5, 63, F32, True),
+                                         (4, 128, F16, True), (3, 127, BF16, False)])
 def test_groupnorm_edge_shapes(C, T, dt, gelu):
     say(f"groupnorm C={C} T={T} dt={dt}")
     r = rng(C * T)
