@@ -33,23 +33,32 @@ extern "C" const char* gsvk_status_string(int status) {
   }
 }
 
-// T2SEngine::pe_row (t2s_engine.cpp:711-720) for every position 0..max_pos-1. The steps are kept
-// as the reference writes them because the table values define the bit-exact gather output:
-// a float log increment, float exp of float(d)*log_inc, and float sin/cos of float(pos)*div.
+// T2SEngine::pe_row (t2s_engine.cpp:711-720) for one position. The steps are kept as the
+// reference writes them because the table values define the bit-exact gather output: a float log
+// increment, float exp of float(d)*log_inc, and float sin/cos of float(pos)*div.
+static void pe_row_into(float* row, size_t pos, size_t D) {
+  const float log_inc = static_cast<float>(-std::log(10000.0) / static_cast<double>(D));
+  const float p = static_cast<float>(pos);
+  for (size_t d = 0; d < D; d += 2) {
+    const float div = std::exp(static_cast<float>(d) * log_inc);
+    const float ang = p * div;
+    row[d] = std::sin(ang);
+    row[d + 1] = std::cos(ang);
+  }
+}
+
 extern "C" int gsvk_pe_table(float* host_out, size_t max_pos, size_t D) {
   if (!host_out) return GSVK_E_NULL;
   if (max_pos == 0 || D == 0 || max_pos > (1ul << 32) || D > (1ul << 24)) return GSVK_E_SIZE;
   if (D % 2) return GSVK_E_ARG;
-  const float log_inc = static_cast<float>(-std::log(10000.0) / static_cast<double>(D));
-  for (size_t pos = 0; pos < max_pos; ++pos) {
-    float* row = host_out + pos * D;
-    const float p = static_cast<float>(pos);
-    for (size_t d = 0; d < D; d += 2) {
-      const float div = std::exp(static_cast<float>(d) * log_inc);
-      const float ang = p * div;
-      row[d] = std::sin(ang);
-      row[d + 1] = std::cos(ang);
-    }
-  }
+  for (size_t pos = 0; pos < max_pos; ++pos) pe_row_into(host_out + pos * D, pos, D);
+  return GSVK_OK;
+}
+
+extern "C" int gsvk_pe_row(float* host_out, size_t pos, size_t D) {
+  if (!host_out) return GSVK_E_NULL;
+  if (D == 0 || D > (1ul << 24) || pos > (1ul << 32)) return GSVK_E_SIZE;
+  if (D % 2) return GSVK_E_ARG;
+  pe_row_into(host_out, pos, D);
   return GSVK_OK;
 }

@@ -55,6 +55,7 @@ SIGNATURES = {
     "gsvk_embed_pe": (_i, [_i, _i, _i, _vp, _sz, _vp, _vp, _i64, _vp, _sz, _f, _vp, _vp, _vp, _sz,
                            _sz, _vp, _vp]),
     "gsvk_pe_table": (_i, [_vp, _sz, _sz]),
+    "gsvk_pe_row": (_i, [_vp, _sz, _sz]),
     "gsvk_t2s_step_eager": (_i, [_vp, _vp]),
     "gsvk_t2s_step_create": (_i, [_vp, ctypes.POINTER(_vp)]),
     "gsvk_t2s_step_run": (_i, [_vp, _vp]),

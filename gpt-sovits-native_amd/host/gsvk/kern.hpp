@@ -8,6 +8,10 @@
 //   gsv::sovits::leaky_relu_io / leaky_relu_write / add_inplace / add_scaled_inplace / mul_write
 //                                                    (src/sovits/nn_ops.hpp:48-105)
 //   gsv::bert::gelu_erf over a buffer                (src/bert/bert_ops.hpp:25-27, 394)
+//   gsv::bert::Matrix / LayerNorm1D::forward(Matrix&) (src/bert/bert_io.hpp:18-27,
+//                                                     bert_ops.hpp:261-286), device storage
+//   gsv::sovits::Tensor2D                            (src/sovits/sovits_types.hpp:21-36)
+//   gsv::ar::PeRows::pe_row(float*, size_t)          (src/ar/t2s_engine.hpp:187)
 //   gsv::sovits::Conv1d / ConvT1d, device-resident   (src/sovits/conv1d.hpp:56-360)
 // Differences, all deliberate: pointers are device pointers; every call is enqueued on the calling
 // thread's current stream (gsvk::set_stream) and returns before the GPU finishes (call
@@ -43,6 +47,73 @@ inline void sync() {
   if (hipStreamSynchronize(current_stream()) != hipSuccess)
     throw std::runtime_error("gsvk::sync: hipStreamSynchronize failed");
 }
+
+// Owning device buffer with the parts of std::vector the reference's containers use (data(),
+// size(), assign(n, 0)), so their call sites (`f(x.d.data(), x.d.size(), ...)`) compile unchanged
+// with device storage. Allocation happens in resize / assign, as the reference allocates in its
+// containers' reset / load; the kernels themselves allocate nothing.
+template <class T>
+class DeviceVector {
+ public:
+  DeviceVector() = default;
+  explicit DeviceVector(size_t n) { resize(n); }
+  DeviceVector(const DeviceVector&) = delete;
+  DeviceVector& operator=(const DeviceVector&) = delete;
+  DeviceVector(DeviceVector&& o) noexcept : p_(o.p_), n_(o.n_), cap_(o.cap_) {
+    o.p_ = nullptr;
+    o.n_ = o.cap_ = 0;
+  }
+  DeviceVector& operator=(DeviceVector&& o) noexcept {
+    if (this != &o) {
+      release();
+      p_ = o.p_, n_ = o.n_, cap_ = o.cap_;
+      o.p_ = nullptr;
+      o.n_ = o.cap_ = 0;
+    }
+    return *this;
+  }
+  ~DeviceVector() { release(); }
+
+  // n elements; the contents are unspecified after a reallocation.
+  void resize(size_t n) {
+    if (n > cap_) {
+      release();
+      if (hipMalloc(reinterpret_cast<void**>(&p_), n * sizeof(T)) != hipSuccess)
+        throw std::runtime_error("gsvk::DeviceVector: hipMalloc failed");
+      cap_ = n;
+    }
+    n_ = n;
+  }
+  // n zero elements (std::vector::assign(n, 0) of the reference's reset()).
+  void assign(size_t n, T zero) {
+    if (zero != T(0)) throw std::runtime_error("gsvk::DeviceVector::assign: only zero fill");
+    resize(n);
+    if (n && hipMemsetAsync(p_, 0, n * sizeof(T), current_stream()) != hipSuccess)
+      throw std::runtime_error("gsvk::DeviceVector::assign: hipMemsetAsync failed");
+  }
+  void copy_from_host(const T* host, size_t n) {
+    resize(n);
+    if (n && hipMemcpy(p_, host, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+      throw std::runtime_error("gsvk::DeviceVector: host-to-device copy failed");
+  }
+  void copy_to_host(T* host) const {
+    if (n_ && hipMemcpy(host, p_, n_ * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+      throw std::runtime_error("gsvk::DeviceVector: device-to-host copy failed");
+  }
+  T* data() { return p_; }
+  const T* data() const { return p_; }
+  size_t size() const { return n_; }
+  bool empty() const { return n_ == 0; }
+
+ private:
+  void release() {
+    if (p_) (void)hipFree(p_);
+    p_ = nullptr;
+    n_ = cap_ = 0;
+  }
+  T* p_ = nullptr;
+  size_t n_ = 0, cap_ = 0;
+};
 
 }  // namespace gsvk
 
@@ -146,6 +217,40 @@ inline void layernorm1d_forward(float* x, const float* g, const float* bta, size
               "gsv::bert::layernorm1d_forward");
 }
 
+// bert::Matrix (bert_io.hpp:18-27) with the same members over device storage: row-major
+// [rows = T, cols = C], d.data() a device pointer.
+struct Matrix {
+  size_t rows = 0, cols = 0;
+  gsvk::DeviceVector<float> d;
+  void reset(size_t r, size_t c) {
+    rows = r;
+    cols = c;
+    d.assign(r * c, 0.f);
+  }
+  size_t size() const { return d.size(); }
+};
+
+// bert::LayerNorm1D (bert_ops.hpp:261-286): members g, bta, eps; forward(Matrix&) in place, one
+// launch for all rows. load() takes the host vectors the reference's load() reads from the .gsv
+// file (weight, bias of length c).
+struct LayerNorm1D {
+  gsvk::DeviceVector<float> g, bta;
+  float eps = 1e-12f;
+  void load(const float* weight, const float* bias, size_t c, float e) {
+    eps = e;
+    g.copy_from_host(weight, c);
+    bta.copy_from_host(bias, c);
+  }
+  void forward(Matrix& x) const {
+    if (g.size() != x.cols || bta.size() != x.cols)
+      throw std::runtime_error("gsv::bert::LayerNorm1D::forward: width mismatch");
+    layernorm1d_forward(x.d.data(), g.data(), bta.data(), x.rows, x.cols, eps);
+  }
+};
+
+// The scalar gelu_erf(float) (bert_ops.hpp:25-27) is called inside host loops over host floats;
+// on the GPU its loops become bias_gelu_erf over a device buffer (one launch per tensor).
+
 }  // namespace gsv::bert
 
 namespace gsv::encoder {
@@ -167,6 +272,24 @@ inline void gelu(float* x, size_t n) {
 }  // namespace gsv::encoder
 
 namespace gsv::sovits {
+
+// sovits::Tensor2D (sovits_types.hpp:21-36) with the same members over device storage: [C, T]
+// rows contiguous, d.data() / row(c) device pointers.
+struct Tensor2D {
+  size_t C = 0, T = 0;
+  gsvk::DeviceVector<float> d;
+
+  Tensor2D() = default;
+  Tensor2D(size_t c, size_t t) { reset(c, t); }
+
+  void reset(size_t c, size_t t) {
+    C = c;
+    T = t;
+    d.assign(c * t, 0.f);
+  }
+  float* row(size_t c) { return d.data() + c * T; }
+  const float* row(size_t c) const { return d.data() + c * T; }
+};
 
 inline void leaky_relu_io(float* io, size_t n, float slope) {
   gsvk::check(gsvk_leaky_relu(GSVK_F32, io, io, n, slope, gsvk::current_stream()),
@@ -290,6 +413,16 @@ namespace gsv::ar {
 inline void pe_table(float* host_out, size_t max_pos, size_t d_model) {
   gsvk::check(gsvk_pe_table(host_out, max_pos, d_model), "gsv::ar::pe_table");
 }
+
+// T2SEngine::pe_row(float* pe, size_t pos) (t2s_engine.hpp:187) as a member of anything that
+// knows d_model: an engine holding (or deriving from) this keeps its pe_row(pe, pos) call sites.
+// Host memory: the rows feed gsvk_embed_pe through a table uploaded once.
+struct PeRows {
+  size_t d_model = 0;
+  void pe_row(float* pe, size_t pos) const {
+    gsvk::check(gsvk_pe_row(pe, pos, d_model), "gsv::ar::PeRows::pe_row");
+  }
+};
 
 // x[r] = e[id_r] + alpha * pe[pos_r] over B rows (t2s_engine.cpp:1781-1786, 1866-1869).
 inline void embed_pe(const uint16_t* table_f16, size_t vocab, const int64_t* ids,

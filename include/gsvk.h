@@ -348,6 +348,9 @@ int gsvk_embed_pe(int out_dtype, int table_dtype, int index_type, const void* ta
  *   pe[2i+1] = cosf(p*div), all in fp32. host_out holds max_pos * D floats. Host memory, no GPU.
  * ------------------------------------------------------------------------------------------------ */
 int gsvk_pe_table(float* host_out, size_t max_pos, size_t D);
+/* One row of it: T2SEngine::pe_row(pe, pos) (t2s_engine.hpp:187) for a model of width D, into
+ * host_out[0 .. D). The same values as row `pos` of gsvk_pe_table. Host memory, no GPU. */
+int gsvk_pe_row(float* host_out, size_t pos, size_t D);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,14 @@ def test_pe_table_host_builder_matches_oracle_bitwise(gsvk_lib):
     got = gsvk.pe_table(2048, 512)
     want = O.pe_table(2048, 512)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # gsvk_pe_row (T2SEngine::pe_row's one-row form) gives the table's rows
+    row = np.empty(512, np.float32)
+    for p in (0, 1, 7, 166, 1234, 2047, 100000):
+        assert gsvk_lib.gsvk_pe_row(row.ctypes.data, p, 512) == gsvk.OK
+        assert np.array_equal(row.view(np.uint32), O.pe_row(p, 512).view(np.uint32)), p
+    assert gsvk_lib.gsvk_pe_row(None, 3, 512) == gsvk.E_NULL
+    assert gsvk_lib.gsvk_pe_row(row.ctypes.data, 3, 511) == gsvk.E_ARG
+    assert gsvk_lib.gsvk_pe_row(row.ctypes.data, 3, 0) == gsvk.E_SIZE
     assert gsvk_lib.gsvk_pe_table(None, 4, 4) == gsvk.E_NULL
     buf = np.empty(12, np.float32)
     assert gsvk_lib.gsvk_pe_table(buf.ctypes.data, 4, 3) == gsvk.E_ARG  # odd D
