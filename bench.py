@@ -575,7 +575,7 @@ def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_F16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(ach / PEAK_F16_TFLOPS, 4),
                          "flops": flops_tot,
-                         "note": "algorithmic flops; exact fp32 runs two fp16 products per term"}}
+                         "note": "algorithmic flops; fp32 activations (hi/lo fp16 split, ~22 bits) run two fp16 products per term"}}
 
 
 def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=500):
@@ -583,7 +583,8 @@ def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=
     fused, 3 ResBlocks x 3 fused conv pairs, branch mean + next LeakyReLU; 20 launches per stage)
     timed one by one as eager launches, then the whole decoder (gsvk.SovitsDecoder: cond folded into
     conv_pre's bias, conv_pre + LeakyReLU, the 5 stages, conv_post + tanh; 104 launches) replayed as
-    one HIP graph on z [192, frames]. Exact fp32, random-init weights of the reference's shapes.
+    one HIP graph on z [192, frames]. fp32 activations (hi/lo fp16 split, ~22 bits), random-init
+    weights of the reference's shapes.
     Each figure is the median of `reps` timed runs after one warm run; 500 frames = 10 s of 32 kHz
     audio."""
     g = lambda *shape: torch.randn(*shape, device=dev)
@@ -630,7 +631,8 @@ def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=
         n_out *= u
     audio_s = n_out / 32000.0
     res = {"geometry": geometry, "stages": out, "stages_us_per_10s_audio": round(tot, 1)}
-    # exact fp32 (the reference's default numerics), fp32 with fp16-rounded convolution inputs
+    # fp32 as a hi/lo fp16 pair (the reference's default sgemm numerics to ~22 bits), fp32 with
+    # fp16-rounded convolution inputs
     # (its AMX numerics), fp16 storage
     for name, zz, rx in (("decoder", z, False), ("decoder_round_x", z, True),
                          ("decoder_f16", z.half(), False)):
@@ -842,7 +844,7 @@ def next_tier_cpu(reps=3):
             "value": round(2.0 * C * C * k * T / t_conv / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
             "kind": "port", "us": round(t_conv * 1e6, 0),
             "sample": f"a {xs.shape[1]}-column window scaled by {T / xs.shape[1]:.1f} to {T} "
-                      f"columns, exact fp32 with the LeakyReLU epilogue; median of {reps}",
+                      f"columns, fp32 (the oracle multiplies exactly) with the LeakyReLU epilogue; median of {reps}",
             "cpu_model": model},
     }
 

@@ -11,6 +11,8 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgsvk.so")
+# tests/sanitizers.sh points this at the host-sanitizer build (gpt-sovits-native_amd/_san/)
+LIB_PATH = os.environ.get("GSVK_LIB", LIB_PATH)
 
 F32, F16, BF16 = 0, 1, 2
 I64, I32 = 0, 1

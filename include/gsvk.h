@@ -209,7 +209,8 @@ int gsvk_decode_attention_noalloc(int kv_dtype, int out_dtype, const float* qkv,
  *   lrelu(cur, slope) (from the fp32 sum); RES cur = r + v (y may be NULL); DUAL y = v, cur =
  *   lrelu(v, slope); TANH y = tanhf(v). With GSVK_CONV_X_LRELU OR-ed into epi, every x value is
  *   replaced by lrelu(x, slope) as it is read (x itself unchanged; the sum then runs on that value:
- *   exact for F32, rounded to fp16 with round_x or F16 storage, as a stored lrelu(x) would be).
+ *   as an fp32 value for F32, rounded to fp16 with round_x or F16 storage, as a stored lrelu(x)
+ *   would be).
  *   For RES_LRELU / RES the residual r is read from `res`
  *   (row stride ldc) or, when res is NULL or equal to cur, from cur itself (in place): a branch's
  *   first pair can then add onto the stage input without copying it into cur first.
@@ -219,9 +220,10 @@ int gsvk_decode_attention_noalloc(int kv_dtype, int out_dtype, const float* qkv,
  * pair's leaky_relu_write).
  * Layout: channel-major [channels, T] rows with strides ldx, ldc, ldy >= T; x, cur, y of dtype
  * (F32 or F16); bias fp32 [c_out] or NULL (conv_post has none, conv1d.hpp:82-88); w_packed from
- * gsvk_conv1d_pack, 16-byte aligned. dtype F32 multiplies the fp32 activations exactly
- * (round_x = 0, the reference's sgemm path; |x| < 65504) or rounded to fp16 (round_x = 1, as the
- * reference's AMX path packs them, conv1d.hpp:130-151); F16 storage rounds each output once.
+ * gsvk_conv1d_pack, 16-byte aligned. dtype F32 keeps the fp32 activations as a hi/lo pair of fp16
+ * halves, x to about 2^-22 relative, not exactly (round_x = 0, the reference's sgemm path;
+ * |x| < 65504), or rounds them to fp16 (round_x = 1, as the reference's AMX path packs them,
+ * conv1d.hpp:130-151); F16 storage rounds each output once.
  * (k - 1) * dilation <= 256. y and cur must not overlap x, the weights, the bias or each other
  * (the reference's in-place x == y goes through a copy; here the caller keeps them apart); res may
  * equal cur but must not otherwise overlap an output.

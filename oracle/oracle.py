@@ -14,6 +14,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
+# tests/sanitizers.sh points this at the AddressSanitizer / UBSan build (oracle/_san/)
+LIB_PATH = os.environ.get("GSVK_ORACLE_LIB", LIB_PATH)
 F32, F16, BF16 = 0, 1, 2
 
 _vp, _sz, _i, _f, _d = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_double

@@ -20,6 +20,19 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
 
 
+def pytest_terminal_summary(terminalreporter):
+    """Session total of 16-bit output elements that passed only through the one-storage-step
+    clause of the parity bar (tests/gpu_util.py)."""
+    try:
+        from gpu_util import WIDENED
+    except Exception:
+        return
+    if WIDENED["elements"]:
+        terminalreporter.write_line(
+            f"16-bit parity: {WIDENED['widened']} of {WIDENED['elements']} compared elements "
+            f"passed only within one storage step (|d| > 2e-3)")
+
+
 def load_bin(name):
     """Reference fixture format `[u32 rank][u32 dims x rank][raw little-endian data]`
     (tools/export_kern_golden.py:4-6, 26-36; reader tests/test_kern.cpp:30-57)."""

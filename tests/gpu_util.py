@@ -4,7 +4,10 @@ rules. Tolerances are the ones the target states for this path:
       NaN compared as NaN;
   fp32 norms / activations: |got - want| <= 1e-6 + 1e-5 * |want|;
   fp16 storage: |got - want| <= 2e-3, or one fp16 step of `want` where that step is larger
-      (|want| >= 4, where a single rounding step is 3.9e-3);
+      (|want| >= 4, where a single rounding step is 3.9e-3; no fp16 value can be closer than half
+      a step to an arbitrary real there). The elements that need the second clause are counted
+      per call (printed, and for fp16 summed over the session by conftest) and bounded at 1% of
+      an fp16 call;
   bf16 storage: |got - want| <= 2e-3, or one bf16 step of `want` where that step is larger.
 """
 import sys
@@ -71,6 +74,14 @@ def tol(dt, w):
     return np.maximum(2e-3, step)
 
 
+# Elements of 16-bit outputs that pass only through the one-rounding-step clause (|d| > 2e-3, the
+# stated absolute bound, but within one storage step of the oracle's value, which exceeds 2e-3 only
+# where |want| >= 4): every call reports how many, and at most this fraction of a call's elements
+# may take that clause.
+WIDENED_MAX_FRACTION = 0.01
+WIDENED = {"elements": 0, "widened": 0}
+
+
 def assert_close(dt, got, want, what=""):
     g = O.to_f32(dt, got).astype(np.float64)
     w = O.to_f32(dt, want).astype(np.float64)
@@ -83,4 +94,15 @@ def assert_close(dt, got, want, what=""):
     assert bad.size == 0, f"{what}: {bad.size}/{g.size} out of tolerance, worst " \
                           f"{err.ravel()[bad].max():.3e} at {bad[:3]} got {g.ravel()[bad[:3]]} " \
                           f"want {w.ravel()[bad[:3]]}"
+    if dt != F32:
+        widened = int(np.count_nonzero(err > 2e-3))
+        if dt == F16:
+            WIDENED["elements"] += g.size
+            WIDENED["widened"] += widened
+        if widened:
+            say(f"{what}: {widened}/{g.size} elements within one storage step but above 2e-3 "
+                f"(all at |want| >= {np.abs(w.ravel()[err.ravel() > 2e-3]).min():.3g})")
+        # bf16's step exceeds 2e-3 from |want| >= 0.25 on, so the bound applies to fp16 only
+        assert dt != F16 or widened <= WIDENED_MAX_FRACTION * g.size, \
+            f"{what}: {widened}/{g.size} elements only within one storage step"
     return float(err.max()) if err.size else 0.0

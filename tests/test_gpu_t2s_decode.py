@@ -148,10 +148,11 @@ def test_decode_step_graph_equals_eager_over_steps():
         assert np.array_equal(xa, xb) and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
 
 
-def test_decode_step_t2s_shape_one_layer():
-    """B = 64, D = 512, 16 heads, FF = 2048, one layer, 1025-token vocabulary: the real shapes."""
+def test_decode_step_t2s_shape_four_layers():
+    """B = 64, D = 512, 16 heads, FF = 2048, four chained layers, 1025-token vocabulary: the real
+    shapes, with the residual path carrying each layer's differences into the next."""
     FF = 2048
-    m, io = build(B=64, D=512, H=16, FF=FF, L=1, V=1025, max_len=300, seed=3)
+    m, io = build(B=64, D=512, H=16, FF=FF, L=4, V=1025, max_len=300, seed=3)
     md, iod = to_device(m, io, FF)
     x_want, lg_want = oracle_step(m, io)
     step = gsvk.T2SDecode(md, iod, len_bound=300)
