@@ -914,6 +914,29 @@ def pmc_workload(torch, gsvk, bufs):
         f"10 x copy {PMC_COPY_BYTES} B")
 
 
+def ln_param_traffic_workload(torch, gsvk, bufs):
+    """For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`: 100 launches of residual+LN [64, 512] f16
+    with its bias / gamma / beta (6 KiB of fp32 parameters), then 100 launches of the same call
+    without them, each after a 512 MiB read that clears the MALL, and 10 copies of PMC_COPY_BYTES
+    (the counter calibration). The per-dispatch difference of the two sets is the parameter
+    vectors' share of the launch's fetched bytes."""
+    L0, _, _ = step_ops(gsvk, bufs)
+    x, h = bufs["x"], bufs["h"]
+    bare = lambda: gsvk.add_layernorm(bufs["attn_out"][0], None, None, h, 1e-5, residual=x)
+    flush = Flusher(torch, x.device)
+    for fn in (L0, bare):
+        for _ in range(100):
+            flush()
+            fn()
+    src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=x.device)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("ln param traffic workload: 100 x LN [64,512] f16 with parameters, 100 without, "
+        f"10 x copy {PMC_COPY_BYTES} B")
+
+
 def measure_traffic(timeout_s=150):
     """HBM-side traffic of one launch of the step's kernel: two `rocprofv3 --pmc` child runs of
     this script's --pmc workload (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what
@@ -971,6 +994,8 @@ def main():
     ap.add_argument("--only", default=None, help="run one kernel of the suite and exit")
     ap.add_argument("--pmc", action="store_true",
                     help="run the step kernel and a plain copy only (for rocprofv3 --pmc)")
+    ap.add_argument("--ln-traffic", action="store_true",
+                    help="LN [64,512] with and without parameters + a copy (rocprofv3 --pmc runs)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure roofline.traffic")
     ap.add_argument("--conv", action="store_true",
@@ -1015,6 +1040,9 @@ def main():
     bufs = make_step_buffers(torch, gsvk, dev)
     if a.pmc:
         pmc_workload(torch, gsvk, bufs)
+        return
+    if a.ln_traffic:
+        ln_param_traffic_workload(torch, gsvk, bufs)
         return
     nbytes = step_bytes()
 
