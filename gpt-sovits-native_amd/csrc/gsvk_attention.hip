@@ -30,6 +30,12 @@ constexpr int kAttnWaves = 4;
 constexpr int kKeysPerGroup = GSVK_ATTN_KPG;  // keys per wave per pipeline step
 constexpr int kDepth = GSVK_ATTN_DEPTH;        // groups of loads in flight per wave
 constexpr int kMaxChunks = 16;
+// A call whose cache rows (K and V) reach this size reads them with the non-temporal hint. Across
+// a decode step the layers' caches stream through the 256 MB MALL once each, so at this size per
+// layer (24 layers: > 384 MB) nothing read this way is found there again; the hint keeps the MALL for
+// the weights and activations that are. Measured on the whole T2S decode step (B = 64, 1024 keys,
+// 134 MB per layer): 1198 -> 1122 us.
+constexpr size_t kAttnStreamBytes = 16ul << 20;
 
 struct AttnArgs {
   const float* qkv;  // [B, ldq]: q | k | v, fp32
@@ -109,7 +115,7 @@ __device__ __forceinline__ float exp_rel(float a, float b) {
   return a == -INFINITY ? 0.f : __expf(a - b);
 }
 
-template <int KVT, int OUTT>
+template <int KVT, int OUTT, bool NT>
 __global__ __launch_bounds__(kWave * kAttnWaves) void attn_chunk(AttnArgs a) {
   __shared__ float st_m[kAttnWaves][kWave], st_l[kAttnWaves][kWave];
   __shared__ float st_o[kAttnWaves][8][kWave];
@@ -159,8 +165,8 @@ __global__ __launch_bounds__(kWave * kAttnWaves) void attn_chunk(AttnArgs a) {
       const size_t byte = (seq + static_cast<size_t>(min(key_of(g, u), k1 - 1)) * D + col) * kEsz;
 #pragma unroll
       for (int w = 0; w < KeyGroup<KVT>::W; ++w) {
-        f.k[u][w] = ld16<false>(static_cast<const char*>(a.kc) + byte + 16 * w);
-        f.v[u][w] = ld16<false>(static_cast<const char*>(a.vc) + byte + 16 * w);
+        f.k[u][w] = ld16<NT>(static_cast<const char*>(a.kc) + byte + 16 * w);
+        f.v[u][w] = ld16<NT>(static_cast<const char*>(a.vc) + byte + 16 * w);
       }
     }
   };
@@ -320,20 +326,23 @@ int chunks_for(size_t batch, size_t len_bound) {
 }
 
 template <int KVT, int OUTT>
-void launch_attn(const AttnArgs& a, size_t B, int C, hipStream_t st) {
-  hipLaunchKernelGGL((attn_chunk<KVT, OUTT>), dim3(C, static_cast<unsigned>(B)),
-                     dim3(kWave * kAttnWaves), 0, st, a);
+void launch_attn(const AttnArgs& a, size_t B, int C, bool nt, hipStream_t st) {
+  const dim3 grid(C, static_cast<unsigned>(B));
+  if (nt)
+    hipLaunchKernelGGL((attn_chunk<KVT, OUTT, true>), grid, dim3(kWave * kAttnWaves), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_chunk<KVT, OUTT, false>), grid, dim3(kWave * kAttnWaves), 0, st, a);
   if (C > 1)
     hipLaunchKernelGGL((attn_merge<OUTT>), dim3(static_cast<unsigned>(B)), dim3(kWave * C), 0, st,
                        a, C);
 }
 
 template <int KVT>
-void launch_out(int outt, const AttnArgs& a, size_t B, int C, hipStream_t st) {
+void launch_out(int outt, const AttnArgs& a, size_t B, int C, bool nt, hipStream_t st) {
   switch (outt) {
-    case GSVK_F32: return launch_attn<KVT, GSVK_F32>(a, B, C, st);
-    case GSVK_F16: return launch_attn<KVT, GSVK_F16>(a, B, C, st);
-    default: return launch_attn<KVT, GSVK_BF16>(a, B, C, st);
+    case GSVK_F32: return launch_attn<KVT, GSVK_F32>(a, B, C, nt, st);
+    case GSVK_F16: return launch_attn<KVT, GSVK_F16>(a, B, C, nt, st);
+    default: return launch_attn<KVT, GSVK_BF16>(a, B, C, nt, st);
   }
 }
 
@@ -397,10 +406,13 @@ __attribute__((visibility("hidden"))) int attention_call(
              static_cast<long>(D), static_cast<long>(head_dim),
              1.0f / std::sqrt(static_cast<float>(head_dim))};
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // cache rows this call reads: K and V of up to len_bound (else max_len) keys per sequence
+  const size_t keys = len_bound ? std::min(len_bound, max_len) : max_len;
+  const bool nt = 2 * batch * keys * D * esz >= kAttnStreamBytes;
   switch (kv_dtype) {
-    case GSVK_F32: launch_out<GSVK_F32>(out_dtype, a, batch, C, st); break;
-    case GSVK_F16: launch_out<GSVK_F16>(out_dtype, a, batch, C, st); break;
-    default: launch_out<GSVK_BF16>(out_dtype, a, batch, C, st); break;
+    case GSVK_F32: launch_out<GSVK_F32>(out_dtype, a, batch, C, nt, st); break;
+    case GSVK_F16: launch_out<GSVK_F16>(out_dtype, a, batch, C, nt, st); break;
+    default: launch_out<GSVK_BF16>(out_dtype, a, batch, C, nt, st); break;
   }
   return launch_status();
 }
