@@ -161,8 +161,10 @@ struct Store<GSVK_BF16> : Store16<GSVK_BF16> {};
 // keeps one request in flight instead of all of them. So out-of-range indices are clamped to a
 // valid element (the value is discarded) and only stores are guarded, and an absent parameter
 // vector reads one of these constant rows instead of being skipped.
-static __device__ float kZeros8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-static __device__ float kOnes8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+static __device__ __attribute__((aligned(16))) float kZeros8[8] = {0.f, 0.f, 0.f, 0.f,
+                                                                    0.f, 0.f, 0.f, 0.f};
+static __device__ __attribute__((aligned(16))) float kOnes8[8] = {1.f, 1.f, 1.f, 1.f,
+                                                                   1.f, 1.f, 1.f, 1.f};
 
 // Address of the 8-float parameter chunk starting at element i, or of a constant row when the
 // vector is absent.
@@ -233,6 +235,14 @@ template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_rows_f32(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
                                                                ROW_MASK, 0xf, false));
+}
+
+// Workgroup barrier that orders LDS only (__syncthreads() would also wait for the thread's
+// outstanding global stores and loads).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -112,6 +112,70 @@ __device__ __forceinline__ EpiIn epi_load(const GvArgs& a, long m, long n) {
   return e;
 }
 
+// The streaming kernel's form of the same operands, as loaded: 4 in-range columns n .. n+3
+// (n % 4 == 0) of an in-range row, one 16-byte bias load and one residual load of 4 elements (the
+// host has checked that bias, residual and the row stride keep them aligned). They stay raw until
+// the store: converting them right after the load would make the wave wait for it there.
+struct EpiRaw {
+  u32x4 b;
+  u32x4 r;  // 4 fp32, or 4 16-bit values in the low two words
+};
+
+template <int YDT>
+__device__ __forceinline__ EpiRaw epi_load_raw(const GvArgs& a, long m, long n) {
+  EpiRaw e;
+  e.b = ld16<false>(a.bias ? a.bias + n : kZeros8);
+  if constexpr (YDT == GSVK_F32) {
+    e.r = ld16<false>(a.res ? static_cast<const float*>(a.res) + static_cast<size_t>(m) * a.ldy + n
+                            : kZeros8);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(
+        a.res ? static_cast<const uint16_t*>(a.res) + static_cast<size_t>(m) * a.ldy + n
+              : reinterpret_cast<const uint16_t*>(kZeros8));
+    e.r = u32x4{v.x, v.y, 0u, 0u};
+  }
+  return e;
+}
+
+// Four outputs of the streaming kernel: act(s + b) + r with the activation fixed at compile time,
+// stored as one vector when the row and the 4 columns are in range (N % 4 == 0). An absent bias or
+// residual is -0, which added leaves every value as it is (-0 included): no branch.
+template <int YDT, int ACT>
+__device__ __forceinline__ void finish4s(const GvArgs& a, long m, long n, f4v s, const EpiRaw& e,
+                                         bool live) {
+  float b[4], r[4];
+  const f4v bf = __builtin_bit_cast(f4v, e.b);
+  if constexpr (YDT == GSVK_F32) {
+    const f4v rf = __builtin_bit_cast(f4v, e.r);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r[q] = rf[q];
+  } else {
+    const uint32_t h[4] = {e.r[0] & 0xffffu, e.r[0] >> 16, e.r[1] & 0xffffu, e.r[1] >> 16};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r[q] = YDT == GSVK_F16 ? h2f(h[q]) : bf2f(h[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    b[q] = a.bias ? bf[q] : -0.f;
+    r[q] = a.res ? r[q] : -0.f;
+  }
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = act_apply<ACT>(s[q] + b[q], a.slope) + r[q];
+  if (live && m < a.M && n < a.N) {
+    const size_t off = static_cast<size_t>(m) * a.ldy + n;
+    if constexpr (YDT == GSVK_F32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(a.y) + off) = float4{v[0], v[1], v[2], v[3]};
+    } else {
+      uint32_t h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h[q] = YDT == GSVK_F16 ? f2h(v[q]) : f2bf(v[q]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + off) =
+          uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    }
+  }
+}
+
 // v = act(acc + bias[n]) (+ residual[m, n]). The bias add is skipped, not replaced by + 0, when
 // there is no bias (x + 0 would turn -0 into +0); likewise the residual add.
 __device__ __forceinline__ float epilogue(const GvArgs& a, float v, float b, float r) {
@@ -526,6 +590,187 @@ __global__ __launch_bounds__(256) void gemv_generic(GvArgs a) {
   }
 }
 
+// ---- long weight streams -------------------------------------------------------------------------
+//
+// A weight stream far larger than the launch's CUs can cover in one round of tiles (many thousands of
+// 16-column tiles at up to 64 rows) runs on persistent workgroups instead. Each wave owns a fixed
+// k slice (KB blocks of 64) and keeps the workgroup's activations of that slice in registers for the
+// whole launch, loaded once; the workgroup then walks column batches (NT tiles of 16 columns)
+// blockIdx.x, + gridDim.x, ... with D batches of weight loads in flight per wave. A lane reads
+// its weight fragments straight from global memory: for k block b and MFMA half h, lane (column c,
+// lane group g) takes the 16 bytes at k = 64 b + 16 g + 8 h of column c, the k assignment of the
+// tiled kernel above, so a batch needs no staging. The waves' partial sums meet in LDS (double
+// buffered, one barrier per batch) and are added in wave order, as in the tiled kernel: for a k
+// slice of 128 per wave (KB = 2) the two kernels give the same bits.
+//
+// The epilogue operands of a batch (bias, residual) travel in its load slot, so no wave waits for a
+// load issued after the weights it is about to use.
+template <int XM, int MF, int KB>
+struct StreamX {
+  h8 hi[MF][2 * KB];
+  h8 lo[XM == kXSplit ? MF : 1][XM == kXSplit ? 2 * KB : 1];
+};
+
+template <int MF, int NT, int KB, int FPW>
+struct StreamSlot {
+  u32x4 w[NT][2 * KB];  // tile t, k block b, half h at [t][2 b + h]
+  EpiRaw e[NT][FPW];    // epilogue operands of the row fragments this wave finishes
+};
+
+template <int XM, int YDT, int ACT, int MF, int KB, int WK, int NT, int D>
+__global__ __launch_bounds__(kWave * WK) void gemv_stream(GvArgs a) {
+  constexpr int FPW = (MF + WK - 1) / WK;  // row fragments each wave finishes per tile
+  constexpr int kRed = WK > 1 ? 2 * WK * NT * MF * kWave : 1;
+  __shared__ f4v red[kRed];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int r16 = lane & 15, grp = lane >> 4;
+  const long m0 = static_cast<long>(blockIdx.y) * (16 * MF);
+  const long kw = static_cast<long>(wave) * (64 * KB);  // first k of this wave's slice
+  const long nb = (a.N + 16 * NT - 1) / (16 * NT);     // column batches
+
+  // Activations of the slice, once: lane (row r16, group grp), block b, half h holds k =
+  // kw + 64 b + 16 grp + 8 h .. +7 of row m0 + 16 i + r16 (clamped: rows past M are never stored).
+  StreamX<XM, MF, KB> xf;
+#pragma unroll
+  for (int i = 0; i < MF; ++i) {
+    const size_t row = static_cast<size_t>(min(m0 + 16 * i + r16, a.M - 1)) * a.ldx;
+#pragma unroll
+    for (int q = 0; q < 2 * KB; ++q) {
+      const size_t k = static_cast<size_t>(kw + 64 * (q >> 1) + 16 * grp + 8 * (q & 1));
+      if constexpr (XM == kXF16) {
+        xf.hi[i][q] = __builtin_bit_cast(h8, ld16<false>(static_cast<const uint16_t*>(a.x) + row + k));
+      } else {
+        const float* xp = static_cast<const float*>(a.x) + row + k;
+        const f4v f0 = __builtin_bit_cast(f4v, ld16<false>(xp));
+        const f4v f1 = __builtin_bit_cast(f4v, ld16<false>(xp + 4));
+        const h4 h0 = __builtin_convertvector(f0, h4), h1 = __builtin_convertvector(f1, h4);
+        xf.hi[i][q] = h8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+        if constexpr (XM == kXSplit) {
+          const h4 l0 = __builtin_convertvector(f0 - __builtin_convertvector(h0, f4v), h4);
+          const h4 l1 = __builtin_convertvector(f1 - __builtin_convertvector(h1, f4v), h4);
+          xf.lo[i][q] = h8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+        }
+      }
+    }
+  }
+
+  // The loop never waits for the activations: their loads go out first and are waited for here,
+  // behind nothing else (a wait inside the loop would also wait for every weight load in flight).
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int q = 0; q < 2 * KB; ++q) {
+      asm volatile("" ::"v"(xf.hi[i][q]));
+      if constexpr (XM == kXSplit) asm volatile("" ::"v"(xf.lo[i][q]));
+    }
+
+  // Loads of batch j (clamped to the last batch: a reload past the end is never used): the weights,
+  // then, once the previous contents of the slot are used, the epilogue operands.
+  auto n0_of = [&](long j) {
+    return min(static_cast<long>(blockIdx.x) + static_cast<long>(gridDim.x) * j, nb - 1) *
+           (16 * NT);
+  };
+  auto load_w = [&](StreamSlot<MF, NT, KB, FPW>& f, long j) {
+    const long n0 = n0_of(j);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const size_t col = static_cast<size_t>(min(n0 + 16 * t + r16, a.N - 1)) * a.K;
+#pragma unroll
+      for (int q = 0; q < 2 * KB; ++q)
+        f.w[t][q] = ld16<false>(a.w + col + kw + 64 * (q >> 1) + 16 * grp + 8 * (q & 1));
+    }
+  };
+  auto load_e = [&](StreamSlot<MF, NT, KB, FPW>& f, long j) {
+    const long n0 = n0_of(j);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int u = 0; u < FPW; ++u) {
+        const int fr = min(wave + u * WK, MF - 1);
+        // N % 4 == 0 here: a group past N reads the last 4 columns (never stored)
+        f.e[t][u] = epi_load_raw<YDT>(a, min(m0 + 16 * fr + r16, a.M - 1),
+                                      min(n0 + 16 * t + 4 * grp, a.N - 4));
+      }
+  };
+
+  StreamSlot<MF, NT, KB, FPW> f[D];
+#pragma unroll
+  for (int s = 0; s < D; ++s) {
+    load_w(f[s], s);
+    load_e(f[s], s);
+  }
+
+  const long nbw = blockIdx.x < nb ? (nb - 1 - blockIdx.x) / gridDim.x + 1 : 0;  // own batches
+
+  // Batch j of this workgroup covers columns n0_of(j) ..; process() multiplies, sums the waves and
+  // stores it (the slot's weights are reloaded for batch j + D as soon as the products are issued,
+  // its epilogue operands once they are used).
+  auto process = [&](StreamSlot<MF, NT, KB, FPW>& f, long j, bool reload) {
+    f4v acc[NT][MF];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < MF; ++i) acc[t][i] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2 * KB; ++q)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const h8 wv = __builtin_bit_cast(h8, f.w[t][q]);
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+          acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xf.hi[i][q], acc[t][i], 0, 0, 0);
+          if constexpr (XM == kXSplit)
+            acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xf.lo[i][q], acc[t][i], 0, 0, 0);
+        }
+      }
+    if (reload) load_w(f, j + D);
+
+    const long n0 = n0_of(j);
+    // A batch past the workgroup's own (the rounding of its count to whole rounds) stores nothing:
+    // with the residual read from y itself it would add the residual twice.
+    const bool live = j < nbw;
+    if constexpr (WK == 1) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+          finish4s<YDT, ACT>(a, m0 + 16 * i + r16, n0 + 16 * t + 4 * grp, acc[t][i], f.e[t][i],
+                             live);
+    } else {
+      f4v* rb = red + (j & 1) * (WK * NT * MF * kWave);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < MF; ++i) rb[((wave * NT + t) * MF + i) * kWave + lane] = acc[t][i];
+      lds_barrier();
+#pragma unroll
+      for (int u = 0; u < FPW; ++u) {
+        const int fr = wave + u * WK;
+        if (FPW * WK == MF || fr < MF) {  // every wave has a fragment when WK divides MF
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            f4v sum = rb[(t * MF + fr) * kWave + lane];
+#pragma unroll
+            for (int w = 1; w < WK; ++w) sum = sum + rb[((w * NT + t) * MF + fr) * kWave + lane];
+            finish4s<YDT, ACT>(a, m0 + 16 * fr + r16, n0 + 16 * t + 4 * grp, sum, f.e[t][u], live);
+          }
+        }
+      }
+    }
+    if (reload) load_e(f, j + D);
+  };
+
+  // The workgroup's batches run in whole rounds of D with no exit inside a round (an exit there
+  // would merge into the loop's entry, and the compiler's wait counts at the top of the loop would
+  // then assume that path's few loads in flight). Batches past the workgroup's last one load the
+  // last batch of the launch again (n0_of clamps) and store nothing.
+  for (long j = 0; j < nbw; j += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) process(f[s], j + s, true);
+  }
+}
+
 // ---- launch plan ---------------------------------------------------------------------------------
 
 template <int XM, int YDT, int MF, int NF, int WK, int D, bool LN>
@@ -563,8 +808,52 @@ Plan plan_for(long M, long N, long K) {
   return {1, 1, 1, 1};
 }
 
+// Long weight streams at K = 512 or 1024 (k slices of 128 over 4 or 8 waves), no activation or
+// ReLU, with aligned bias / residual / output rows: the persistent streaming kernel, one
+// workgroup per CU (more per CU measured slower on MI355X), two 16-column tiles per batch and two
+// batches of loads in flight (of 1-4 and 1-3 tried, the best on the replicated decode shapes).
+constexpr int kStreamNT = 2, kStreamD = 2;
+
+// (fp32 x kept as hi + lo needs twice the activation registers: K = 512 only.)
+bool stream_ok(const GvArgs& a, bool tiled, long tiles, size_t ysz, bool split) {
+  if (!tiled || tiles < 16384 || a.N % 4 || !a.vec_store) return false;
+  if (a.K != 512 && (a.K != 1024 || split)) return false;
+  if (a.act != GSVK_ACT_NONE && a.act != GSVK_ACT_RELU) return false;
+  if (a.bias && !aligned16(a.bias)) return false;
+  return !a.res || reinterpret_cast<uintptr_t>(a.res) % (4 * ysz) == 0;
+}
+
+template <int XM, int YDT, int ACT, int WK>
+void launch_stream_wk(const GvArgs& a, hipStream_t st) {
+  constexpr int MF = 4, KB = 2;
+  const long nb = (a.N + 16 * kStreamNT - 1) / (16 * kStreamNT);
+  const dim3 grid(static_cast<unsigned>(std::min<long>(nb, device_cus())),
+                  static_cast<unsigned>((a.M + 16 * MF - 1) / (16 * MF)));
+  hipLaunchKernelGGL((gemv_stream<XM, YDT, ACT, MF, KB, WK, kStreamNT, kStreamD>), grid,
+                     dim3(kWave * WK), 0, st, a);
+}
+
+template <int XM, int YDT>
+void launch_stream(const GvArgs& a, hipStream_t st) {
+  if constexpr (XM == kXSplit) {
+    if (a.act == GSVK_ACT_RELU) return launch_stream_wk<XM, YDT, GSVK_ACT_RELU, 4>(a, st);
+    return launch_stream_wk<XM, YDT, GSVK_ACT_NONE, 4>(a, st);
+  } else {
+    if (a.act == GSVK_ACT_RELU)
+      return a.K == 512 ? launch_stream_wk<XM, YDT, GSVK_ACT_RELU, 4>(a, st)
+                        : launch_stream_wk<XM, YDT, GSVK_ACT_RELU, 8>(a, st);
+    return a.K == 512 ? launch_stream_wk<XM, YDT, GSVK_ACT_NONE, 4>(a, st)
+                      : launch_stream_wk<XM, YDT, GSVK_ACT_NONE, 8>(a, st);
+  }
+}
+
 template <int XM, int YDT, bool LN>
 void launch_plan(const GvArgs& a, bool tiled, hipStream_t st) {
+  if constexpr (!LN) {
+    const long tiles = (a.N + 15) / 16 * ((a.M + 15) / 16);
+    if (stream_ok(a, tiled, tiles, YDT == GSVK_F32 ? 4 : 2, XM == kXSplit))
+      return launch_stream<XM, YDT>(a, st);
+  }
   if (!tiled && !LN) {
     const long blocks = std::min<long>((a.M * a.N + 255) / 256, 4096);
     hipLaunchKernelGGL((gemv_generic<XM, YDT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,

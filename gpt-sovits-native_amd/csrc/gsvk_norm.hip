@@ -248,14 +248,6 @@ __device__ __forceinline__ double block_sum(float v, double* red) {
 constexpr int kGrBlock = 512;
 constexpr int kGrWaves = kGrBlock / kWave;
 
-// Workgroup barrier that orders LDS only (__syncthreads() would also wait for the thread's
-// outstanding global stores and loads).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ double block_sum512(float v, double* red) {
   const float w_sum = wave_sum(v);
   const int w = threadIdx.x / kWave;

@@ -156,10 +156,75 @@ def test_gemv_activations(act):
 
 
 def test_gemv_many_column_tiles():
-    """N >= 65536 takes the 64-column workgroup tiles."""
+    """16 rows x 65,576 columns: 4,099 tiles of 16 x 16, below the long-stream threshold (16,384
+    tiles), so the decode tiles run over many column blocks."""
     got, want, _ = run_case(16, 65536 + 40, 512, F16, True, F16, gsvk.ACT_RELU, True, False,
                             seed=5)
     assert_gemv_close(F16, got, want, gsvk.ACT_RELU, "wide")
+
+
+# Long weight streams (>= 16,384 tiles of 16 x 16 at K = 512 or 1024, no activation or ReLU, aligned
+# operands) run on the persistent streaming kernel: against the oracle at three shapes (a ragged last
+# column batch, a ragged row group with bf16 output and residual, K = 1024), and bit for bit against
+# the 64-row tiled kernel at K = 512, which sums in the same order (k slices of 128 per wave, waves
+# added in order): forced there by a bias that is not 16-byte aligned.
+STREAM = [  # rows, n_out, n_in, x_dt, round_x, y_dt, act, use_bias, use_res
+    (64, 65536 + 4, 512, F16, True, F32, gsvk.ACT_NONE, True, False),
+    (50, 65536, 512, F32, True, BF16, gsvk.ACT_NONE, True, True),
+    (64, 65536 + 32, 1024, F16, True, F16, gsvk.ACT_RELU, True, True),
+]
+
+
+@pytest.mark.parametrize("rows,n_out,n_in,x_dt,round_x,y_dt,act,use_bias,use_res", STREAM)
+def test_gemv_long_stream(rows, n_out, n_in, x_dt, round_x, y_dt, act, use_bias, use_res):
+    got, want, _ = run_case(rows, n_out, n_in, x_dt, round_x, y_dt, act, use_bias, use_res,
+                            seed=11)
+    assert_gemv_close(y_dt, got, want, act, f"stream {rows}x{n_out}x{n_in}")
+
+
+@pytest.mark.parametrize("y_dt", [F32, F16, BF16])
+@pytest.mark.parametrize("x_dt,round_x", [(F16, True), (F32, True), (F32, False)])
+def test_gemv_long_stream_equals_tiled(x_dt, round_x, y_dt):
+    rows, n_out, n_in = 64, 65536 + 36, 512
+    say(f"stream vs tiled x={x_dt} round={round_x} y={y_dt}")
+    r = rng(40 + 3 * x_dt + y_dt + int(round_x))
+    x = O.to_storage(x_dt, r.standard_normal((rows, n_in)).astype(np.float32))
+    w = weights(r, n_out, n_in)
+    b = (0.02 * r.standard_normal(n_out)).astype(np.float32)
+    res = O.to_storage(y_dt, r.standard_normal((rows, n_out)).astype(np.float32))
+    X, W, R = dev(x, x_dt), dev(w, F16), dev(res, y_dt)
+    aligned = devf(b)
+    shifted = devf(np.concatenate([np.zeros(1, np.float32), b]))[1:]  # same values, 4 bytes off
+    assert aligned.data_ptr() % 16 == 0 and shifted.data_ptr() % 16 == 4
+    outs = []
+    for bias in (aligned, shifted):
+        Y = torch.empty_like(R)
+        gsvk.gemv_f16w(X, W, Y, bias=bias, act=gsvk.ACT_RELU, residual=R, round_x=round_x)
+        torch.cuda.synchronize()
+        outs.append(host(Y, y_dt))
+    g, t = O.to_f32(y_dt, outs[0]), O.to_f32(y_dt, outs[1])
+    assert np.array_equal(np.isnan(g), np.isnan(t))
+    assert np.array_equal(outs[0], outs[1]), \
+        f"{np.count_nonzero(outs[0] != outs[1])} elements differ between the two kernels"
+
+
+def test_gemv_long_stream_residual_in_place():
+    r = rng(12)
+    rows, n_out, n_in = 64, 65536 + 4, 512
+    x = O.to_storage(F16, r.standard_normal((rows, n_in)).astype(np.float32))
+    w = weights(r, n_out, n_in)
+    bias = (0.02 * r.standard_normal(n_out)).astype(np.float32)
+    h = O.to_storage(F16, r.standard_normal((rows, n_out)).astype(np.float32))
+    want = O.gemv_f16w(F16, x, w, F16, bias=bias, residual=h)
+    X, W, B = dev(x, F16), dev(w, F16), devf(bias)
+    outs = []
+    for _ in range(2):
+        Y = dev(h, F16)
+        gsvk.gemv_f16w(X, W, Y, bias=B, residual=Y)
+        torch.cuda.synchronize()
+        outs.append(host(Y, F16))
+    assert_gemv_close(F16, outs[0], want, what="stream in place")
+    assert np.array_equal(outs[0], outs[1])
 
 
 def test_gemv_residual_in_place_and_deterministic():
