@@ -29,6 +29,11 @@
  *                        identity between the two modes, epilogue order
  * Functions marked "no reference vector" are pinned by mathematics only: the reference holds no
  * golden data for them.
+ *
+ * Parity unpinned at the last bit: whether the reference binary fuses embed_pe's e + alpha * pe
+ * (taken here as one fmaf) and branch_mean's product and sum (taken here as two roundings) is a
+ * choice of its compiler that no reference vector records; the two readings differ by at most one
+ * rounding of the product per term.
  */
 #include "gsvk_oracle.h"
 
