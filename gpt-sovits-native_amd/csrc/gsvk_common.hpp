@@ -245,13 +245,30 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// The two cross-row steps: rows 1 and 3 add lane 15 of the row before (row_bcast:15), then rows 2
+// and 3 add lane 31 (row_bcast:31), each as one v_add_f32_dpp whose other rows keep v (where
+// v + dpp_rows_f32 computes v + 0: the same value up to the sign of a zero, in rows that are never
+// read). Written as dpp_rows_f32 + add, each step is three instructions: the move with a zero old
+// value is not folded into the add when the row mask is partial. The compiler does not see inside
+// the asm, so it carries the wait states DPP needs after a VALU write of its source: two before
+// each DPP read, two after for the v_readlane of the result.
+__device__ __forceinline__ float add_row_bcasts(float v) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f32<0x141>(v);  // row_half_mirror
   v += dpp_f32<0x140>(v);  // row_mirror
-  v += dpp_rows_f32<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-  v += dpp_rows_f32<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  v = add_row_bcasts(v);   // rows 1, 3 then 2, 3: lane 63 holds (r3 + r2) + (r1 + r0)
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 

@@ -105,26 +105,75 @@ struct LayerIn {
   float bo[CPL][V], g1[CPL][V], be1[CPL][V], b2[CPL][V], g2[CPL][V], be2[CPL][V];
 };
 
+// Rows an absent parameter vector reads instead (d_model <= 1024 here): the choice between a
+// given vector and these is made once per layer on the wave-uniform pointer, so each lane only
+// adds its own 32-bit offset (and the loads take the scalar-base + 32-bit-offset address form).
+static __device__ __attribute__((aligned(16))) float kRowZeros[1024] = {};
+static __device__ __attribute__((aligned(16))) float kRowOnes[1024] = {[0 ... 1023] = 1.f};
+
 template <int DT, int CPL>
 __device__ __forceinline__ void load_layer(const StepLayer& L, size_t row_off,
-                                           const int (&idx)[CPL], LayerIn<DT, CPL>& f) {
-  constexpr int V = Store<DT>::VEC;
-  constexpr size_t kEsz = DT == GSVK_F32 ? 4 : 2;
+                                           const uint32_t (&eo)[CPL], LayerIn<DT, CPL>& f) {
+  constexpr uint32_t kEsz = DT == GSVK_F32 ? 4 : 2;
+  const char* att = static_cast<const char*>(L.attn_out) + row_off * kEsz;  // wave-uniform
+  const char* ffo = static_cast<const char*>(L.ffn_out) + row_off * kEsz;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const size_t e = row_off + static_cast<size_t>(idx[c]) * V;
-    f.att[c] = ld16<false>(static_cast<const char*>(L.attn_out) + e * kEsz);
-    f.ffo[c] = ld16<false>(static_cast<const char*>(L.ffn_out) + e * kEsz);
+    f.att[c] = ld16<false>(att + eo[c] * kEsz);
+    f.ffo[c] = ld16<false>(ffo + eo[c] * kEsz);
   }
+  const float* bo = L.bout ? L.bout : kRowZeros;
+  const float* g1 = L.n1g ? L.n1g : kRowOnes;
+  const float* be1 = L.n1b ? L.n1b : kRowZeros;
+  const float* b2 = L.b2 ? L.b2 : kRowZeros;
+  const float* g2 = L.n2g ? L.n2g : kRowOnes;
+  const float* be2 = L.n2b ? L.n2b : kRowZeros;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const size_t i = static_cast<size_t>(idx[c]) * V;
-    load_param(L.bout, i, kZeros8, f.bo[c]);
-    load_param(L.n1g, i, kOnes8, f.g1[c]);
-    load_param(L.n1b, i, kZeros8, f.be1[c]);
-    load_param(L.b2, i, kZeros8, f.b2[c]);
-    load_param(L.n2g, i, kOnes8, f.g2[c]);
-    load_param(L.n2b, i, kZeros8, f.be2[c]);
+#pragma unroll
+    for (int k = 0; k < Store<DT>::VEC; k += 4) {
+      load_f32x4(bo + eo[c], k, &f.bo[c][k]);
+      load_f32x4(g1 + eo[c], k, &f.g1[c][k]);
+      load_f32x4(be1 + eo[c], k, &f.be1[c][k]);
+      load_f32x4(b2 + eo[c], k, &f.b2[c][k]);
+      load_f32x4(g2 + eo[c], k, &f.g2[c][k]);
+      load_f32x4(be2 + eo[c], k, &f.be2[c][k]);
+    }
+  }
+}
+
+// The rounded value of a stored row chunk as the next LayerNorm reads it back: fp16 rows stay
+// packed (the next residual add takes the halves directly), other types as fp32.
+template <int DT, int CPL>
+struct RowVal {
+  float f[CPL][Store<DT>::VEC];
+};
+template <int CPL>
+struct RowVal<GSVK_F16, CPL> {
+  u32x4 p[CPL];
+};
+
+// float(half) + b with one rounding: v_fma_mix_f32 h, 1.0, b (the half is converted exactly and
+// multiplied by one exactly, so this is the conversion and the add in one instruction, the same
+// bits). HI selects the upper half of the word.
+template <bool HI>
+__device__ __forceinline__ float add_half(uint32_t w, float b) {
+  float d;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(b));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(b));
+  return d;
+}
+
+// v[k] = (float(h[k]) + bias[k]) + float(r[k]) for 8 packed halves h and r.
+__device__ __forceinline__ void add2_halves(const u32x4& h, const float (&bias)[8], const u32x4& r,
+                                            float (&v)[8]) {
+  const uint32_t hw[4] = {h.x, h.y, h.z, h.w}, rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[2 * k] = add_half<false>(rw[k], add_half<false>(hw[k], bias[2 * k]));
+    v[2 * k + 1] = add_half<true>(rw[k], add_half<true>(hw[k], bias[2 * k + 1]));
   }
 }
 
@@ -135,11 +184,11 @@ __device__ __forceinline__ void load_layer(const StepLayer& L, size_t row_off,
 template <int DT, int CPL, bool FULL>
 __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL],
                                        const float (&bias)[CPL][Store<DT>::VEC],
-                                       const float (&res)[CPL][Store<DT>::VEC],
+                                       const RowVal<DT, CPL>& res,
                                        const float (&g)[CPL][Store<DT>::VEC],
                                        const float (&b)[CPL][Store<DT>::VEC],
                                        const bool (&on)[CPL], void* y, size_t row_off,
-                                       const int (&idx)[CPL], float (&yr)[CPL][Store<DT>::VEC]) {
+                                       const uint32_t (&eo)[CPL], RowVal<DT, CPL>& yr) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   float v[CPL][V];
@@ -147,11 +196,15 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     if (FULL || on[c]) {
-      S::unpack(in[c], v[c]);
+      if constexpr (DT == GSVK_F16) {
+        add2_halves(in[c], bias[c], res.p[c], v[c]);
+      } else {
+        S::unpack(in[c], v[c]);
 #pragma unroll
-      for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + bias[c][k];
+        for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + bias[c][k];
 #pragma unroll
-      for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + res[c][k];
+        for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + res.f[c][k];
+      }
       s = c == 0 ? chunk_sum(v[c]) : s + chunk_sum(v[c]);
     } else {
 #pragma unroll
@@ -171,17 +224,17 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
   const float var = FULL ? wave_sum(q * a.inv_n_f)
                          : static_cast<float>(static_cast<double>(wave_sum(q)) * a.inv_n);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
+  constexpr uint32_t kEsz = DT == GSVK_F32 ? 4 : 2;
+  char* yrow = static_cast<char*>(y) + row_off * kEsz;  // wave-uniform
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     float o[V];
 #pragma unroll
     for (int k = 0; k < V; ++k) o[k] = __builtin_fmaf((v[c][k] - mean) * rstd, g[c][k], b[c][k]);
     const u32x4 packed = S::pack(o);
-    if (FULL || on[c])
-      st16<false>(static_cast<char*>(y) + (row_off + static_cast<size_t>(idx[c]) * V) *
-                                              (DT == GSVK_F32 ? 4 : 2),
-                  packed);
-    S::unpack(packed, yr[c]);
+    if (FULL || on[c]) st16<false>(yrow + eo[c] * kEsz, packed);
+    if constexpr (DT == GSVK_F16) yr.p[c] = packed;
+    else S::unpack(packed, yr.f[c]);
   }
 }
 
@@ -199,13 +252,14 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   constexpr int V = S::VEC;
   const int lane = threadIdx.x;
   const int nch = static_cast<int>(a.D / V);
-  int idx[CPL];
+  uint32_t eo[CPL];  // element offset of the lane's chunk c within a row
   bool on[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int i = lane + c * kWave;
     on[c] = FULL || i < nch;
-    idx[c] = on[c] ? i : nch - 1;  // clamped: loads stay unconditional, stores are guarded
+    // clamped: loads stay unconditional, stores are guarded
+    eo[c] = static_cast<uint32_t>(on[c] ? i : nch - 1) * V;
   }
   const size_t row_off = static_cast<size_t>(b) * static_cast<size_t>(a.D);
 
@@ -219,19 +273,19 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   // Layers 0, 1 and 2 are in flight while the gather resolves its id.
   const int L = a.layers;
   LayerIn<DT, CPL> f[3];
-  load_layer<DT, CPL>(a.L[0], row_off, idx, f[0]);
-  load_layer<DT, CPL>(a.L[L > 1 ? 1 : 0], row_off, idx, f[1]);
-  load_layer<DT, CPL>(a.L[L > 2 ? 2 : L - 1], row_off, idx, f[2]);
+  load_layer<DT, CPL>(a.L[0], row_off, eo, f[0]);
+  load_layer<DT, CPL>(a.L[L > 1 ? 1 : 0], row_off, eo, f[1]);
+  load_layer<DT, CPL>(a.L[L > 2 ? 2 : L - 1], row_off, eo, f[2]);
 
   const int64_t id = a.ids32 ? static_cast<int64_t>(static_cast<int32_t>(id_lo))
                              : static_cast<int64_t>((static_cast<uint64_t>(id_hi) << 32) | id_lo);
   const bool ok = id >= 0 && id < a.vocab && p >= 0 && p < a.max_pos;
   const size_t trow = static_cast<size_t>(ok ? id : 0) * static_cast<size_t>(a.D);
   const size_t prow = static_cast<size_t>(ok ? p : 0) * static_cast<size_t>(a.D);
-  float xr[CPL][V];
+  RowVal<DT, CPL> xr;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const size_t i = static_cast<size_t>(idx[c]) * V;
+    const size_t i = eo[c];
     float e[V], pe[V], o[V];
     switch (a.tab_dt) {  // wave-uniform
       case GSVK_F32: load_elems<GSVK_F32, V>(a.table, trow + i, e); break;
@@ -244,14 +298,15 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
     const u32x4 packed = S::pack(o);
     if (FULL || on[c])
       st16<false>(static_cast<char*>(a.x) + (row_off + i) * (DT == GSVK_F32 ? 4 : 2), packed);
-    S::unpack(packed, xr[c]);
+    if constexpr (DT == GSVK_F16) xr.p[c] = packed;
+    else S::unpack(packed, xr.f[c]);
   }
   if (!ok && lane == 0 && a.err) *a.err = 1;
 
-  float hr[CPL][V];
+  RowVal<DT, CPL> hr;
   auto layer = [&](LayerIn<DT, CPL>& fi) {
-    ln_row<DT, CPL, FULL>(a, fi.att, fi.bo, xr, fi.g1, fi.be1, on, a.h, row_off, idx, hr);
-    ln_row<DT, CPL, FULL>(a, fi.ffo, fi.b2, hr, fi.g2, fi.be2, on, a.x, row_off, idx, xr);
+    ln_row<DT, CPL, FULL>(a, fi.att, fi.bo, xr, fi.g1, fi.be1, on, a.h, row_off, eo, hr);
+    ln_row<DT, CPL, FULL>(a, fi.ffo, fi.b2, hr, fi.g2, fi.be2, on, a.x, row_off, eo, xr);
   };
   // sched_barrier(0) keeps the scheduler from hoisting the next layer's arithmetic (and so its
   // loads' waits) into the current layer's reductions: measured, that put a wait on loads issued
@@ -262,7 +317,7 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   StepLayer rec = a.L[L > 3 ? 3 : L - 1];
   auto refill = [&](LayerIn<DT, CPL>& fi, int l) {
     __builtin_amdgcn_sched_barrier(0);
-    load_layer<DT, CPL>(rec, row_off, idx, fi);
+    load_layer<DT, CPL>(rec, row_off, eo, fi);
     rec = a.L[l + 1 < L ? l + 1 : L - 1];
     __builtin_amdgcn_sched_barrier(0);
   };
