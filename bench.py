@@ -862,6 +862,22 @@ def step_ops(gsvk, bufs):
     return L0, R0, E0
 
 
+def step_layer_sweep(torch, gsvk, bufs, layers=(1, 2, 4, 8, 16, 24), iters=300):
+    """The fused step over the first L layers of the same buffers, eager launches: the per-layer
+    slope of the chain and the fixed cost of one launch."""
+    out = {}
+    for L in layers:
+        b = dict(bufs)
+        for k in ("attn_out", "ff", "ffn_out", "bout", "b1", "b2", "n1g", "n2g", "n1b", "n2b"):
+            b[k] = bufs[k][:L]
+        st = gsvk.T2SStep(b, eps=1e-5, graph=False, fused=True)
+        us = time_loop(torch, st.run, iters, warmup=20) * 1e3
+        st.close()
+        out[L] = round(us, 2)
+        log(f"  fused step, {L} layers: {us:.2f} us")
+    return out
+
+
 def copy_bandwidth(torch, dev, nbytes=1 << 30):
     """A plain device-to-device copy of 1 GiB (read + write counted), timed like the replicated
     kernels: the achievable-bandwidth reference of this GPU under the same method."""
@@ -994,6 +1010,8 @@ def main():
     ap.add_argument("--only", default=None, help="run one kernel of the suite and exit")
     ap.add_argument("--pmc", action="store_true",
                     help="run the step kernel and a plain copy only (for rocprofv3 --pmc)")
+    ap.add_argument("--step-layers", action="store_true",
+                    help="the fused step over 1..24 layers of the same buffers (per-layer slope)")
     ap.add_argument("--ln-traffic", action="store_true",
                     help="LN [64,512] with and without parameters + a copy (rocprofv3 --pmc runs)")
     ap.add_argument("--no-traffic", action="store_true",
@@ -1043,6 +1061,9 @@ def main():
         return
     if a.ln_traffic:
         ln_param_traffic_workload(torch, gsvk, bufs)
+        return
+    if a.step_layers:
+        print(json.dumps({"fused_step_us_by_layers": step_layer_sweep(torch, gsvk, bufs)}))
         return
     nbytes = step_bytes()
 

@@ -286,7 +286,9 @@ def test_groupnorm_out_of_phase_buffers_use_generic_path():
 
 # ---- SoVITS element-wise -------------------------------------------------------------------------
 
-SOVITS_SHAPES = [(384, 5000), (24, 320000), (3, 1001)]
+# the reference geometry's first and last stages, configuration 5's literal geometry (512 channels
+# halving per stage: its first and last stages, 256 x 5000 and 32 x 320000), and a ragged small one
+SOVITS_SHAPES = [(384, 5000), (24, 320000), (256, 5000), (32, 320000), (3, 1001)]
 
 
 @pytest.mark.parametrize("C,T", SOVITS_SHAPES)
