@@ -308,18 +308,19 @@ __global__ __launch_bounds__(kWave * kMaxChunks) void attn_merge(AttnArgs a, int
   store8<OUTT>(a.out, static_cast<size_t>(b) * a.ldo + 8 * lane, y);
 }
 
-// Key chunks per sequence. The workgroups of a launch stream their keys in step, so the grid is
-// sized to whole rounds of about two workgroups per CU: with B = 64 on 256 CUs, 8 chunks. Measured
-// on the whole T2S decode step (B = 64, 1088 and 2112 keys): 8 chunks ran 7% faster than 9 (2.25
-// workgroups per CU: a quarter-full last round) and 2% faster than 16. Contexts up to 256 keys
-// take one chunk per 128 keys, and no chunk is shorter than 64 keys.
+// Key chunks per sequence: one round of at most one workgroup per CU, 4 chunks at B = 64 on 256
+// CUs. The workgroups of a launch stream their keys in step, so a partly filled last round costs a
+// whole one. Measured on the whole T2S decode step (B = 64, 1024 and 2048 cached keys, non-temporal
+// cache reads): 4 chunks ran 2.3% faster than 8 (two full rounds, twice the merge reads) and 5-6%
+// faster than 6 (a half-full second round); 9 chunks were slower than 8 and 16 slower again.
+// Contexts up to 256 keys take one chunk per 128 keys, and no chunk is shorter than 64 keys.
 int chunks_for(size_t batch, size_t len_bound) {
   const long lb = static_cast<long>(len_bound), B = static_cast<long>(batch);
   long c;
   if (lb <= 256) {
     c = (lb + 127) / 128;
   } else {
-    c = (2L * device_cus() + B - 1) / B;
+    c = device_cus() / B;
     c = std::min(c, (lb + 63) / 64);
   }
   return static_cast<int>(std::max(1L, std::min<long>(c, kMaxChunks)));

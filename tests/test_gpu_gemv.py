@@ -164,14 +164,16 @@ def test_gemv_many_column_tiles():
 
 
 # Long weight streams (>= 16,384 tiles of 16 x 16 at K = 512 or 1024, no activation or ReLU, aligned
-# operands) run on the persistent streaming kernel: against the oracle at three shapes (a ragged last
-# column batch, a ragged row group with bf16 output and residual, K = 1024), and bit for bit against
+# operands) run on the persistent streaming kernel: against the oracle at four shapes (a ragged last
+# column batch, a ragged row group with bf16 output and residual, K = 1024, 100 rows in two row
+# groups), and bit for bit against
 # the 64-row tiled kernel at K = 512, which sums in the same order (k slices of 128 per wave, waves
 # added in order): forced there by a bias that is not 16-byte aligned.
 STREAM = [  # rows, n_out, n_in, x_dt, round_x, y_dt, act, use_bias, use_res
     (64, 65536 + 4, 512, F16, True, F32, gsvk.ACT_NONE, True, False),
     (50, 65536, 512, F32, True, BF16, gsvk.ACT_NONE, True, True),
     (64, 65536 + 32, 1024, F16, True, F16, gsvk.ACT_RELU, True, True),
+    (100, 40000, 512, F32, True, F32, gsvk.ACT_RELU, True, True),  # two row groups, the second partial
 ]
 
 
