@@ -862,19 +862,20 @@ def step_ops(gsvk, bufs):
     return L0, R0, E0
 
 
-def step_layer_sweep(torch, gsvk, bufs, layers=(1, 2, 4, 8, 16, 24), iters=300):
-    """The fused step over the first L layers of the same buffers, eager launches: the per-layer
-    slope of the chain and the fixed cost of one launch."""
+def step_layer_sweep(torch, gsvk, bufs, layers=(1, 2, 4, 8, 16, 24)):
+    """The fused step over the first L layers of the same buffers, device time per launch (a graph
+    of 32 back-to-back launches; eager launches from Python would measure the host's launch rate
+    at few layers): the per-layer slope of the chain and the fixed cost of one launch."""
     out = {}
     for L in layers:
         b = dict(bufs)
         for k in ("attn_out", "ff", "ffn_out", "bout", "b1", "b2", "n1g", "n2g", "n1b", "n2b"):
             b[k] = bufs[k][:L]
         st = gsvk.T2SStep(b, eps=1e-5, graph=False, fused=True)
-        us = time_loop(torch, st.run, iters, warmup=20) * 1e3
+        us = graph_us_per_launch(torch, st.run, launches=32, replays=20)
         st.close()
-        out[L] = round(us, 2)
-        log(f"  fused step, {L} layers: {us:.2f} us")
+        out[L] = round(us, 3)
+        log(f"  fused step, {L} layers: {us:.3f} us")
     return out
 
 

@@ -272,6 +272,36 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// add_row_bcasts for two independent values, the steps of one interleaved with the other's (each
+// DPP read is then two or more wait states after the VALU write of its source).
+__device__ __forceinline__ void add_row_bcasts2(float& a, float& b) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "v_add_f32_dpp %1, %1, %1 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "v_add_f32_dpp %1, %1, %1 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(a), "+v"(b));
+}
+
+// Two wave sums at once (each the same bits as wave_sum of that value): the two dependent chains
+// interleave, so the pair costs about one chain's latency.
+__device__ __forceinline__ void wave_sum2(float a, float b, float& ra, float& rb) {
+  a += dpp_f32<0xB1>(a);
+  b += dpp_f32<0xB1>(b);
+  a += dpp_f32<0x4E>(a);
+  b += dpp_f32<0x4E>(b);
+  a += dpp_f32<0x141>(a);
+  b += dpp_f32<0x141>(b);
+  a += dpp_f32<0x140>(a);
+  b += dpp_f32<0x140>(b);
+  add_row_bcasts2(a, b);
+  ra = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
+  rb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 63));
+}
+
 // Per-lane partial sums of one 16-byte chunk (4 or 8 values) as a balanced tree: depth 2-3
 // instead of a 3-7 long dependent chain (each dependent VALU step costs ~11 cycles on MI355X, and
 // the LayerNorm reductions sit on the critical path of latency-bound calls).
@@ -280,6 +310,15 @@ __device__ __forceinline__ float chunk_sum(const float (&v)[V]) {
   static_assert(V == 4 || V == 8, "chunk of 4 or 8 values");
   if constexpr (V == 4) return (v[0] + v[1]) + (v[2] + v[3]);
   else return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+// Sum of v^2 over one chunk: pairs fma(v1, v1, v0 * v0), then a tree of the pairs.
+template <int V>
+__device__ __forceinline__ float chunk_sq(const float (&v)[V]) {
+  float q[V / 2];
+#pragma unroll
+  for (int k = 0; k < V / 2; ++k) q[k] = __builtin_fmaf(v[2 * k + 1], v[2 * k + 1], v[2 * k] * v[2 * k]);
+  if constexpr (V == 4) return q[0] + q[1];
+  else return (q[0] + q[1]) + (q[2] + q[3]);
 }
 // Sum of (v - mean)^2 over one chunk: pairs fma(d1, d1, d0 * d0), then a tree of the pairs.
 template <int V>

@@ -15,13 +15,18 @@
 //
 // The chain wave prefetches the next layers' inputs (attn_out / ffn_out rows and the six parameter
 // vectors) three layers ahead into a register ring, so HBM latency is paid once, not per LayerNorm.
-// Its row reductions are DPP only (gsvk_common.hpp wave_sum): no LDS round trip per LayerNorm.
+// Its row reductions are DPP only (gsvk_common.hpp wave_sum2): no LDS round trip per LayerNorm.
 //
-// Numerics: the same operations in the same order as ln_rows_tile (gsvk_norm.hip), bias_act_tile
-// (gsvk_epilogue.hip) and embed_pe_vec (gsvk_embed.hip) with the same lane partition, and each
-// stored h / x is re-read as its rounded storage value (unpack of the packed store), so the fused
-// step is bitwise identical to the per-op launches.
+// Numerics: each LayerNorm takes its statistics in one pass, as kern::layernorm does
+// (kern.cpp:27-59: the row's sum and sum of squares, var = E[x^2] - mean^2, a centred second pass
+// only where that comes out negative), so its two row reductions run together and the chain pays
+// one reduction latency per LayerNorm. The per-op kernel (ln_rows_tile) takes exact two-pass
+// statistics; the two forms agree within the LayerNorm tolerance, not bit for bit. The gather and
+// the ReLU tiles are embed_pe_vec's and bias_act_tile's arithmetic (bit-exact), and each stored
+// h / x is re-read as its rounded storage value (unpack of the packed store), so every LayerNorm
+// sees exactly the residual the per-op form would read back.
 #include <cmath>
+#include <mutex>
 
 #include "gsvk_common.hpp"
 #include "gsvk_t2s.h"
@@ -105,9 +110,10 @@ struct LayerIn {
   float bo[CPL][V], g1[CPL][V], be1[CPL][V], b2[CPL][V], g2[CPL][V], be2[CPL][V];
 };
 
-// Rows an absent parameter vector reads instead (d_model <= 1024 here): the choice between a
-// given vector and these is made once per layer on the wave-uniform pointer, so each lane only
-// adds its own 32-bit offset (and the loads take the scalar-base + 32-bit-offset address form).
+// Rows an absent parameter vector reads instead (d_model <= 1024 here). The host puts their
+// device addresses into the layer records in place of null pointers, so the chain wave spends no
+// instruction choosing between a given vector and these: each lane only adds its own 32-bit offset
+// to the record's pointer (the scalar-base + 32-bit-offset address form).
 static __device__ __attribute__((aligned(16))) float kRowZeros[1024] = {};
 static __device__ __attribute__((aligned(16))) float kRowOnes[1024] = {[0 ... 1023] = 1.f};
 
@@ -122,12 +128,7 @@ __device__ __forceinline__ void load_layer(const StepLayer& L, size_t row_off,
     f.att[c] = ld16<false>(att + eo[c] * kEsz);
     f.ffo[c] = ld16<false>(ffo + eo[c] * kEsz);
   }
-  const float* bo = L.bout ? L.bout : kRowZeros;
-  const float* g1 = L.n1g ? L.n1g : kRowOnes;
-  const float* be1 = L.n1b ? L.n1b : kRowZeros;
-  const float* b2 = L.b2 ? L.b2 : kRowZeros;
-  const float* g2 = L.n2g ? L.n2g : kRowOnes;
-  const float* be2 = L.n2b ? L.n2b : kRowZeros;
+  const float *bo = L.bout, *g1 = L.n1g, *be1 = L.n1b, *b2 = L.b2, *g2 = L.n2g, *be2 = L.n2b;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
 #pragma unroll
@@ -177,10 +178,11 @@ __device__ __forceinline__ void add2_halves(const u32x4& h, const float (&bias)[
   }
 }
 
-// y = LN((in + bias) + res) over one row held by the wave, the operation order of ln_rows_tile:
-// per-lane chunk trees added in chunk order, wave_sum, mean = float(double(sum) / n), centred
-// second moment (chunk_sumsq), rstd = rsq(var + eps), y = fmaf((v - mean) rstd, g, b). Stores y and returns its
-// rounded storage value in `yr` (what the next LayerNorm reads back as its residual).
+// y = LN((in + bias) + res) over one row held by the wave: per-lane chunk trees of the values and
+// of their squares added in chunk order, both wave sums at once, mean = float(double(sum) / n),
+// var = E[x^2] - mean^2 (the centred second moment where that is negative), rstd = rsq(var + eps),
+// y = fmaf((v - mean) rstd, g, b). Stores y and returns its rounded storage value in `yr` (what the
+// next LayerNorm reads back as its residual).
 template <int DT, int CPL, bool FULL>
 __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL],
                                        const float (&bias)[CPL][Store<DT>::VEC],
@@ -211,18 +213,42 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
       for (int k = 0; k < V; ++k) v[c][k] = 0.f;
     }
   }
+  // One pass, as kern::layernorm (kern.cpp:29-48): the row's sum and sum of squares are reduced
+  // together (two interleaved DPP chains, one reduction latency on the critical path), then
+  // var = E[x^2] - mean^2, and only a row where that comes out negative or NaN (cancellation)
+  // takes the second, centred pass (kern.cpp:49-56).
   // With FULL rows n = 64 * CPL * VEC is a power of two, so scaling by 1/n is exact in fp32 and
-  // commutes with every rounding of the sum: the lane partials are scaled before the reduction
-  // (one fewer dependent step after it), and the result is the same value as ln_rows_tile's
-  // float(double(sum) * (1/n)) without the double-precision latency.
-  const float mean = FULL ? wave_sum(s * a.inv_n_f)
-                          : static_cast<float>(static_cast<double>(wave_sum(s)) * a.inv_n);
+  // commutes with every rounding of the sums: the lane partials are scaled before the reduction,
+  // and fmaf(-mean, mean, E[x^2]) rounds the exact difference once, as the reference's
+  // float(double(sqsum) / n - double(mean)^2) does (mean^2 is exact in double).
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
-    if (FULL || on[c]) q = c == 0 ? chunk_sumsq(v[c], mean) : q + chunk_sumsq(v[c], mean);
-  const float var = FULL ? wave_sum(q * a.inv_n_f)
-                         : static_cast<float>(static_cast<double>(wave_sum(q)) * a.inv_n);
+    if (FULL || on[c]) q = c == 0 ? chunk_sq(v[c]) : q + chunk_sq(v[c]);
+  float mean, var;
+  if constexpr (FULL) {
+    float ex2;
+    wave_sum2(s * a.inv_n_f, q * a.inv_n_f, mean, ex2);
+    var = __builtin_fmaf(-mean, mean, ex2);
+  } else {
+    float S, Q;
+    wave_sum2(s, q, S, Q);
+    mean = static_cast<float>(static_cast<double>(S) * a.inv_n);
+    const double m = mean;
+    var = static_cast<float>(static_cast<double>(Q) * a.inv_n - m * m);
+  }
+  if (!(var >= 0.f)) {  // wave-uniform
+    // (mean passed through an empty asm: otherwise the compiler shares this pass's v - mean with
+    // the normalization below and computes it ahead of the branch, on the common path)
+    float m2 = mean;
+    asm volatile("" : "+v"(m2));
+    float q2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      if (FULL || on[c]) q2 = c == 0 ? chunk_sumsq(v[c], m2) : q2 + chunk_sumsq(v[c], m2);
+    var = FULL ? wave_sum(q2 * a.inv_n_f)
+               : static_cast<float>(static_cast<double>(wave_sum(q2)) * a.inv_n);
+  }
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
   constexpr uint32_t kEsz = DT == GSVK_F32 ? 4 : 2;
   char* yrow = static_cast<char*>(y) + row_off * kEsz;  // wave-uniform
@@ -399,6 +425,30 @@ int launch_step(const StepArgs& a, hipStream_t st) {
 bool a16(const void* p) { return !p || aligned16(p); }
 
 }  // namespace
+
+// Device addresses of kRowZeros / kRowOnes on the current device, looked up once per device (with
+// that device current) and kept until the process ends. In host code the arrays' names are only
+// stand-ins for the symbols: the layer records get these addresses. False when the lookup fails.
+__attribute__((visibility("hidden"))) bool step_fill_rows(const float** zeros, const float** ones) {
+  static std::mutex mu;
+  static const float* z[kMaxDevices] = {};
+  static const float* o[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!z[dev]) {
+    void *pz = nullptr, *po = nullptr;
+    if (hipGetSymbolAddress(&pz, HIP_SYMBOL(kRowZeros)) != hipSuccess || !pz ||
+        hipGetSymbolAddress(&po, HIP_SYMBOL(kRowOnes)) != hipSuccess || !po)
+      return false;
+    z[dev] = static_cast<const float*>(pz);
+    o[dev] = static_cast<const float*>(po);
+  }
+  *zeros = z[dev];
+  *ones = o[dev];
+  return true;
+}
+
 }  // namespace gsvk
 
 using namespace gsvk;
@@ -483,9 +533,20 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
   a.ids32 = d->index_type == GSVK_I32;
   a.tab_dt = d->table_dtype;
   a.layers = static_cast<int>(d->layers);
+  const float *zeros = nullptr, *ones = nullptr;
+  if (!step_fill_rows(&zeros, &ones)) return GSVK_E_HIP;
+  auto or_fill = [](const float* p, const float* fill) { return p ? p : fill; };
   for (size_t l = 0; l < d->layers; ++l)
-    a.L[l] = StepLayer{d->attn_out[l], at(d->bout, l), at(d->n1g, l), at(d->n1b, l), d->ff[l],
-                       at(d->b1, l),   d->ffn_out[l],  at(d->b2, l),  at(d->n2g, l), at(d->n2b, l)};
+    a.L[l] = StepLayer{d->attn_out[l],
+                       or_fill(at(d->bout, l), zeros),
+                       or_fill(at(d->n1g, l), ones),
+                       or_fill(at(d->n1b, l), zeros),
+                       d->ff[l],
+                       at(d->b1, l),
+                       d->ffn_out[l],
+                       or_fill(at(d->b2, l), zeros),
+                       or_fill(at(d->n2g, l), ones),
+                       or_fill(at(d->n2b, l), zeros)};
   if (static_cast<size_t>(a.B + a.layers * a.relu_waves_per_layer) >= (1ul << 31)) return GSVK_E_SIZE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (d->dtype) {

@@ -569,7 +569,8 @@ class T2SStepDesc(ctypes.Structure):
 
 class T2SStep:
     """Owns a gsvk_t2s_step (graph of one decode step's epilogue launches) over torch buffers.
-    fused=True: the whole step as one kernel launch (gsvk_t2s_step_fused), bitwise the same."""
+    fused=True: the whole step as one kernel launch (gsvk_t2s_step_fused): the gather and ff
+    bitwise the same, h and x within the LayerNorm tolerance (one-pass statistics)."""
 
     def __init__(self, bufs, eps=1e-5, graph=True, fused=False):
         import torch

@@ -9,6 +9,12 @@
 #include "gsvk.h"
 #include "gsvk_t2s.h"
 
+namespace gsvk {
+// csrc/gsvk_step.hip: the device addresses the fused step's launch puts in place of absent
+// parameter vectors, looked up once per device.
+bool step_fill_rows(const float** zeros, const float** ones);
+}  // namespace gsvk
+
 namespace {
 
 bool desc_ok(const gsvk_t2s_step_desc* d) {
@@ -177,6 +183,9 @@ extern "C" int gsvk_t2s_step_create_fused(const gsvk_t2s_step_desc* desc, gsvk_t
   if (!out) return GSVK_E_NULL;
   *out = nullptr;
   if (!desc_ok(desc)) return GSVK_E_NULL;
+  // the launch's device-address lookup runs here, before the capture, not inside it
+  const float *zeros = nullptr, *ones = nullptr;
+  if (!gsvk::step_fill_rows(&zeros, &ones)) return GSVK_E_HIP;
   // an unsupported shape fails inside the capture; record() then ends it and keeps no graph
   return record([desc](hipStream_t st) { return gsvk_t2s_step_fused(desc, st); }, 1, out);
 }

@@ -74,9 +74,13 @@ void gsvk_t2s_step_destroy(gsvk_t2s_step* step);
 /* The same step as ONE kernel launch (no counterpart in the reference, which runs these loops
  * one row at a time; replaces the 1 + 3*layers launches above). The LayerNorm chain is row-local
  * (row b of layer l+1 reads only row b of layer l), so one wave walks the whole chain of one
- * sequence while the other waves of the launch run the ReLU tiles. Results are bitwise those of
- * gsvk_t2s_step_eager: every h and x is stored as the per-op launches store it (the final x and h
- * are the last layer's), every ff[l] is updated in place.
+ * sequence while the other waves of the launch run the ReLU tiles. Every h and x is stored as the
+ * per-op launches store it (the final x and h are the last layer's), every ff[l] is updated in
+ * place. The gather and ff[l] are bitwise those of gsvk_t2s_step_eager; each LayerNorm takes its
+ * statistics in one pass as gsv::kern::layernorm does (kern.cpp:27-59: sum and sum of squares,
+ * a centred second pass only where E[x^2] - mean^2 < 0), where gsvk_add_layernorm takes exact
+ * two-pass ones, so h and x agree with the per-op launches within the LayerNorm tolerance per
+ * layer, not bit for bit. Deterministic: the same inputs give the same bits on every call.
  * Limits: layers <= 32 (the layer pointers travel in the kernel arguments); d_model a multiple of
  * 8 (4 for f32) and at most 1024 (f16 / bf16) or 512 (f32) elements; ffn a multiple of 8 (4);
  * every pointer 16-byte aligned; x, h, ff[l] overlapping nothing else.
