@@ -688,11 +688,21 @@ def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
               ff=torch.empty(B, FF, dtype=f16, device=dev),
               qkv=torch.empty(B, 3 * D, dtype=f32, device=dev),
               logits=torch.empty(B, V, dtype=f32, device=dev))
+    # The step as built (B = 64 runs as two halves on two graph branches) and as one chain of
+    # launches, timed alternately.
     step = gsvk.T2SDecode(m, io, len_bound=max_len, graph=True)
+    one = gsvk.T2SDecode(m, io, len_bound=max_len, graph=True, split=False)
     for _ in range(warmup):
         step.run()
+        one.run()
     torch.cuda.synchronize()
-    ms = time_loop(torch, step.run, steps)
+    t_split, t_one = [], []
+    for _ in range(3):
+        t_split.append(time_loop(torch, step.run, steps))
+        t_one.append(time_loop(torch, one.run, steps))
+    ms, ms_one = statistics.median(t_split), statistics.median(t_one)
+    one_launches = one.launches
+    one.close()
     assert int(io["err"].item()) == 0
     # algorithmic bytes: every weight and parameter once, the kv_len cached rows of K and V per
     # layer once, the appended rows, and each activation read / written once
@@ -704,10 +714,12 @@ def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
     out = {"batch": B, "layers": LAYERS, "d_model": D, "ffn": FF, "heads": H, "vocab": V,
            "kv_len": kv_len, "storage": "f16", "kv_storage": "f16", "launches": step.launches,
            "us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(B / ms * 1e3, 0),
+           "one_chain_us_per_step": round(ms_one * 1e3, 1), "one_chain_launches": one_launches,
            "bytes_per_step": nbytes, "GBps": round(nbytes / ms / 1e6, 1),
            "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_GBS, 4)}
     log(f"  whole decode step (B={B}, kv_len={kv_len}, graph of {step.launches} launches): "
-        f"{out['us_per_step']} us, {out['tokens_per_s']:.0f} tokens/s, {out['GBps']} GB/s")
+        f"{out['us_per_step']} us, {out['tokens_per_s']:.0f} tokens/s, {out['GBps']} GB/s; "
+        f"as one chain of {one_launches} launches {out['one_chain_us_per_step']} us")
     step.close()
     del m, io, layers
     torch.cuda.empty_cache()

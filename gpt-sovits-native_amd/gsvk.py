@@ -79,6 +79,7 @@ SIGNATURES = {
     "gsvk_gsv_upload": (_i, [_vp, _i, _vp, _sz, _vp]),
     "gsvk_gsv_device_ptr": (_vp, [_vp, _i, _vp, _sz]),
     "gsvk_t2s_decode_create": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "gsvk_t2s_decode_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
     "gsvk_sovits_decoder_workspace_bytes": (_sz, [_vp]),
     "gsvk_sovits_decoder_eager": (_i, [_vp, _vp]),
     "gsvk_sovits_decoder_create": (_i, [_vp, ctypes.POINTER(_vp)]),
@@ -653,6 +654,7 @@ class T2SDecodeDesc(ctypes.Structure):
         ("max_pos", _sz), ("alpha", _f), ("err", _vp), ("layer", ctypes.POINTER(T2SLayer)),
         ("w_logits", _vp), ("logits", _vp), ("x", _vp), ("h", _vp), ("z", _vp), ("attn", _vp),
         ("ff", _vp), ("qkv", _vp), ("workspace", _vp), ("workspace_bytes", _sz),
+        ("parts", ctypes.c_int),
     ]
 
 
@@ -660,9 +662,11 @@ class T2SDecode:
     """One whole decode step (embedding, every layer's GEMVs / attention / LayerNorms, logits)
     over torch buffers; recorded into a graph unless graph=False. `m` holds the model tensors:
     table, pe, alpha, heads, layers (list of dicts with the gsvk_t2s_layer names), w_logits (or
-    None); `io` holds ids, pos, kv_pos, err and the activations x, h, z, attn, ff, qkv, logits."""
+    None); `io` holds ids, pos, kv_pos, err and the activations x, h, z, attn, ff, qkv, logits.
+    split=False runs a batch of 32 or more as one chain of launches instead of two concurrent
+    halves (desc.parts = 1)."""
 
-    def __init__(self, m, io, eps=1e-5, len_bound=0, graph=True):
+    def __init__(self, m, io, eps=1e-5, len_bound=0, graph=True, split=True):
         import torch
         self.m, self.io = m, io
         layers = m["layers"]
@@ -693,8 +697,9 @@ class T2SDecode:
         d.logits = _ptr(io.get("logits"))
         for name in ("x", "h", "z", "attn", "ff", "qkv"):
             setattr(d, name, _ptr(io[name]))
-        need = lib().gsvk_decode_attention_workspace_bytes(B, m["heads"], D // m["heads"],
-                                                           len_bound or d.max_len)
+        d.parts = 0 if split else 1
+        need = lib().gsvk_t2s_decode_workspace_bytes(B, m["heads"], D // m["heads"],
+                                                     len_bound or d.max_len)
         if need:
             ws = workspace(io["x"].device, need)
             d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()

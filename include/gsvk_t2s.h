@@ -155,13 +155,25 @@ typedef struct gsvk_t2s_decode_desc {
   void* attn;/* [B, D]  */
   void* ff;  /* [B, FF] */
   float* qkv;/* [B, 3D] */
-  void* workspace;         /* gsvk_decode_attention_workspace_bytes(batch, heads, D/heads, len) */
+  void* workspace;         /* gsvk_t2s_decode_workspace_bytes(batch, heads, D/heads, len)     */
   size_t workspace_bytes;
+  int parts;               /* 0: two halves when batch >= 32, else one chain; 1: one chain    */
 } gsvk_t2s_decode_desc;
 
+/* With parts 0 a batch of 32 sequences or more runs as two halves, when the workspace holds both
+ * halves' attention states (gsvk_t2s_decode_workspace_bytes; otherwise as one chain): every launch
+ * is row-local, so each half is the same chain of launches over its rows, and the graph records the
+ * two chains on two branches that run concurrently (one half's latency-bound GEMVs overlap the
+ * other half's cache scan). An eager step issues the two chains one after the other on `stream`:
+ * the same launches, the same bits. */
 int gsvk_t2s_decode_eager(const gsvk_t2s_decode_desc* desc, void* stream);
 /* Records one step into a HIP graph; run / launches / destroy with the gsvk_t2s_step calls. */
 int gsvk_t2s_decode_create(const gsvk_t2s_decode_desc* desc, gsvk_t2s_step** out);
+/* Workspace bytes for a step of `batch` sequences (len_bound as in the desc; 0 = any length):
+ * the larger of what one chain and the two halves' attention calls need. No counterpart in the
+ * reference (its attention keeps no chunk states). */
+size_t gsvk_t2s_decode_workspace_bytes(size_t batch, size_t heads, size_t head_dim,
+                                       size_t len_bound);
 
 #ifdef __cplusplus
 }

@@ -174,6 +174,36 @@ def test_attention_validation(gsvk_lib):
     assert gsvk_lib.gsvk_decode_attention_workspace_bytes(64, 16, 32, 1024) > 0
 
 
+def test_t2s_decode_workspace_and_parts(gsvk_lib):
+    att = gsvk_lib.gsvk_decode_attention_workspace_bytes
+    dec = gsvk_lib.gsvk_t2s_decode_workspace_bytes
+    assert dec(0, 16, 32, 1024) == 0
+    # below 32 sequences one chain: the attention call's own workspace
+    assert dec(31, 16, 32, 1024) == att(31, 16, 32, 1024)
+    # two halves: each half's chunk states, the first slice rounded up to 256 bytes
+    for B, lb in ((64, 1024), (64, 0), (37, 200), (33, 5000)):
+        h0 = att(B // 2, 16, 32, lb)
+        need = (h0 + 255) // 256 * 256 + att(B - B // 2, 16, 32, lb)
+        assert dec(B, 16, 32, lb) == max(need, att(B, 16, 32, lb)), (B, lb)
+    assert dec(64, 16, 32, 1024) > att(64, 16, 32, 1024)  # halves split their keys finer
+    # parts outside {0, 1}: E_ARG before anything runs (fake, never dereferenced pointers)
+    fake = 0x10000000
+    lay = (gsvk.T2SLayer * 1)()
+    for name, _ in gsvk.T2SLayer._fields_:
+        setattr(lay[0], name, fake)
+    d = gsvk.T2SDecodeDesc()
+    d.dtype = d.kv_dtype = gsvk.F16
+    d.batch, d.d_model, d.heads, d.ffn, d.layers, d.max_len = 64, 512, 16, 2048, 1, 64
+    d.layer = ctypes.cast(lay, ctypes.POINTER(gsvk.T2SLayer))
+    for name in ("x", "h", "z", "attn", "ff", "qkv", "kv_pos"):
+        setattr(d, name, fake)
+    d.parts = 2
+    assert gsvk_lib.gsvk_t2s_decode_eager(ctypes.byref(d), None) == gsvk.E_ARG
+    out = ctypes.c_void_p()
+    assert gsvk_lib.gsvk_t2s_decode_create(ctypes.byref(d), ctypes.byref(out)) == gsvk.E_ARG
+    assert not out.value
+
+
 def test_conv_validation(gsvk_lib):
     f = gsvk_lib.gsvk_conv1d
     n = gsvk_lib.gsvk_conv1d_packed_elems(8, 16, 3)

@@ -159,3 +159,62 @@ def test_decode_step_t2s_shape_four_layers():
     step.run()
     torch.cuda.synchronize()
     compare(host(iod["x"], F16), host(iod["logits"], F32), x_want, lg_want, "T2S shape")
+
+
+def test_decode_step_two_halves_equal_one_chain():
+    """A batch of 32 or more runs as two halves on two graph branches when the workspace holds both
+    halves' attention states. 37 sequences (halves of 18 and 19) with 200 cached keys: the
+    attention's key chunks depend only on the length there, so the halves give exactly the bits of
+    the one-chain step (split=False), graph and eager, and both match the oracle chain."""
+    FF = 256
+    m, io = build(B=37, D=128, H=4, FF=FF, L=2, V=50, max_len=256, seed=4)
+    io["kv_pos"][:] = np.random.default_rng(99).integers(150, 200, 37)
+    x_want, lg_want = oracle_step({**m, "layers": [dict(ly, k_cache=ly["k_cache"].copy(),
+                                                        v_cache=ly["v_cache"].copy())
+                                                   for ly in m["layers"]]}, io)
+    outs = {}
+    for split, graph in ((False, True), (True, True), (True, False)):
+        md, iod = to_device(m, io, FF)
+        step = gsvk.T2SDecode(md, iod, len_bound=200, graph=graph, split=split)
+        if graph:
+            # gather, 2 layers x (QKV, attention, merge, out-proj, W1, W2), logits: per chain
+            assert step.launches == (2 if split else 1) * (1 + 6 * 2 + 1), step.launches
+        step.run()
+        torch.cuda.synchronize()
+        assert int(iod["err"].item()) == 0
+        outs[(split, graph)] = (host(iod["x"], F16), host(iod["logits"], F32),
+                                [host(ly["k_cache"], F16) for ly in md["layers"]])
+        step.close()
+    ref = outs[(False, True)]
+    compare(ref[0], ref[1], x_want, lg_want, "one chain")
+    for key in ((True, True), (True, False)):
+        x, lg, kc = outs[key]
+        assert np.array_equal(x, ref[0]), key
+        assert np.array_equal(lg.view(np.uint32), ref[1].view(np.uint32)), key
+        for a, b in zip(kc, ref[2]):
+            assert np.array_equal(a, b), key
+
+
+def test_decode_step_t2s_shape_halves_match_oracle():
+    """B = 64 at the real shapes with 1000 cached keys: the two halves (each attention call splits
+    its keys into more chunks than the whole batch's would) against the oracle chain, and their
+    graph replay against their eager run, bit for bit."""
+    FF = 2048
+    m, io = build(B=64, D=512, H=16, FF=FF, L=2, V=1025, max_len=1024, seed=5)
+    io["kv_pos"][:] = np.random.default_rng(98).integers(900, 1000, 64)
+    x_want, lg_want = oracle_step({**m, "layers": [dict(ly, k_cache=ly["k_cache"].copy(),
+                                                        v_cache=ly["v_cache"].copy())
+                                                   for ly in m["layers"]]}, io)
+    got = []
+    for graph in (True, False):
+        md, iod = to_device(m, io, FF)
+        step = gsvk.T2SDecode(md, iod, len_bound=1000, graph=graph)
+        if graph:
+            assert step.launches == 2 * (1 + 6 * 2 + 1), step.launches
+        step.run()
+        torch.cuda.synchronize()
+        got.append((host(iod["x"], F16), host(iod["logits"], F32)))
+        step.close()
+    compare(got[0][0], got[0][1], x_want, lg_want, "halves, T2S shape")
+    assert np.array_equal(got[0][0], got[1][0])
+    assert np.array_equal(got[0][1].view(np.uint32), got[1][1].view(np.uint32))
