@@ -317,6 +317,29 @@ def kernel_suite(torch, gsvk, dev, only=None):
     st_, rp_, b_, ub_ = prefill_case(512)
     run("embed_pe_prefill_pos0_511_2x512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_,
         rows=lambda k: 1024 * k)
+
+    def prefill_input_case(rep):
+        """The same prefill input as one launch (gsvk_t2s_prefill_input): xy [1024, 512] f16 = 512
+        text rows and 512 prompt rows at positions 0..511, each PE row read once for both. The
+        replicated case is one call over 512 * rep positions with a PE table of as many rows, so
+        every PE row is read from HBM exactly once; its floor counts the ids, both output rows and
+        the PE row per position, and the tables once."""
+        def make(k):
+            n = 512 * k
+            tp, ts = rn(732, D, std=0.02), rn(VOCAB, D, std=0.02)
+            ip = torch.randint(0, 732, (n,), device=dev, generator=g)
+            isem = torch.randint(0, VOCAB, (n,), device=dev, generator=g)
+            pe_k = pe if k == 1 else rn(n, D, dtype=f32)
+            xy = torch.empty(2 * n, D, dtype=f16, device=dev)
+            return lambda: gsvk.t2s_prefill_input(tp, ip, 0.93, ts, isem, 1.07, pe_k, xy)
+        per = lambda k: 1024 * k * (8 + 2 * D + 2 * D) + 512 * k * 4 * D
+        floor = lambda k: (512 * k * (16 + 2 * 2 * D + 4 * D) + (732 + VOCAB) * D * 2 if k > 1
+                           else per(1))
+        return (lambda: make(1), lambda: (rep, make(rep)), per, floor)
+
+    st_, rp_, b_, ub_ = prefill_input_case(512)
+    run("t2s_prefill_input_pos0_511_2x512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_,
+        rows=lambda k: 1024 * k)
     run_emb("embed_pe_decode_64x512", 64, 8192)
 
     def text_case(rows, rep):

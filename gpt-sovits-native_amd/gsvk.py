@@ -37,6 +37,8 @@ SIGNATURES = {
     "gsvk_decode_attention": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz, _sz,
                                    _sz, _vp, _sz, _vp, _vp]),
     "gsvk_decode_attention_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
+    "gsvk_t2s_prefill_input": (_i, [_i, _i, _i, _vp, _sz, _vp, _sz, _vp, _vp, _f, _vp, _sz, _vp,
+                                    _sz, _f, _vp, _sz, _vp, _sz, _vp, _vp]),
     "gsvk_decode_attention_noalloc": (_i, [_i, _i, _vp, _sz, _vp, _vp, _sz, _vp, _vp, _sz, _sz, _sz,
                                            _sz, _sz, _vp, _vp]),
     "gsvk_conv1d": (_i, [_i, _i, _vp, _sz, _vp, _vp, _i, _f, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
@@ -543,6 +545,23 @@ def embed_pe(table, ids, pe, alpha, out, pos=None, pos0=0, mm=None, bias=None, e
                                       _ptr(ids), _ptr(pos), pos0, _ptr(pe), max_pos, alpha,
                                       _ptr(mm), _ptr(bias), _ptr(out), ids.numel(), D, _ptr(err),
                                       _stream(stream)))
+
+
+def t2s_prefill_input(text_table, phones, alpha_text, audio_table, prompt, alpha_audio, pe, xy,
+                      mm=None, bias=None, err=None, stream=None):
+    """xy [T + P, D]: the text rows (phones, positions 0..T-1, optional bert_proj rows mm and bias)
+    then the prompt rows (prompt ids, positions 0..P-1), one launch."""
+    import torch
+    T, P = phones.numel(), prompt.numel()
+    D = xy.shape[1]
+    assert xy.shape[0] == T + P and phones.dtype == prompt.dtype
+    itype = I32 if phones.dtype == torch.int32 else I64
+    return _check("gsvk_t2s_prefill_input",
+                  lib().gsvk_t2s_prefill_input(
+                      dtype_code(xy), dtype_code(text_table), itype, _ptr(text_table),
+                      text_table.shape[0], _ptr(phones), T, _ptr(mm), _ptr(bias), alpha_text,
+                      _ptr(audio_table), audio_table.shape[0], _ptr(prompt), P, alpha_audio,
+                      _ptr(pe), pe.shape[0], _ptr(xy), D, _ptr(err), _stream(stream)))
 
 
 def pe_table(max_pos, D):

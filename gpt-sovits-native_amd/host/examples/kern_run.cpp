@@ -17,6 +17,7 @@
 //   gsv::bert::LayerNorm1D{g, b, 1e-12}.forward(Matrix x)         R * N    (bert_ops.hpp:269)
 //   leaky_relu_io(t.d.data(), t.d.size(), 0.01) on Tensor2D t(3, M / 3) of v   3 * (M / 3)
 //   gsv::ar::PeRows{N}.pe_row(pe, p), p = 0, 1, 7, 166, 1234, 2047 6 * N   (t2s_engine.hpp:187)
+//   gsv::ar::prefill_input(...) (the block at t2s_engine.cpp:1770-1786)      4 R * N
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -119,6 +120,30 @@ int main(int argc, char** argv) {
         rows.pe_row(pe.data(), p);
         out.insert(out.end(), pe.begin(), pe.end());
       }
+    }
+    {
+      // gsv::ar::prefill_input: both tables are the fp16 rounding of x's R rows, text ids t mod R,
+      // prompt ids R - 1 - (t mod R), T = P = 2R; the bert_proj rows already in xy are w's first
+      // 2R N values, bias b, alphas 0.75 / 1.25, PE rows 0 .. 2R - 1 of the 2048-row table.
+      const size_t T = 2 * R, P = 2 * R;
+      if (M < T * N) throw std::runtime_error("prefill_input needs M >= 2 R N");
+      DeviceVector<uint16_t> tab(R * N);
+      gsvk::check(gsvk_f32_to_f16(X.data(), tab.data(), R * N, gsvk::current_stream()),
+                  "gsvk_f32_to_f16");
+      std::vector<int64_t> ph(T), pr(P);
+      for (size_t t = 0; t < T; ++t) ph[t] = static_cast<int64_t>(t % R);
+      for (size_t t = 0; t < P; ++t) pr[t] = static_cast<int64_t>(R - 1 - t % R);
+      DeviceVector<int64_t> PH, PR;
+      PH.copy_from_host(ph.data(), T);
+      PR.copy_from_host(pr.data(), P);
+      std::vector<float> pe_host(2048 * N);
+      gsv::ar::pe_table(pe_host.data(), 2048, N);
+      DeviceVector<float> PE = upload(pe_host.data(), 2048 * N), XY((T + P) * N);
+      XY.copy_from_host(w, T * N);
+      XY.resize((T + P) * N);
+      gsv::ar::prefill_input(tab.data(), R, PH.data(), T, B.data(), 0.75f, tab.data(), R, PR.data(),
+                             P, 1.25f, PE.data(), 2048, XY.data(), N);
+      append(out, XY, (T + P) * N);
     }
     std::ofstream o(argv[2], std::ios::binary);
     if (!o.write(reinterpret_cast<const char*>(out.data()),

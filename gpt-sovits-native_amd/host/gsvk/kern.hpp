@@ -434,4 +434,20 @@ inline void embed_pe(const uint16_t* table_f16, size_t vocab, const int64_t* ids
               "gsv::ar::embed_pe");
 }
 
+// The prefill input xy[T + P, D] of T2SEngine::generate (t2s_engine.cpp:1770-1786) in one launch:
+// text rows xy[t] += (text_emb[phones[t]] + bert_b) then += alpha_text * pe(t), over the bert_proj
+// rows already in xy (the reference's order), then prompt rows xy[T + t] = audio_emb[prompt[t]] +
+// alpha_audio * pe(t). fp32 activations, fp16 tables, int64 ids, device pointers.
+inline void prefill_input(const uint16_t* text_emb_f16, size_t text_vocab, const int64_t* phones,
+                          size_t T, const float* bert_b, float alpha_text,
+                          const uint16_t* audio_emb_f16, size_t audio_vocab,
+                          const int64_t* prompt, size_t P, float alpha_audio, const float* pe,
+                          size_t max_pos, float* xy, size_t D, int32_t* err = nullptr) {
+  gsvk::check(gsvk_t2s_prefill_input(GSVK_F32, GSVK_F16, GSVK_I64, text_emb_f16, text_vocab,
+                                     phones, T, xy, bert_b, alpha_text, audio_emb_f16,
+                                     audio_vocab, prompt, P, alpha_audio, pe, max_pos, xy, D, err,
+                                     gsvk::current_stream()),
+              "gsv::ar::prefill_input");
+}
+
 }  // namespace gsv::ar

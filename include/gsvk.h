@@ -345,6 +345,26 @@ int gsvk_embed_pe(int out_dtype, int table_dtype, int index_type, const void* ta
                   size_t rows, size_t D, int32_t* err, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * The T2S prefill input xy [T + P, D] in one launch: the text rows and the prompt rows, which both
+ * take positions 0, 1, ... (T2SEngine::generate, t2s_engine.cpp:1770-1786):
+ *   xy[t, :]     = fmaf(alpha_text,  pe[t, :], mm[t, :] + (e_text[phones[t]] (+ bias)))  t < T
+ *   xy[T + t, :] = fmaf(alpha_audio, pe[t, :], e_audio[prompt[t]])                       t < P
+ * Each output row has the bits of gsvk_embed_pe with pos0 = 0 (mm / bias: the text form, as there;
+ * mm may be NULL). The PE row of position t is read once for both rows. mm is the bert_proj output
+ * [T, D] in out_dtype: xy itself (the reference writes it into xy first, t2s_engine.cpp:1772) or a
+ * buffer that does not overlap xy. Both tables have table_dtype, phones / prompt index_type.
+ * Out-of-range ids and positions >= max_pos write NaN rows and set *err, as gsvk_embed_pe.
+ * D must be even; rows that are not 16-byte aligned, or D % 8 != 0, run as two gsvk_embed_pe
+ * launches (the same results).
+ * ------------------------------------------------------------------------------------------------ */
+int gsvk_t2s_prefill_input(int out_dtype, int table_dtype, int index_type, const void* text_table,
+                           size_t text_vocab, const void* phones, size_t T, const void* mm,
+                           const float* bias, float alpha_text, const void* audio_table,
+                           size_t audio_vocab, const void* prompt, size_t P, float alpha_audio,
+                           const float* pe, size_t max_pos, void* xy, size_t D, int32_t* err,
+                           void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Host helper: the sinusoidal PE table, row p = T2SEngine::pe_row(pe, p) (t2s_engine.cpp:711-720):
  *   log_inc = float(-ln(10000)/D); div = expf(float(d)*log_inc); pe[2i] = sinf(p*div),
  *   pe[2i+1] = cosf(p*div), all in fp32. host_out holds max_pos * D floats. Host memory, no GPU.

@@ -291,6 +291,31 @@ def test_embed_validation(gsvk_lib):
     assert call(outp=C + 16) == gsvk.E_ALIAS     # writes over the PE table
 
 
+def test_prefill_input_validation(gsvk_lib):
+    f = gsvk_lib.gsvk_t2s_prefill_input
+    args = dict(out=1, tab=1, it=0, ttab=A, tv=10, ph=B, T=4, mm=None, bias=None, at=1.0,
+                atab=A + 4096, av=10, pr=B + 64, P=4, aa=1.0, pe=C, max_pos=8, xy=0x900000,
+                D=8, err=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return f(a["out"], a["tab"], a["it"], a["ttab"], a["tv"], a["ph"], a["T"], a["mm"],
+                 a["bias"], a["at"], a["atab"], a["av"], a["pr"], a["P"], a["aa"], a["pe"],
+                 a["max_pos"], a["xy"], a["D"], a["err"], None)
+
+    assert call(out=7) == gsvk.E_DTYPE
+    assert call(it=2) == gsvk.E_DTYPE
+    assert call(atab=None) == gsvk.E_NULL
+    assert call(ph=None) == gsvk.E_NULL           # T > 0 needs phones
+    assert call(T=0, P=0) == gsvk.E_SIZE
+    assert call(max_pos=0) == gsvk.E_SIZE
+    assert call(T=1 << 35) == gsvk.E_SIZE
+    assert call(D=7) == gsvk.E_ARG
+    assert call(xy=A) == gsvk.E_ALIAS             # over the text table
+    assert call(xy=C + 16) == gsvk.E_ALIAS        # over the PE table
+    assert call(mm=0x900000 + 64) == gsvk.E_ALIAS  # bert_proj rows partly over xy (not xy itself)
+
+
 def test_f32_to_f16_validation(gsvk_lib):
     f = gsvk_lib.gsvk_f32_to_f16
     assert f(None, 0x1000, 8, None) == gsvk.E_NULL

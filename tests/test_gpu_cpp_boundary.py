@@ -2,7 +2,7 @@
 buffers: host/examples/kern_run calls gsv::kern::layernorm / layernorm_rows / relu,
 gsv::sovits::leaky_relu_io / leaky_relu_write / add_inplace / add_scaled_inplace / mul_write,
 gsv::bert::LayerNorm1D::forward(Matrix&), a Tensor2D-backed leaky_relu_io and
-gsv::ar::PeRows::pe_row exactly as the reference's engines call them (kern.hpp:25, 33;
+gsv::ar::PeRows::pe_row and gsv::ar::prefill_input exactly as the reference's engines call them (kern.hpp:25, 33;
 nn_ops.hpp:48-105; bert_ops.hpp:261-286; sovits_types.hpp:21-36; t2s_engine.hpp:187), in its own
 process. Every output is checked against the oracle: bit-exact for ReLU, LeakyReLU, the adds and
 the PE rows; the LayerNorms within the fp32 tolerance (1e-6 + 1e-5 |want|)."""
@@ -14,7 +14,7 @@ import pytest
 
 import gsvk
 import oracle as O
-from gpu_util import F32, assert_bitexact, assert_close, say
+from gpu_util import F16, F32, assert_bitexact, assert_close, say
 
 pytestmark = pytest.mark.gpu
 
@@ -23,7 +23,7 @@ EXE = os.path.join(os.path.dirname(gsvk.LIB_PATH), "kern_run")
 
 def test_cpp_kernel_layer_on_device_buffers(tmp_path):
     assert os.path.exists(EXE), "kern_run is not built (make -C gpt-sovits-native_amd)"
-    R, N, M = 4, 512, 3001
+    R, N, M = 4, 512, 4101
     r = np.random.default_rng(20250823 + 77)
     x = (r.standard_normal((R, N)) * 1.5 + 0.25).astype(np.float32)
     g = (1 + 0.1 * r.standard_normal(N)).astype(np.float32)
@@ -40,7 +40,7 @@ def test_cpp_kernel_layer_on_device_buffers(tmp_path):
                          text=True, timeout=120)
     assert res.returncode == 0, res.stderr
     out = np.fromfile(dst, dtype=np.float32)
-    sizes = [N, R * N, M, M, M, M, M, M, R * N, 3 * (M // 3), 6 * N]
+    sizes = [N, R * N, M, M, M, M, M, M, R * N, 3 * (M // 3), 6 * N, 4 * R * N]
     assert out.size == sum(sizes)
     parts = np.split(out, np.cumsum(sizes)[:-1])
 
@@ -63,3 +63,14 @@ def test_cpp_kernel_layer_on_device_buffers(tmp_path):
     table = O.pe_table(2048, N)
     for i, p in enumerate((0, 1, 7, 166, 1234, 2047)):
         assert np.array_equal(pe[i].view(np.uint32), table[p].view(np.uint32)), f"pe_row({p})"
+    # prefill_input: text rows over the bert_proj rows in place, then prompt rows, bit-exact
+    T = P = 2 * R
+    tab16 = x.astype(np.float16).view(np.uint16)
+    ph = (np.arange(T) % R).astype(np.int64)
+    pr = (R - 1 - np.arange(P) % R).astype(np.int64)
+    want_t, _ = O.embed_pe(F32, F16, tab16, ph, table, 0.75, pos0=0,
+                           mm=w[:T * N].reshape(T, N).copy(), bias=b)
+    want_a, _ = O.embed_pe(F32, F16, tab16, pr, table, 1.25, pos0=0)
+    xy = parts[11].reshape(T + P, N)
+    assert_bitexact(F32, xy[:T], want_t, "prefill_input text rows")
+    assert_bitexact(F32, xy[T:], want_a, "prefill_input prompt rows")

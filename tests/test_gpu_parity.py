@@ -8,7 +8,8 @@ import torch
 
 import gsvk
 import oracle as O
-from gpu_util import (ALL_DT, BF16, F16, F32, assert_bitexact, assert_close, dev, devf, host, say)
+from gpu_util import (ALL_DT, BF16, F16, F32, TORCH_DT, assert_bitexact, assert_close, dev, devf,
+                      host, say)
 
 pytestmark = pytest.mark.gpu
 
@@ -418,6 +419,85 @@ def test_embed_config2_bit_exact(out_dt, pe2048):
                   pos=torch.from_numpy(dec_pos).cuda())
     sync()
     assert_bitexact(out_dt, host(OUT2, out_dt), want, "decode rows")
+
+
+PREFILL_CASES = [
+    # (out dtype, T, P, D, text rows with bert_proj rows mm in place / apart / none, bias, int32)
+    (F16, 512, 512, 512, "inplace", True, False),   # configuration 2's prefill input
+    (F32, 512, 512, 512, "apart", True, True),
+    (BF16, 512, 512, 512, None, False, False),
+    (F16, 300, 77, 512, "inplace", True, False),    # more text than prompt rows
+    (F16, 5, 260, 256, "apart", False, True),       # more prompt rows, narrower model
+    (F32, 33, 40, 1024, "inplace", True, False),    # two column blocks per lane
+    (F16, 9000, 8500, 512, "inplace", True, False), # the multi-position wave path
+    (F16, 20, 10, 6, "apart", True, False),         # D % 8 != 0: two gather launches
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_prefill_input_equals_two_gathers_bit_exact(case, pe2048):
+    """gsvk_t2s_prefill_input: every text row and every prompt row has the bits of the oracle's
+    gather of that row (the two reference loops, t2s_engine.cpp:1774-1786)."""
+    out_dt, T, P, D, mm_kind, use_bias, i32 = case
+    say(f"prefill input {case}")
+    r = rng(220 + T + P + D)
+    pe = pe2048 if D == 512 and max(T, P) <= 2048 else gsvk.pe_table(max(T, P), D)
+    text_tab = (0.02 * r.standard_normal((732, D))).astype(np.float16).view(np.uint16)
+    audio_tab = (0.02 * r.standard_normal((1025, D))).astype(np.float16).view(np.uint16)
+    a_text, a_audio = (float(np.float32(v)) for v in r.uniform(0.5, 1.5, 2))
+    idt = np.int32 if i32 else np.int64
+    phones = r.integers(0, 732, T).astype(idt)
+    prompt = r.integers(0, 1025, P).astype(idt)
+    mm = st(out_dt, r.standard_normal((T, D))) if mm_kind else None
+    bert_b = (0.02 * r.standard_normal(D)).astype(np.float32) if use_bias else None
+    want_t, bad_t = O.embed_pe(out_dt, F16, text_tab, phones, pe, a_text, pos0=0, mm=mm,
+                               bias=bert_b)
+    want_a, bad_a = O.embed_pe(out_dt, F16, audio_tab, prompt, pe, a_audio, pos0=0)
+    assert bad_t == 0 and bad_a == 0
+    XY = torch.empty((T + P, D), dtype=TORCH_DT[out_dt], device="cuda")
+    MM = None
+    if mm_kind == "inplace":
+        XY[:T].copy_(dev(mm, out_dt))
+        MM = XY
+    elif mm_kind == "apart":
+        MM = dev(mm, out_dt)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    gsvk.t2s_prefill_input(dev(text_tab, F16), torch.from_numpy(phones).cuda(), a_text,
+                           dev(audio_tab, F16), torch.from_numpy(prompt).cuda(), a_audio,
+                           devf(pe), XY, mm=MM, bias=None if bert_b is None else devf(bert_b),
+                           err=err)
+    sync()
+    got = host(XY, out_dt)
+    assert int(err.item()) == 0
+    assert_bitexact(out_dt, got[:T], want_t, "text rows")
+    assert_bitexact(out_dt, got[T:], want_a, "prompt rows")
+
+
+def test_prefill_input_out_of_range_rows(pe2048):
+    """Bad ids in either gather, and positions past the PE table, give NaN rows and the flag; the
+    other rows keep their bits."""
+    r = rng(230)
+    D, T, P = 512, 40, 30
+    pe = pe2048[:35]  # positions 35.. are outside the table
+    text_tab = (0.02 * r.standard_normal((100, D))).astype(np.float16).view(np.uint16)
+    audio_tab = (0.02 * r.standard_normal((100, D))).astype(np.float16).view(np.uint16)
+    phones = r.integers(0, 100, T).astype(np.int64)
+    prompt = r.integers(0, 100, P).astype(np.int64)
+    phones[[3, 7]] = [100, -2]
+    prompt[5] = 1000
+    want_t, bad_t = O.embed_pe(F16, F16, text_tab, phones, pe, 0.7, pos0=0)
+    want_a, bad_a = O.embed_pe(F16, F16, audio_tab, prompt, pe, 0.9, pos0=0)
+    assert bad_t == 2 + (T - 35) and bad_a == 1
+    XY = torch.empty((T + P, D), dtype=torch.float16, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    gsvk.t2s_prefill_input(dev(text_tab, F16), torch.from_numpy(phones).cuda(), 0.7,
+                           dev(audio_tab, F16), torch.from_numpy(prompt).cuda(), 0.9, devf(pe), XY,
+                           err=err)
+    sync()
+    assert int(err.item()) == 1
+    got = host(XY, F16)
+    assert_bitexact(F16, got[:T], want_t, "text rows")
+    assert_bitexact(F16, got[T:], want_a, "prompt rows")
 
 
 def test_embed_out_of_range_sets_flag_and_nan_rows(pe2048):
