@@ -16,10 +16,10 @@
 // columns the taps reach past the tile, is staged once in LDS and read k times, once per tap at
 // shift kk dil: layout [plane][channel group g = 0..3][t][8 channels], so a fragment read is 16
 // consecutive 16-byte rows (no bank conflicts) and the tap shift is a row offset. The weights are
-// packed once (gsvk_conv1d_pack) as [chunk][tap][o][32 channels]: the B fragment of one step is 16
-// rows x 64 contiguous bytes straight from global memory (L1 / L2: the whole filter bank is at most
-// a few MB and every workgroup reads it), loaded two steps ahead of its use. The next chunk of x is
-// loaded into registers while the current one is multiplied.
+// packed once (gsvk_conv1d_pack) as [chunk][tap][channel group][o][8 channels] and staged through
+// LDS in groups of kTapGroup taps of a chunk, laid out like x (a B fragment read is 16 consecutive
+// 16-byte rows); each group's weights are loaded into registers while the group before it
+// multiplies, and the next chunk of x while the current chunk's first group does.
 //
 // x in fp32: round_x = 1 rounds it to fp16 (the reference's AMX packing, im2col_to_panel_f16);
 // round_x = 0 keeps fp32 (the reference's default sgemm path) by multiplying hi = f16(x) and
