@@ -218,3 +218,30 @@ def test_decode_step_t2s_shape_halves_match_oracle():
     compare(got[0][0], got[0][1], x_want, lg_want, "halves, T2S shape")
     assert np.array_equal(got[0][0], got[1][0])
     assert np.array_equal(got[0][1].view(np.uint32), got[1][1].view(np.uint32))
+
+
+def test_decode_step_two_halves_without_positions():
+    """With no PE position array every row r takes position r; the second half's rows then start at
+    position B / 2. Halves and one chain, graph and eager, give the same bits."""
+    FF = 256
+    m, io = build(B=40, D=128, H=4, FF=FF, L=1, V=50, max_len=256, seed=6)
+    io["kv_pos"][:] = np.random.default_rng(97).integers(100, 200, 40)
+    outs = []
+    for split, graph in ((False, True), (True, True), (True, False)):
+        md, iod = to_device(m, io, FF)
+        iod["pos"] = None
+        step = gsvk.T2SDecode(md, iod, len_bound=200, graph=graph, split=split)
+        step.run()
+        torch.cuda.synchronize()
+        assert int(iod["err"].item()) == 0
+        outs.append((host(iod["x"], F16), host(iod["logits"], F32)))
+        step.close()
+    for x, lg in outs[1:]:
+        assert np.array_equal(x, outs[0][0])
+        assert np.array_equal(lg.view(np.uint32), outs[0][1].view(np.uint32))
+    # and the one chain against the oracle with positions 0..B-1
+    x_want, lg_want = oracle_step({**m, "layers": [dict(ly, k_cache=ly["k_cache"].copy(),
+                                                        v_cache=ly["v_cache"].copy())
+                                                   for ly in m["layers"]]},
+                                  dict(io, pos=np.arange(40, dtype=np.int64)))
+    compare(outs[0][0], outs[0][1], x_want, lg_want, "no position array")
