@@ -726,6 +726,17 @@ def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
     ms, ms_one = statistics.median(t_split), statistics.median(t_one)
     one_launches = one.launches
     one.close()
+    # One half of the batch alone (the first 32 sequences as one chain): how much of the step is
+    # the chain's launch latency rather than its rows.
+    sl = slice(0, B // 2)
+    half = gsvk.T2SDecode(
+        dict(m, layers=[dict(ly, k_cache=ly["k_cache"][sl], v_cache=ly["v_cache"][sl])
+                        for ly in layers]),
+        {n: (t[sl] if n != "err" else t) for n, t in io.items()}, len_bound=max_len, graph=True)
+    for _ in range(warmup):
+        half.run()
+    ms_half = statistics.median(time_loop(torch, half.run, steps) for _ in range(3))
+    half.close()
     assert int(io["err"].item()) == 0
     # algorithmic bytes: every weight and parameter once, the kv_len cached rows of K and V per
     # layer once, the appended rows, and each activation read / written once
@@ -738,11 +749,13 @@ def full_decode_step(torch, gsvk, dev, kv_len=1024, steps=50, warmup=5):
            "kv_len": kv_len, "storage": "f16", "kv_storage": "f16", "launches": step.launches,
            "us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(B / ms * 1e3, 0),
            "one_chain_us_per_step": round(ms_one * 1e3, 1), "one_chain_launches": one_launches,
+           "half_batch_chain_us_per_step": round(ms_half * 1e3, 1),
            "bytes_per_step": nbytes, "GBps": round(nbytes / ms / 1e6, 1),
            "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_GBS, 4)}
     log(f"  whole decode step (B={B}, kv_len={kv_len}, graph of {step.launches} launches): "
         f"{out['us_per_step']} us, {out['tokens_per_s']:.0f} tokens/s, {out['GBps']} GB/s; "
-        f"as one chain of {one_launches} launches {out['one_chain_us_per_step']} us")
+        f"as one chain of {one_launches} launches {out['one_chain_us_per_step']} us; "
+        f"half the batch alone {out['half_batch_chain_us_per_step']} us")
     step.close()
     del m, io, layers
     torch.cuda.empty_cache()

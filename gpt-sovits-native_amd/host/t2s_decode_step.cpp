@@ -133,11 +133,11 @@ int issue_rows(const gsvk_t2s_decode_desc* d, size_t b0, size_t n, void* ws, siz
 
 // The batch in two parts. At decode sizes every launch but the attention scan is bound by latency,
 // not bandwidth, so the two parts' launch chains are recorded on two streams of one graph, which
-// the runtime issues on two hardware queues. Measured on the whole step (B = 64, 24 layers): 1098
-// -> 1082-1092 us at 1024 cached keys and 1548-1555 -> 1457-1461 us at 2048. The queues overlap
-// little: two graph branches, four attention calls (B = 32, 2048 keys, 104 us) beside 24 W1 GEMVs
-// (71 us), took 144-155 us against 172 us in one branch. Batches of fewer than kSplitRows
-// sequences, and workspaces too small for both parts' attention states, run as one part.
+// the runtime issues on two hardware queues and runs side by side. Measured on the whole step
+// (B = 64, 24 layers): 1098 -> 1082-1092 us at 1024 cached keys and 1548-1555 -> 1457-1461 us at
+// 2048. The gain is small because one part's chain alone takes 1023-1049 us: the chain's launch
+// latency, not its rows, sets the step time. Batches of fewer than kSplitRows sequences, and
+// workspaces too small for both parts' attention states, run as one part.
 constexpr size_t kSplitRows = 32;
 constexpr size_t kWsAlign = 256;
 
