@@ -470,8 +470,9 @@ extern "C" int gsvk_t2s_prefill_input(int out_dtype, int table_dtype, int index_
   if (index_type != GSVK_I64 && index_type != GSVK_I32) return GSVK_E_DTYPE;
   if (!text_table || !audio_table || !pe || !xy || (T && !phones) || (P && !prompt))
     return GSVK_E_NULL;
+  // (positions <= 2^24: one wave each, so a launch stays under 2^32 work-items)
   if (T + P == 0 || D == 0 || text_vocab == 0 || audio_vocab == 0 || max_pos == 0 ||
-      T > (1ul << 34) || P > (1ul << 34) || D > (1ul << 30) || text_vocab > (1ul << 40) ||
+      T > (1ul << 24) || P > (1ul << 24) || D > (1ul << 30) || text_vocab > (1ul << 40) ||
       audio_vocab > (1ul << 40) || max_pos > (1ul << 40))
     return GSVK_E_SIZE;
   if (D % 2) return GSVK_E_ARG;

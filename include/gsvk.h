@@ -354,8 +354,8 @@ int gsvk_embed_pe(int out_dtype, int table_dtype, int index_type, const void* ta
  * [T, D] in out_dtype: xy itself (the reference writes it into xy first, t2s_engine.cpp:1772) or a
  * buffer that does not overlap xy. Both tables have table_dtype, phones / prompt index_type.
  * Out-of-range ids and positions >= max_pos write NaN rows and set *err, as gsvk_embed_pe.
- * D must be even; rows that are not 16-byte aligned, or D % 8 != 0, run as two gsvk_embed_pe
- * launches (the same results).
+ * D must be even and T, P at most 2^24; rows that are not 16-byte aligned, or D % 8 != 0, run as
+ * two gsvk_embed_pe launches (the same results).
  * ------------------------------------------------------------------------------------------------ */
 int gsvk_t2s_prefill_input(int out_dtype, int table_dtype, int index_type, const void* text_table,
                            size_t text_vocab, const void* phones, size_t T, const void* mm,

@@ -310,6 +310,7 @@ def test_prefill_input_validation(gsvk_lib):
     assert call(T=0, P=0) == gsvk.E_SIZE
     assert call(max_pos=0) == gsvk.E_SIZE
     assert call(T=1 << 35) == gsvk.E_SIZE
+    assert call(P=(1 << 24) + 1) == gsvk.E_SIZE   # one wave per position: under 2^32 work-items
     assert call(D=7) == gsvk.E_ARG
     assert call(xy=A) == gsvk.E_ALIAS             # over the text table
     assert call(xy=C + 16) == gsvk.E_ALIAS        # over the PE table
