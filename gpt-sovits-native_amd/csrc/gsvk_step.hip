@@ -533,6 +533,8 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
   a.ids32 = d->index_type == GSVK_I32;
   a.tab_dt = d->table_dtype;
   a.layers = static_cast<int>(d->layers);
+  // one-wave workgroups: the launch's work-items (64 per workgroup) must stay under 2^32
+  if (static_cast<size_t>(a.B + a.layers * a.relu_waves_per_layer) >= (1ul << 26)) return GSVK_E_SIZE;
   const float *zeros = nullptr, *ones = nullptr;
   if (!step_fill_rows(&zeros, &ones)) return GSVK_E_HIP;
   auto or_fill = [](const float* p, const float* fill) { return p ? p : fill; };
@@ -547,7 +549,6 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
                        or_fill(at(d->b2, l), zeros),
                        or_fill(at(d->n2g, l), ones),
                        or_fill(at(d->n2b, l), zeros)};
-  if (static_cast<size_t>(a.B + a.layers * a.relu_waves_per_layer) >= (1ul << 31)) return GSVK_E_SIZE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (d->dtype) {
     case GSVK_F32: return launch_step<GSVK_F32>(a, st);

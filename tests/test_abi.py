@@ -338,13 +338,14 @@ def test_t2s_step_validation(gsvk_lib):
     assert gsvk_lib.gsvk_t2s_step_create_fused(None, ctypes.byref(out)) == gsvk.E_NULL
 
 
-def _step_desc(L=24, B=64, D=512, FF=2048, dt=gsvk.F16, base=0x10000000):
+def _step_desc(L=24, B=64, D=512, FF=2048, dt=gsvk.F16, base=0x10000000, gap=1 << 24):
     """A decode-step descriptor over fake, never dereferenced, disjoint 16-byte aligned device
-    addresses (16 MiB apart): the fused entry point must reject every variant below in validation."""
+    addresses (`gap` bytes apart): the fused entry point must reject every variant below in
+    validation."""
     nxt = [base]
 
     def addr():
-        nxt[0] += 1 << 24
+        nxt[0] += gap
         return nxt[0]
     keep = {}
 
@@ -395,6 +396,10 @@ def test_t2s_step_fused_validation(gsvk_lib):
     d, k = _step_desc()
     d.ids = None
     assert f(d) == gsvk.E_NULL
+    # 65,536 sequences with an FFN of 2^20: 24 x 2^25 one-wave ReLU workgroups, past the 2^32
+    # work-items of one launch (buffers 2^40 bytes apart, so no overlap is reported first)
+    d, k = _step_desc(B=1 << 16, FF=1 << 20, gap=1 << 40)
+    assert f(d) == gsvk.E_SIZE
 
 
 def _decoder_desc(frames=500, c0=768, n_stages=5, fake=0x1000):
