@@ -135,7 +135,7 @@ int issue_rows(const gsvk_t2s_decode_desc* d, size_t b0, size_t n, void* ws, siz
 // not bandwidth, so the two parts' launch chains are recorded on two streams of one graph, which
 // the runtime issues on two hardware queues and runs side by side. Measured on the whole step
 // (B = 64, 24 layers): 1098 -> 1082-1092 us at 1024 cached keys and 1548-1555 -> 1457-1461 us at
-// 2048. The gain is small because one part's chain alone takes 1023-1049 us: the chain's launch
+// 2048. The gain is small because one part's chain alone takes 916-1049 us: the chain's launch
 // latency, not its rows, sets the step time. Batches of fewer than kSplitRows sequences, and
 // workspaces too small for both parts' attention states, run as one part.
 constexpr size_t kSplitRows = 32;
