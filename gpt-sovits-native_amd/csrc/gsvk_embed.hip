@@ -1,12 +1,15 @@
 // gsvk_embed.hip — token-embedding gather fused with the scaled sinusoidal positional add (gfx950).
 //
-// One wave64 per output row, one-shot grid: one-wave workgroups for short calls (latency-bound),
-// four-wave workgroups (rows 4b..4b+3) for long ones. The wave reads its id
-// and position once (wave-uniform scalar loads), then each lane moves 8 consecutive columns: the
-// table row chunk (16 B for f16/bf16, 32 B for f32), the PE row chunk (32 B fp32), optionally the mm
-// row chunk and the bias chunk, and writes 8 output columns. Table and PE rows are read through the
-// caches (ids repeat); output rows of calls beyond kStreamBytes are written non-temporally. The arithmetic is the reference's exactly (fmaf is the contraction AppleClang applies to
-// `e + alpha * pe`), so the result is bit-identical to the CPU restatement for every input.
+// Three row kernels. embed_pe_vec (short calls, latency-bound): one wave64 per output row, the
+// wave's id and position read once, then each lane moves 8 consecutive columns: the table row chunk
+// (16 B for f16/bf16, 32 B for f32), the PE row chunk (32 B fp32), optionally the mm row chunk and
+// the bias chunk, and writes 8 output columns. embed_pe_rows (long calls): RPW consecutive rows per
+// wave, their ids and positions read with one vector load, U rows' loads in flight at once.
+// prefill_input_rows (the T2S prefill input): the text row and the prompt row at one position
+// share a single read of the PE row. Table and PE rows are read through the caches (ids repeat);
+// output rows of calls beyond kStreamBytes are written non-temporally. The arithmetic is the
+// reference's exactly (fmaf is the contraction AppleClang applies to `e + alpha * pe`), so the
+// result is bit-identical to the CPU restatement for every input.
 #include "gsvk_common.hpp"
 
 namespace gsvk {
