@@ -16,8 +16,11 @@ __attribute__((visibility("hidden"))) int attention_call(
 
 namespace {
 
-// The chunk states, one copy per GPU, held until the process ends: B x C x 3 KiB for C key chunks
-// (at most 1023 x 3 KiB on a 256-CU device). Every call on a GPU shares its copy. The chunk kernel
+// The chunk states, one copy per GPU, held until the process ends: B x C x 3 KiB for C > 1 key
+// chunks (one chunk needs none). 4 MiB holds 1365 states: on a 256-CU device every batch of up to
+// 256 sequences at any length (B x C <= 256 there) and up to 682 sequences at contexts of at most
+// 256 keys (C <= 2); a call that needs more is rejected (GSVK_E_SIZE). Every call on a GPU shares
+// its copy. The chunk kernel
 // writes every state the merge kernel reads, so nothing needs clearing between calls; two calls in
 // flight at once on one GPU (different streams) race on it.
 constexpr size_t kScratchBytes = size_t(4) << 20;

@@ -193,9 +193,10 @@ size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t 
  * the process ends; the call allocates nothing. Every call on a GPU shares that copy, so calls in
  * flight at once on one GPU (different streams) race on it. Same arguments (minus the workspace)
  * and the same bits as gsvk_decode_attention with a workspace of
- * gsvk_decode_attention_workspace_bytes. GSVK_E_SIZE when the chunk states would exceed 4 MiB
- * (batch x chunks x 3 KiB: at most 1023 x 3 KiB on a 256-CU MI355X, so never there); GSVK_E_HIP
- * when the array's device address cannot be looked up. */
+ * gsvk_decode_attention_workspace_bytes. GSVK_E_SIZE, before any launch, when the chunk states
+ * would exceed 4 MiB (batch x chunks x 3 KiB, 1365 states: on a 256-CU MI355X every batch of up to
+ * 256 sequences fits at any length, and up to 682 sequences at contexts of at most 256 keys);
+ * GSVK_E_HIP when the array's device address cannot be looked up. */
 int gsvk_decode_attention_noalloc(int kv_dtype, int out_dtype, const float* qkv, size_t ldq,
                                   void* k_cache, void* v_cache, size_t max_len, const int64_t* pos,
                                   void* out, size_t ldo, size_t batch, size_t heads,

@@ -43,3 +43,31 @@ def test_noalloc_attention_equals_workspace_form(kv):
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"call {call}: out"
         assert torch.equal(kc2, kc) and torch.equal(vc2, vc), f"call {call}: appended rows"
         assert np.isfinite(got.float().cpu().numpy()).all()
+
+
+def test_noalloc_attention_rejects_states_past_the_array():
+    """4 MiB holds 1365 chunk states of 3 KiB. 700 sequences at contexts of up to 200 keys take two
+    chunks each (1400 states): refused with GSVK_E_SIZE before anything is launched, and the
+    workspace form of the same call still runs. 682 sequences (1364 states) fit."""
+    D, H, L = 512, 16, 200
+    for B, fits in ((682, True), (700, False)):
+        say(f"noalloc attention capacity: B={B} L={L} fits={fits}")
+        need = gsvk.lib().gsvk_decode_attention_workspace_bytes(B, H, D // H, L)
+        assert need == B * 2 * 3072
+        assert (need <= 4 << 20) == fits
+        kc, vc, qkv, pos, H, D = _case(B, L, torch.float16, 950 + B)
+        out = torch.empty(B, D, dtype=torch.float16, device="cuda")
+        if fits:
+            want = torch.empty_like(out)
+            kc2, vc2 = kc.clone(), vc.clone()
+            gsvk.decode_attention(qkv, kc2, vc2, pos, want, H, len_bound=L)
+            gsvk.decode_attention_noalloc(qkv, kc, vc, pos, out, H, len_bound=L)
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+        else:
+            before = kc.clone()
+            with pytest.raises(gsvk.GsvkError) as e:
+                gsvk.decode_attention_noalloc(qkv, kc, vc, pos, out, H, len_bound=L)
+            assert e.value.status == gsvk.E_SIZE
+            torch.cuda.synchronize()
+            assert torch.equal(kc, before)  # nothing appended: no launch
