@@ -196,7 +196,9 @@ size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t heads, size_t 
  * gsvk_decode_attention_workspace_bytes. GSVK_E_SIZE, before any launch, when the chunk states
  * would exceed 4 MiB (batch x chunks x 3 KiB, 1365 states: on a 256-CU MI355X every batch of up to
  * 256 sequences fits at any length, and up to 682 sequences at contexts of at most 256 keys);
- * GSVK_E_HIP when the array's device address cannot be looked up. */
+ * GSVK_E_HIP when the array's device address cannot be looked up. The lookup runs on the first
+ * call on each device (hipGetSymbolAddress, not a stream operation); a caller that captures every
+ * call into a graph makes one ordinary call on that device before capturing. */
 int gsvk_decode_attention_noalloc(int kv_dtype, int out_dtype, const float* qkv, size_t ldq,
                                   void* k_cache, void* v_cache, size_t max_len, const int64_t* pos,
                                   void* out, size_t ldo, size_t batch, size_t heads,
