@@ -417,17 +417,17 @@ def kernel_suite(torch, gsvk, dev, only=None):
     # T2S decode GEMVs with their fused epilogues, B = 64 rows (t2s_engine.cpp:1044-1116): the
     # stated shape cycles through 24 distinct weight matrices (one per layer, as a decode step
     # does); the replicated case is one weight stream of `rep` such matrices stacked along N.
-    def gemv_case(N, K, act, use_bias, use_res, ydt, rep, layers=24):
+    def gemv_case(N, K, act, use_bias, use_res, ydt, rep, layers=24, M=B):
         yesz = 4 if ydt == f32 else 2
 
         def make(k):
             n = N * k
             nw = layers if k == 1 else 1
             Ws = [rn(n, K, std=0.05) for _ in range(nw)]
-            x = rn(B, K)
+            x = rn(M, K)
             bi = rn(n, dtype=f32, std=0.02) if use_bias else None
-            y = torch.empty(B, n, dtype=ydt, device=dev)
-            res = rn(B, n, dtype=ydt) if use_res else None
+            y = torch.empty(M, n, dtype=ydt, device=dev)
+            res = rn(M, n, dtype=ydt) if use_res else None
             it = [0]
 
             def call():
@@ -438,8 +438,8 @@ def kernel_suite(torch, gsvk, dev, only=None):
 
         def nbytes(k):
             n = N * k
-            return (n * K * 2 + B * K * 2 + B * n * yesz + (n * 4 if use_bias else 0) +
-                    (B * n * yesz if use_res else 0))
+            return (n * K * 2 + M * K * 2 + M * n * yesz + (n * 4 if use_bias else 0) +
+                    (M * n * yesz if use_res else 0))
         return (lambda: make(1), lambda: (rep, make(rep)), nbytes)
 
     for name, N, K, act, ub, ur, ydt, rep, count in (
@@ -450,6 +450,11 @@ def kernel_suite(torch, gsvk, dev, only=None):
             ("logits_f32out", 1025, 512, gsvk.ACT_NONE, False, False, f32, 128, 1)):
         run(f"gemv_{name}_64x{N}x{K}", 2, *gemv_case(N, K, act, ub, ur, ydt, rep), count,
             rows=lambda k: B)
+    # The same long-stream kernel with little to write: 16 rows over 2048 x 128 columns, 268 MB of
+    # weights read for 8 MB of output, against 4-5 bytes read per byte written on the 64-row lines
+    # above. The difference is what the output stores cost the weight stream.
+    run("gemv_read_dominated_16x2048x512", 2,
+        *gemv_case(2048, 512, gsvk.ACT_NONE, False, False, f16, 128, M=16), 0, rows=lambda k: 16)
 
     # T2S decode attention with the KV append (t2s_engine.cpp:1051-1087): B = 64 sequences, 16 heads
     # of 32, fp16 caches, every sequence at position L - 1. One call already streams 2 B L D cache
