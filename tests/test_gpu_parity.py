@@ -429,7 +429,7 @@ PREFILL_CASES = [
     (F16, 300, 77, 512, "inplace", True, False),    # more text than prompt rows
     (F16, 5, 260, 256, "apart", False, True),       # more prompt rows, narrower model
     (F32, 33, 40, 1024, "inplace", True, False),    # two column blocks per lane
-    (F16, 9000, 8500, 512, "inplace", True, False), # the multi-position wave path
+    (F16, 9000, 8500, 512, "inplace", True, False), # 9000 positions: four-wave workgroups
     (F16, 20, 10, 6, "apart", True, False),         # D % 8 != 0: two gather launches
 ]
 
