@@ -56,8 +56,93 @@ SEED = 20250823
 B, D, FF, LAYERS, VOCAB, MAX_POS = 64, 512, 2048, 24, 1025, 2048
 
 
+LOG = []          # every measurement line of the run; written to the detail file
+VERBOSE = False   # --verbose: also print them to stderr as they come
+
+
 def log(*a):
-    print(*a, file=sys.stderr, flush=True)
+    msg = " ".join(str(x) for x in a)
+    LOG.append(msg)
+    if VERBOSE:
+        print(msg, file=sys.stderr, flush=True)
+
+
+def progress(msg):
+    """One short line per finished section, always on stderr (the run's progress)."""
+    LOG.append(msg)
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+# ---- the headline line and the detail file ---------------------------------------------------------
+
+HEADLINE_MAX_CHARS = 3000
+HEADLINE_KEYS = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                 "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+                 "roofline", "cpu_baseline")
+# dropped in this order when the line would exceed HEADLINE_MAX_CHARS
+HEADLINE_OPTIONAL = ("detail_file", "sovits", "whole_decode_step", "configs")
+
+
+def config_summary(kernels):
+    """Per configuration (1-5): how many kernel lines it has, the range of their fractions of 8 TB/s
+    at the stated shape and replicated, and the range of the oracle's best CPU GB/s."""
+    out = {}
+    for k in kernels or ():
+        c = out.setdefault(str(k["config"]), {"lines": 0, "stated_frac": [], "replicated_frac": [],
+                                              "cpu_best_GBps": []})
+        c["lines"] += 1
+        c["stated_frac"].append(k["stated_shape"]["frac_of_peak"])
+        c["replicated_frac"].append(k["replicated"]["frac_of_peak"])
+        if k.get("cpu"):
+            c["cpu_best_GBps"].append(k["cpu"]["best_GBps"])
+    for c in out.values():
+        for key in ("stated_frac", "replicated_frac", "cpu_best_GBps"):
+            v = c[key]
+            c[key] = [min(v), max(v)] if v else None
+    return out
+
+
+def headline_line(rec):
+    """The one JSON line the bench prints last: the headline keys, roofline and cpu_baseline, and
+    compact summaries of the rest (the full record is in the detail file). At most
+    HEADLINE_MAX_CHARS characters: optional summaries are dropped, last first, until it fits."""
+    line = {k: rec.get(k) for k in HEADLINE_KEYS}
+    full = rec.get("t2s_whole_decode_step")
+    if full:
+        line["whole_decode_step"] = {f"kv{r['kv_len']}": {"us": r["us_per_step"],
+                                                          "tokens_per_s": r["tokens_per_s"],
+                                                          "frac": r["frac_of_peak"]} for r in full}
+    if rec.get("kernels"):
+        line["configs"] = config_summary(rec["kernels"])
+    conv = rec.get("sovits_conv")
+    if conv:
+        gen = conv.get("generator") or {}
+        line["sovits"] = {"conv_frac_mfma": conv["roofline"]["frac"],
+                          "decoder_graph_us": (gen.get("decoder") or {}).get("us")}
+    if rec.get("detail_file"):
+        line["detail_file"] = rec["detail_file"]
+    s = json.dumps(line, separators=(",", ":"))
+    for key in HEADLINE_OPTIONAL:
+        if len(s) <= HEADLINE_MAX_CHARS:
+            break
+        line.pop(key, None)
+        s = json.dumps(line, separators=(",", ":"))
+    return s
+
+
+def write_detail(rec, path):
+    """The full record (every kernel line, per-op breakdown, decoder and convolution sweeps, CPU
+    baselines) and the run's measurement log as JSON at `path`; returns the path, or None when it
+    cannot be written."""
+    if not path:
+        return None
+    try:
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(dict(rec, log=LOG), f, indent=1)
+        return os.path.relpath(path, ROOT)
+    except OSError:
+        return None
 
 
 # ---- algorithmic bytes ---------------------------------------------------------------------------
@@ -189,11 +274,15 @@ def graph_us_per_launch(torch, fn, launches=32, replays=10):
     return us
 
 
-def kernel_suite(torch, gsvk, dev, only=None):
-    """Each fused kernel at its stated shape and as a replicated batch."""
+def kernel_suite(torch, gsvk, dev, only=None, capture=None):
+    """Each fused kernel at its stated shape and as a replicated batch. only: run that line alone.
+    capture (a dict, with only): build the line's replicated launch and put it into capture
+    ("fn", "instances", "bytes") without timing anything. only="__names__": return the line names
+    and build nothing."""
     f16, f32 = torch.float16, torch.float32
     g = torch.Generator(device=dev).manual_seed(SEED)
-    flush = Flusher(torch, dev)
+    names = only == "__names__"
+    flush = None if names or capture is not None else Flusher(torch, dev)
     out = []
 
     def rn(*shape, dtype=f16, std=1.0, mean=0.0):
@@ -205,7 +294,14 @@ def kernel_suite(torch, gsvk, dev, only=None):
         rep_bytes_fn: HBM-unique bytes of the replicated launch when they differ from
         bytes_fn (the gather re-reads shared tables from cache). rows: k -> rows one launch of k
         instances produces (sequences, tokens or channel rows), for rows/s."""
+        if names:
+            out.append(name)
+            return
         if only and only != name:
+            return
+        if capture is not None:
+            rep, fnr = replicated()
+            capture.update(fn=fnr, instances=rep, bytes=(rep_bytes_fn or bytes_fn)(rep))
             return
         rec = {"kernel": name, "config": cfg}
         fn1 = stated()
@@ -839,6 +935,233 @@ def cpu_baseline(torch, bufs, rep_s=0.3, reps=9):
     return res, threads_all
 
 
+def cpu_threads_all():
+    """Every thread this process may run on, at most 16 (one GPU's share of the host)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return max(1, min(n or 1, 16))
+
+
+def _bands(n, parts):
+    """[lo, hi) bands of n items over at most `parts` workers (rt::parallel_for's even split)."""
+    parts = max(1, min(parts, n))
+    step = -(-n // parts)
+    return [(lo, min(n, lo + step)) for lo in range(0, n, step)]
+
+
+def cpu_kernel_lines():
+    """The oracle's C restatement of every fused kernel line of the suite at its stated shape, as
+    (make(threads) -> list of band calls, algorithmic bytes, rows). Each band call covers a band of
+    rows (channels, output columns, sequences or elements) with preallocated outputs, so `threads`
+    bands run at once from a thread pool (ctypes releases the interpreter lock for the call)."""
+    import ctypes
+
+    import numpy as np
+
+    import oracle as O
+    L = O.lib()
+    r = np.random.default_rng(SEED + 21)
+    ptr = lambda a, off=0: None if a is None else a.ctypes.data + off
+    lines = {}
+
+    def st(dt, *shape, std=1.0):
+        return O.to_storage(dt, (std * r.standard_normal(shape)).astype(np.float32))
+
+    def vec(n, mean=0.0, std=0.02):
+        return (mean + std * r.standard_normal(n)).astype(np.float32)
+
+    def ln(name, rows, n, dt, eps, bias, res, mode):
+        esz = 4 if dt == O.F32 else 2
+        x, rr = st(dt, rows, n), (st(dt, rows, n) if res else None)
+        g, b, bi = vec(n, 1.0, 0.1), vec(n, 0.0, 0.1), (vec(n) if bias else None)
+        y = np.empty_like(x)
+        make = lambda T: [
+            (lambda lo=lo, hi=hi: L.oracle_add_layernorm(
+                dt, ptr(x, lo * n * esz), ptr(bi), ptr(rr, lo * n * esz), ptr(g), ptr(b),
+                ptr(y, lo * n * esz), hi - lo, n, n, eps, mode)) for lo, hi in _bands(rows, T)]
+        lines[name] = (make, ln_bytes(rows, n, esz, bias, res), rows)
+
+    def bact(name, rows, n, act):
+        x, bi = st(O.F16, rows, n), vec(n)
+        make = lambda T: [
+            (lambda lo=lo, hi=hi: L.oracle_bias_act(O.F16, act, ptr(x, lo * n * 2), ptr(bi),
+                                                    ptr(x, lo * n * 2), hi - lo, n, n, 0.0))
+            for lo, hi in _bands(rows, T)]
+        lines[name] = (make, bias_act_bytes(rows, n, 2), rows)
+
+    pe = O.pe_table(MAX_POS, D)
+
+    def gathers(specs):
+        """specs: (table, ids, pos or None, pos0, alpha, mm, bias, out) per gather of one call."""
+        def make(T):
+            calls = []
+            for tab, ids, pos, pos0, alpha, mm, bias, out in specs:
+                rows = ids.size
+                for lo, hi in _bands(rows, T):
+                    calls.append(lambda tab=tab, ids=ids, pos=pos, pos0=pos0, alpha=alpha, mm=mm,
+                                 bias=bias, out=out, lo=lo, hi=hi: L.oracle_embed_pe(
+                                     O.F16, O.F16, 0, ptr(tab), tab.shape[0], ptr(ids, 8 * lo),
+                                     ptr(pos, 8 * lo), pos0 + lo, ptr(pe), MAX_POS, alpha,
+                                     ptr(mm, lo * D * 2), ptr(bias), ptr(out, lo * D * 2), hi - lo, D))
+            return calls
+        return make
+
+    def gather_line(name, rows, vocab, positions, nbytes, mm=False):
+        tab = st(O.F16, vocab, D, std=0.02)
+        ids = r.integers(0, vocab, rows).astype(np.int64)
+        pos = positions(rows)
+        out = np.empty((rows, D), np.uint16)
+        m = st(O.F16, rows, D) if mm else None
+        bias = vec(D) if mm else None
+        lines[name] = (gathers([(tab, ids, pos, 0, 0.93, m, bias, out)]), nbytes, rows)
+
+    rand_pos = lambda n: r.integers(0, MAX_POS, n).astype(np.int64)
+    gather_line("embed_pe_prefill_1024x512", 1024, VOCAB, rand_pos, embed_bytes(1024, D, 2, 2))
+    tab1 = st(O.F16, 1, D, std=0.02)
+    z = np.zeros(1024, np.int64)
+    lines["embed_pe_hot_row_ceiling_1024x512"] = (
+        gathers([(tab1, z, z, 0, 0.93, None, None, np.empty((1024, D), np.uint16))]),
+        embed_bytes(1024, D, 2, 2), 1024)
+    tp, ts = st(O.F16, 732, D, std=0.02), st(O.F16, VOCAB, D, std=0.02)
+    ip, isem = r.integers(0, 732, 512).astype(np.int64), r.integers(0, VOCAB, 512).astype(np.int64)
+    two = gathers([(tp, ip, None, 0, 0.93, None, None, np.empty((512, D), np.uint16)),
+                   (ts, isem, None, 0, 1.07, None, None, np.empty((512, D), np.uint16))])
+    lines["embed_pe_prefill_pos0_511_2x512x512"] = (two, 1024 * (8 + 2 * D + 4 * D + 2 * D), 1024)
+    lines["t2s_prefill_input_pos0_511_2x512x512"] = (
+        two, 1024 * (8 + 2 * D + 2 * D) + 512 * 4 * D, 1024)
+    gather_line("embed_pe_decode_64x512", 64, VOCAB, rand_pos, embed_bytes(64, D, 2, 2))
+    tt = st(O.F16, 732, D, std=0.02)
+    it = r.integers(0, 732, 512).astype(np.int64)
+    mm, bb = st(O.F16, 512, D), vec(D)
+    lines["embed_pe_text_rows_512x512"] = (
+        gathers([(tt, it, None, 0, 0.93, mm, bb, np.empty((512, D), np.uint16))]),
+        512 * (8 + 2 * D + 4 * D + 2 * D + 2 * D) + 4 * D, 512)
+
+    ln("residual_layernorm_f32_256x512", 256, 512, O.F32, 1e-5, False, True, 0)
+    ln("residual_layernorm_f16_64x512", 64, 512, O.F16, 1e-5, True, True, 0)
+    bact("bias_relu_f16_64x2048", 64, 2048, 1)
+    bact("bias_gelu_f16_512x4096", 512, 4096, 2)
+    ln("residual_layernorm_f16_512x1024_eps1e-12", 512, 1024, O.F16, 1e-12, False, True, 1)
+    ln("residual_layernorm_f16_499x768", 499, 768, O.F16, 1e-5, True, True, 0)
+    bact("bias_gelu_f16_499x3072", 499, 3072, 2)
+
+    C, T = 512, 31999
+    gx = O.to_storage(O.F32, (0.5 * r.standard_normal((C, T))).astype(np.float32))
+    gg, gb, gy = vec(C, 1.0, 0.1), vec(C, 0.0, 0.1), np.empty((C, T), np.float32)
+    lines["groupnorm_gelu_f32_512x31999"] = (
+        lambda Tn: [(lambda lo=lo, hi=hi: L.oracle_groupnorm_gelu(
+            O.F32, ptr(gx, lo * T * 4), ptr(gg, 4 * lo), ptr(gb, 4 * lo), ptr(gy, lo * T * 4),
+            hi - lo, T, T, 1e-5, 1)) for lo, hi in _bands(C, Tn)],
+        gn_bytes(C, T, 4), C)
+
+    E = 24 * 320000
+    for dt, nm in ((O.F32, "f32"), (O.F16, "f16")):
+        esz = 4 if dt == O.F32 else 2
+        t, cur, tb, tin = st(dt, E), st(dt, E), st(dt, E), np.empty(E, O.storage_dtype(dt))
+        curs, tbs, o = [st(dt, E) for _ in range(3)], [st(dt, E) for _ in range(3)], np.empty_like(t)
+
+        def k3(lo, hi, dt=dt, esz=esz, curs=curs, tbs=tbs, o=o):
+            ca = (ctypes.c_void_p * 3)(*[ptr(c, lo * esz) for c in curs])
+            ta = (ctypes.c_void_p * 3)(*[ptr(c, lo * esz) for c in tbs])
+            return lambda: L.oracle_resblock_branch_mean(dt, ca, ta, 3, ptr(o, lo * esz), hi - lo, 1,
+                                                         0.1)
+        lines[f"sovits_K1_{nm}_24x320000"] = (
+            lambda T, dt=dt, esz=esz, t=t: [
+                (lambda lo=lo, hi=hi: L.oracle_leaky_relu(dt, ptr(t, lo * esz), ptr(t, lo * esz),
+                                                          hi - lo, 0.1)) for lo, hi in _bands(E, T)],
+            2 * E * esz, 24)
+        lines[f"sovits_K2_{nm}_24x320000"] = (
+            lambda T, dt=dt, esz=esz, cur=cur, tb=tb, tin=tin: [
+                (lambda lo=lo, hi=hi: L.oracle_resblock_add_lrelu(
+                    dt, ptr(cur, lo * esz), ptr(tb, lo * esz), ptr(tin, lo * esz), hi - lo, 0.1))
+                for lo, hi in _bands(E, T)],
+            4 * E * esz, 24)
+        lines[f"sovits_K3_{nm}_24x320000"] = (
+            lambda T, k3=k3: [k3(lo, hi) for lo, hi in _bands(E, T)], 7 * E * esz, 24)
+
+    def gemv(name, N, K, act, use_bias, use_res, ydt, M=B):
+        yesz = 4 if ydt == O.F32 else 2
+        x, w = st(O.F16, M, K), st(O.F16, N, K, std=0.05)
+        bi = vec(N) if use_bias else None
+        y = np.empty((M, N), O.storage_dtype(ydt))
+        res = st(ydt, M, N) if use_res else None
+        # bands of output columns: every band reads all M activation rows and its own weight rows
+        make = lambda T: [
+            (lambda lo=lo, hi=hi: L.oracle_gemv_f16w(
+                O.F16, 1, ptr(x), K, ptr(w, lo * K * 2), ptr(bi, 4 * lo) if bi is not None else None,
+                act, 0.0, ptr(res, lo * yesz), ydt, ptr(y, lo * yesz), N, M, hi - lo, K))
+            for lo, hi in _bands(N, T)]
+        nbytes = (N * K * 2 + M * K * 2 + M * N * yesz + (N * 4 if use_bias else 0) +
+                  (M * N * yesz if use_res else 0))
+        lines[name] = (make, nbytes, M)
+
+    gemv("gemv_qkv_bias_f32out_64x1536x512", 1536, 512, 0, True, False, O.F32)
+    gemv("gemv_outproj_bias_residual_64x512x512", 512, 512, 0, True, True, O.F16)
+    gemv("gemv_w1_bias_relu_64x2048x512", 2048, 512, 1, True, False, O.F16)
+    gemv("gemv_w2_bias_residual_64x512x2048", 512, 2048, 0, True, True, O.F16)
+    gemv("gemv_logits_f32out_64x1025x512", 1025, 512, 0, False, False, O.F32)
+    gemv("gemv_read_dominated_16x2048x512", 2048, 512, 0, False, False, O.F16, M=16)
+
+    Ln, H = 1024, 16
+    kc, vc = st(O.F16, B, Ln, D), st(O.F16, B, Ln, D)
+    q = r.standard_normal((B, 3 * D)).astype(np.float32)
+    apos = np.full(B, Ln - 1, np.int64)
+    ao = np.empty((B, D), np.float32)
+    lines["decode_attention_f16kv_64x1024x512"] = (
+        lambda T: [(lambda lo=lo, hi=hi: L.oracle_decode_attention(
+            O.F16, ptr(q, lo * 3 * D * 4), 3 * D, ptr(kc, lo * Ln * D * 2), ptr(vc, lo * Ln * D * 2),
+            Ln, ptr(apos, 8 * lo), ptr(ao, lo * D * 4), D, hi - lo, H, D // H))
+            for lo, hi in _bands(B, T)],
+        2 * B * Ln * D * 2 + B * 3 * D * 4 + B * D * 2, B)
+    return lines
+
+
+def time_cpu_line(pool, calls, rep_s=0.03, reps=9):
+    """The reference's bench convention (src/kern/bench_harness.hpp:8-13): 2 warm-up calls, then the
+    median of `reps` repetitions (each a batch of calls lasting ~rep_s) and their coefficient of
+    variation. The band calls of one call run at once on the pool (or inline for one band)."""
+    if len(calls) == 1:
+        run = calls[0]
+    else:
+        run = lambda: [f.result() for f in [pool.submit(c) for c in calls]]
+    for _ in range(2):
+        run()
+    t0 = time.perf_counter()
+    run()
+    per_rep = max(1, int(rep_s / max(time.perf_counter() - t0, 1e-7)))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for _ in range(per_rep):
+            run()
+        times.append((time.perf_counter() - t0) / per_rep)
+    med = statistics.median(times)
+    return med, statistics.pstdev(times) / statistics.mean(times), per_rep
+
+
+def cpu_kernel_baselines(names=None):
+    """Per kernel line: the oracle at the stated shape on 1 thread and on every allowed thread
+    (cpu_threads_all), GB/s over the line's algorithmic bytes and rows/s. Returns name -> record."""
+    from concurrent.futures import ThreadPoolExecutor
+    lines = cpu_kernel_lines()
+    tall = cpu_threads_all()
+    out = {}
+    with ThreadPoolExecutor(max_workers=tall) as pool:
+        for name, (make, nbytes, rows) in lines.items():
+            if names is not None and name not in names:
+                continue
+            rec = {"bytes": nbytes, "rows": rows}
+            for threads in sorted({1, tall}):
+                s, cv, per_rep = time_cpu_line(pool, make(threads))
+                rec[f"t{threads}"] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 3),
+                                      "rows_per_s": round(rows / s, 0), "cv": round(cv, 4),
+                                      "calls_per_rep": per_rep}
+            best = min((rec[k] for k in rec if k.startswith("t")), key=lambda v: v["us"])
+            rec["best_GBps"] = best["GBps"]
+            out[name] = rec
+            log(f"  CPU {name}: 1 thread {rec['t1']['GBps']} GB/s, best {best['GBps']} GB/s")
+    return out, tall
+
+
 def next_tier_cpu(reps=3):
     """Bounded CPU samples of the next-tier rows on the oracle's C restatement (one thread; the
     reference's own NEON / Accelerate code does not build on x86): one T2S decoder layer of the
@@ -1052,6 +1375,112 @@ def measure_traffic(timeout_s=150):
             "write_scale": round(f_write, 4)}, None
 
 
+PMC_LINE_LAUNCHES = 5
+
+
+def pmc_line_workload(torch, gsvk, dev, name):
+    """For `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`: the replicated launch of one suite line
+    once to warm, then PMC_LINE_LAUNCHES times each after a 512 MiB read that clears the MALL, then
+    10 plain copies of PMC_COPY_BYTES (the calibration). Prints the line's algorithmic bytes."""
+    cap = {}
+    kernel_suite(torch, gsvk, dev, only=name, capture=cap)
+    if not cap:
+        raise SystemExit(f"no suite line named {name}")
+    flush = Flusher(torch, dev)
+    cap["fn"]()
+    torch.cuda.synchronize()
+    for _ in range(PMC_LINE_LAUNCHES):
+        flush()
+        cap["fn"]()
+    torch.cuda.synchronize()
+    src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"line": name, "instances": cap["instances"], "bytes": cap["bytes"]}), flush=True)
+
+
+def _counter_rows(path, ctr):
+    """(kernel name, value) per dispatch of counter `ctr` in a rocprofv3 counter CSV, in dispatch
+    order."""
+    import csv
+    rows = []
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] == ctr:
+            rows.append((int(r.get("Dispatch_Id") or r.get("Correlation_Id") or len(rows)),
+                         r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
+
+
+def line_traffic(names, timeout_s=180):
+    """HBM traffic per replicated launch of each named suite line: two `rocprofv3 --pmc` child runs
+    of this script's --pmc-line workload (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch). The
+    library's dispatches (kernel names in namespace gsvk) of one call are summed, the median over
+    the PMC_LINE_LAUNCHES timed calls taken, and each counter scaled by what it reads for the
+    PMC_COPY_BYTES copy of the same run. Returns name -> record."""
+    import glob
+    import subprocess
+    import tempfile
+
+    out = {}
+    for name in names:
+        rec = {}
+        with tempfile.TemporaryDirectory(prefix="gsvk_pmc_") as td:
+            for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+                cmd = ["rocprofv3", "--pmc", ctr, "-f", "csv", "-d", td, "-o", ctr.lower(), "--",
+                       sys.executable, os.path.abspath(__file__), "--pmc-line", name]
+                try:
+                    p = subprocess.run(cmd, cwd=td, capture_output=True, text=True,
+                                       timeout=timeout_s, env=dict(os.environ, TMPDIR=td))
+                except (OSError, subprocess.TimeoutExpired) as exc:
+                    rec["error"] = f"{ctr}: {type(exc).__name__}"
+                    break
+                for ln in p.stdout.splitlines():
+                    if ln.startswith("{") and '"line"' in ln:
+                        rec.update({k: v for k, v in json.loads(ln).items() if k != "line"})
+                files = glob.glob(os.path.join(td, "**", f"{ctr.lower()}_counter_collection.csv"),
+                                  recursive=True)
+                if not files:
+                    rec["error"] = f"{ctr}: no counter file (rc {p.returncode})"
+                    break
+                rows = _counter_rows(files[0], ctr)
+                lib_rows = [v for k, v in rows if "gsvk::" in k]
+                copies = [v for k, v in rows if "copy" in k.lower()][-10:]
+                n = PMC_LINE_LAUNCHES + 1
+                if not copies or not lib_rows or len(lib_rows) % n:
+                    rec["error"] = f"{ctr}: {len(lib_rows)} library / {len(copies)} copy dispatches"
+                    break
+                kpc = len(lib_rows) // n
+                calls = [sum(lib_rows[i * kpc:(i + 1) * kpc]) for i in range(1, n)]
+                scale = PMC_COPY_BYTES / 1024 / statistics.median(copies)
+                rec[ctr.lower() + "_bytes"] = round(statistics.median(calls) * scale * 1024)
+                rec[ctr.lower() + "_scale"] = round(scale, 4)
+                rec["dispatches_per_call"] = kpc
+        if "error" not in rec:
+            rec["traffic"] = rec["fetch_size_bytes"] + rec["write_size_bytes"]
+            rec["traffic_over_algorithmic"] = round(rec["traffic"] / rec["bytes"], 3)
+        out[name] = rec
+        progress(f"traffic {name}: " + (rec.get("error") or
+                                        f"{rec['traffic']} B for {rec['bytes']} algorithmic "
+                                        f"({rec['traffic_over_algorithmic']}x)"))
+    return out
+
+
+def traffic_table(res):
+    """Markdown table of line_traffic's records."""
+    rows = ["| line | instances | algorithmic B | FETCH B | WRITE B | traffic / algorithmic |",
+            "|---|---|---|---|---|---|"]
+    for name, r in res.items():
+        if "error" in r:
+            rows.append(f"| {name} | | | | | {r['error']} |")
+        else:
+            rows.append(f"| {name} | {r['instances']} | {r['bytes']:,} | {r['fetch_size_bytes']:,} "
+                        f"| {r['write_size_bytes']:,} | {r['traffic_over_algorithmic']:.3f} |")
+    return "\n".join(rows)
+
+
 # ---- main --------------------------------------------------------------------------------------------
 
 def main():
@@ -1076,12 +1505,40 @@ def main():
                     help="the SoVITS Generator stages and the whole decoder graph only (rocprofv3 runs)")
     ap.add_argument("--whole-step", type=int, default=0, metavar="KV_LEN",
                     help="run only the whole T2S decode step at this KV length (rocprofv3 runs)")
+    ap.add_argument("--pmc-line", default=None, metavar="LINE",
+                    help="one suite line's replicated launch + a copy (for rocprofv3 --pmc runs)")
+    ap.add_argument("--line-traffic", default=None, metavar="LINES",
+                    help="FETCH_SIZE / WRITE_SIZE per replicated launch of the named suite lines "
+                         "(comma-separated, or 'all'), each from two rocprofv3 --pmc child runs")
+    ap.add_argument("--cpu-lines", action="store_true",
+                    help="the oracle's CPU baseline of every suite line only")
+    ap.add_argument("--detail", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
+                    help="where the full record goes (the last stdout line is the headline only)")
+    ap.add_argument("--verbose", action="store_true",
+                    help="print every measurement line to stderr as it comes")
     a = ap.parse_args()
+    global VERBOSE
+    VERBOSE = a.verbose
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every kernel here is row- or element-local, so more "
               "GPUs would each run an independent share (no figure at several GPUs is produced).",
               file=sys.stderr)
         sys.exit(2)
+
+    if a.cpu_lines:
+        res, tall = cpu_kernel_baselines()
+        print(json.dumps({"threads_all": tall, "cpu_model": cpu_model(), **cpu_topology(),
+                          "lines": res}), flush=True)
+        return
+    if a.line_traffic:
+        import gsvk
+        import torch
+        names = (kernel_suite(torch, gsvk, None, only="__names__") if a.line_traffic == "all"
+                 else a.line_traffic.split(","))
+        res = line_traffic(names)
+        write_detail({"line_traffic": res}, a.detail)
+        print(traffic_table(res), flush=True)
+        return
 
     import torch
 
@@ -1089,6 +1546,9 @@ def main():
     gsvk.lib()  # fails loudly when libgsvk.so is missing
     dev = torch.device("cuda:0")
 
+    if a.pmc_line:
+        pmc_line_workload(torch, gsvk, dev, a.pmc_line)
+        return
     if a.only == "write_bandwidth":
         write_bandwidth(torch, dev)
         return
@@ -1149,6 +1609,8 @@ def main():
     ms73 = time_step(step73)
     log(f"decode step (graph, {step73.launches} launches): {ms73 * 1e3:.2f} us")
     step73.close()
+    progress(f"decode step: {ms * 1e3:.2f} us eager (one launch), {ms_g * 1e3:.2f} us as a "
+             f"one-node graph, {ms73 * 1e3:.2f} us as {1 + 3 * LAYERS} launches")
 
     # per-op breakdown at the step's shapes: graphs of 48 back-to-back launches of each op
     L0, R0, E0 = step_ops(gsvk, bufs)
@@ -1184,6 +1646,8 @@ def main():
             roofline["traffic_error"] = why
             log(f"  traffic not measured: {why}")
 
+    progress(f"roofline: t2s_step_fused {us_fused:.2f} us per launch = {ach:.0f} GB/s "
+             f"({100 * ach / PEAK_GBS:.1f}% of 8 TB/s), traffic {roofline['traffic']}")
     cpu = None
     if not a.no_cpu:
         res, tall = cpu_baseline(torch, bufs)
@@ -1199,31 +1663,35 @@ def main():
                "single_thread_cv": round(res[1]["cv"], 4),
                "cpu_model": cpu_model(), **cpu_topology(), "threads_used": tall}
 
-    kernels = copy_gbs = write_gbs = decoder = full = conv = None
+    kernels = copy_gbs = write_gbs = decoder = full = conv = cpu_lines = None
     if not a.no_kernels:
         copy_gbs = copy_bandwidth(torch, dev)
         write_gbs = write_bandwidth(torch, dev)
         kernels = kernel_suite(torch, gsvk, dev)
+        progress(f"kernel suite: {len(kernels)} lines")
         decoder = sovits_decoder(torch, gsvk, dev)
         full = [full_decode_step(torch, gsvk, dev, kv_len=n) for n in (1024, 2048)]
+        progress("whole decode step: " + ", ".join(f"kv {r['kv_len']} {r['us_per_step']} us"
+                                                  for r in full))
         conv = sovits_conv(torch, gsvk, dev)
         conv["generator"] = sovits_generator(torch, gsvk, dev)
+        progress(f"SoVITS decoder graph: {conv['generator']['decoder']['us']} us per 10 s of audio")
         if not a.no_cpu:
+            cpu_lines, tall = cpu_kernel_baselines()
+            for rec in kernels:
+                c = cpu_lines.get(rec["kernel"])
+                if c:
+                    rec["cpu"] = c
+                    rec["vs_cpu_best"] = round(rec["stated_shape"]["GBps"] / c["best_GBps"], 1)
+            progress(f"CPU baselines: {len(cpu_lines)} kernel lines on 1 and {tall} threads")
             nt = next_tier_cpu()
             full[0]["cpu_baseline"] = nt["t2s_whole_decode_step"]
             full[0]["vs_cpu"] = round(full[0]["tokens_per_s"] / nt["t2s_whole_decode_step"]["value"], 1)
             conv["cpu_baseline"] = nt["sovits_conv_192x40000_k11_d5"]
             big = [c for c in conv["stages"][1]["convs"] if c["k"] == 11 and c["dil"] == 5][0]
             conv["vs_cpu"] = round(conv["cpu_baseline"]["us"] / big["us"], 1)
-            log(f"  CPU (oracle, 1 thread): decode step {nt['t2s_whole_decode_step']['us_per_step']:.0f}"
-                f" us, conv 192x40000 k11 {nt['sovits_conv_192x40000_k11_d5']['us']:.0f} us")
 
-    whole = None
-    if full:
-        whole = {f"kv{r['kv_len']}": {"us_per_step": r["us_per_step"],
-                                      "tokens_per_s": r["tokens_per_s"],
-                                      "frac_of_peak": r["frac_of_peak"]} for r in full}
-    line = {
+    rec = {
         "metric": METRIC, "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -1239,7 +1707,6 @@ def main():
                    "per_op_graph_launches": 1 + 3 * LAYERS},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "whole_decode_step": whole,
         "per_op": per_op,
         "copy_GBps": copy_gbs,
         "write_only_GBps": write_gbs,
@@ -1248,8 +1715,9 @@ def main():
         "t2s_whole_decode_step": full,
         "sovits_conv": conv,
     }
-    print(json.dumps(line), flush=True)
+    rec["detail_file"] = write_detail(rec, a.detail)
     step.close()
+    print(headline_line(rec), flush=True)
 
 
 if __name__ == "__main__":

@@ -359,9 +359,13 @@ extern "C" size_t gsvk_decode_attention_workspace_bytes(size_t batch, size_t hea
   (void)heads;
   (void)head_dim;
   if (batch == 0) return 0;
-  // len_bound 0 (the launch then uses max_len, which this query does not see): size for the
-  // longest context, an upper bound of what any max_len needs.
-  return part_bytes(batch, chunks_for(batch, len_bound ? len_bound : (1ul << 31)));
+  if (len_bound) return part_bytes(batch, chunks_for(batch, len_bound));
+  // len_bound 0: the launch then uses max_len, which this query does not see, so size for the
+  // most chunks any context takes. Short contexts (<= 256 keys) take one chunk per 128 keys
+  // whatever the batch; longer ones at most CUs / batch. With more sequences than half the CUs
+  // the short form takes more chunks than the long one (B = 200 on 256 CUs: 2 against 1).
+  return std::max(part_bytes(batch, chunks_for(batch, 256)),
+                  part_bytes(batch, chunks_for(batch, 1ul << 31)));
 }
 
 namespace gsvk {

@@ -47,7 +47,9 @@ __device__ __forceinline__ float finish_rstd(float var, double eps) {
 // arithmetic. The statistics are finalized with the host's 1/n and v_rsq_f32 (1 ulp): the latency
 // of a double-precision divide and square root sits on the critical path of every small call.
 // Per-lane partial sums are balanced trees per chunk (chunk_sum / chunk_sumsq), chunks added in
-// order: the order the one-launch decode step (gsvk_step.hip) repeats, so both give the same bits.
+// order. The one-launch decode step (gsvk_step.hip) shares that tree order but not the statistics
+// (it takes one pass, E[x^2] - mean^2, where this kernel takes a centred second pass), so the two
+// agree within the LayerNorm tolerance, not bit for bit.
 template <int DT, int CPL, int R, bool NT, int BLOCK, bool HAS_RES>
 __global__ __launch_bounds__(BLOCK) void ln_rows_tile(LnArgs a) {
   using S = Store<DT>;

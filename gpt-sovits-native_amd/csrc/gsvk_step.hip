@@ -501,14 +501,24 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
         if (overlaps(out, row_b, p, p ? pb : 0)) return GSVK_E_ALIAS;
     }
   }
-  for (size_t l = 0; l < d->layers; ++l)
+  // The ReLU tiles write ff[l] while the chain waves read every other input, so ff[l] may overlap
+  // nothing but itself.
+  for (size_t l = 0; l < d->layers; ++l) {
+    const void* ff = d->ff[l];
+    if (overlaps(ff, ff_b, d->audio_table, d->vocab * D * dtype_size(d->table_dtype)) ||
+        overlaps(ff, ff_b, d->ids, B * isz) || overlaps(ff, ff_b, d->pos, B * 8) ||
+        overlaps(ff, ff_b, d->pe, d->max_pos * D * 4) || overlaps(ff, ff_b, d->err, d->err ? 4 : 0))
+      return GSVK_E_ALIAS;
     for (size_t m = 0; m < d->layers; ++m) {
-      if ((m != l && overlaps(d->ff[l], ff_b, d->ff[m], ff_b)) ||
-          overlaps(d->ff[l], ff_b, d->attn_out[m], row_b) ||
-          overlaps(d->ff[l], ff_b, d->ffn_out[m], row_b) ||
-          overlaps(d->ff[l], ff_b, at(d->b1, m), at(d->b1, m) ? FF * 4 : 0))
+      if ((m != l && overlaps(ff, ff_b, d->ff[m], ff_b)) ||
+          overlaps(ff, ff_b, d->attn_out[m], row_b) || overlaps(ff, ff_b, d->ffn_out[m], row_b) ||
+          overlaps(ff, ff_b, at(d->b1, m), at(d->b1, m) ? FF * 4 : 0))
         return GSVK_E_ALIAS;
+      for (const float* p : {at(d->bout, m), at(d->n1g, m), at(d->n1b, m), at(d->b2, m),
+                             at(d->n2g, m), at(d->n2b, m)})
+        if (overlaps(ff, ff_b, p, p ? pb : 0)) return GSVK_E_ALIAS;
     }
+  }
 
   StepArgs a{};
   a.table = d->audio_table;

@@ -91,13 +91,19 @@ class DeviceVector {
     if (n && hipMemsetAsync(p_, 0, n * sizeof(T), current_stream()) != hipSuccess)
       throw std::runtime_error("gsvk::DeviceVector::assign: hipMemsetAsync failed");
   }
+  // Both copies run on the thread's current stream, after the work already queued there (a zero
+  // fill from assign(), a kernel writing the buffer), and return once the copy has completed.
   void copy_from_host(const T* host, size_t n) {
     resize(n);
-    if (n && hipMemcpy(p_, host, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+    if (n && (hipMemcpyAsync(p_, host, n * sizeof(T), hipMemcpyHostToDevice, current_stream()) !=
+                  hipSuccess ||
+              hipStreamSynchronize(current_stream()) != hipSuccess))
       throw std::runtime_error("gsvk::DeviceVector: host-to-device copy failed");
   }
   void copy_to_host(T* host) const {
-    if (n_ && hipMemcpy(host, p_, n_ * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+    if (n_ && (hipMemcpyAsync(host, p_, n_ * sizeof(T), hipMemcpyDeviceToHost, current_stream()) !=
+                   hipSuccess ||
+               hipStreamSynchronize(current_stream()) != hipSuccess))
       throw std::runtime_error("gsvk::DeviceVector: device-to-host copy failed");
   }
   T* data() { return p_; }

@@ -170,8 +170,15 @@ def test_attention_validation(gsvk_lib):
     assert call(q=A + 4) == gsvk.E_ARG           # rows not 16-byte aligned
     assert call(y=B + 64) == gsvk.E_ALIAS        # output over the key cache
     assert call(v=B + 1024) == gsvk.E_ALIAS      # caches overlap
-    assert gsvk_lib.gsvk_decode_attention_workspace_bytes(64, 16, 32, 100) == 0
-    assert gsvk_lib.gsvk_decode_attention_workspace_bytes(64, 16, 32, 1024) > 0
+    ws = gsvk_lib.gsvk_decode_attention_workspace_bytes
+    assert ws(64, 16, 32, 100) == 0
+    assert ws(64, 16, 32, 1024) > 0
+    # len_bound 0 sizes for any max_len: at least what every explicit bound needs, also where the
+    # batch exceeds half the CUs (long contexts then take one chunk, short ones still two)
+    for batch in (1, 64, 129, 200, 256, 700):
+        need = max(ws(batch, 16, 32, lb) for lb in (1, 128, 129, 200, 256, 257, 1024, 1 << 20))
+        assert ws(batch, 16, 32, 0) >= need, batch
+    assert ws(200, 16, 32, 0) >= ws(200, 16, 32, 200) > 0
 
 
 def test_t2s_decode_workspace_and_parts(gsvk_lib):
@@ -384,6 +391,15 @@ def test_t2s_step_fused_validation(gsvk_lib):
     d, k = _step_desc()
     k["ff"][5] = k["ff"][2] + 1024
     assert f(d) == gsvk.E_ALIAS                      # two layers' FFN buffers overlap
+    # an FFN buffer over anything the chain waves read while the ReLU tiles write it
+    for name, layer in (("bout", 7), ("n1g", 0), ("n2b", 23), ("b2", 5)):
+        d, k = _step_desc()
+        k["ff"][4] = k[name][layer] - 64
+        assert f(d) == gsvk.E_ALIAS, name
+    for field in ("pe", "audio_table", "ids", "pos", "err"):
+        d, k = _step_desc()
+        k["ff"][9] = getattr(d, field)
+        assert f(d) == gsvk.E_ALIAS, field
     d, k = _step_desc()
     d.x = d.x + 8
     assert f(d) == gsvk.E_ARG                        # x not 16-byte aligned

@@ -179,6 +179,10 @@ FUSED_CASES = [
     (F32, 3, 256, 64, 1, BF16, False),
     (BF16, 7, 1024, 2056, 2, F16, True),
     (F16, 1, 8, 8, 32, F16, False),         # the layer limit, one lane of one chunk
+    # two chunks per lane with the second partly active (64 < D / VEC < 128): guarded stores and
+    # zeroed tail chunks
+    (F16, 5, 800, 1000, 4, F16, False),
+    (F32, 6, 400, 520, 3, F32, True),
 ]
 
 
