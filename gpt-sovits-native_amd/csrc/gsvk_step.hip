@@ -15,7 +15,16 @@
 //
 // The chain wave prefetches the next layers' inputs (attn_out / ffn_out rows and the six parameter
 // vectors) three layers ahead into a register ring, so HBM latency is paid once, not per LayerNorm.
-// Its row reductions are DPP only (gsvk_common.hpp wave_sum2): no LDS round trip per LayerNorm.
+// Its row reductions are DPP only: no LDS round trip per LayerNorm.
+//
+// What bounds it: one wave issues at most one instruction per four cycles (a wave64 VALU op takes
+// four passes of the 16-lane SIMD), and the chain wave issues ~5,400 of them (rocprofv3 counters:
+// SQ_INSTS, SQ_INSTS_VALU, SQ_ACTIVE_INST_VALU per wave with the ReLU waves removed). So the chain
+// is shortened by issuing fewer instructions, not by shorter dependences: the next LayerNorm's
+// input + bias conversions fill the issue slots in which the DPP reduction steps would wait out
+// their hazards (no s_nop there), fp16 halves are converted and added by v_fma_mix_f32 that the
+// compiler sees (an opaque fp16 one as the multiplier: around inline asm the compiler adds wait
+// states), and the lane's sum of squares is one fma chain.
 //
 // Numerics: each LayerNorm takes its statistics in one pass, as kern::layernorm does
 // (kern.cpp:27-59: the row's sum and sum of squares, var = E[x^2] - mean^2, a centred second pass
@@ -154,43 +163,51 @@ struct RowVal<GSVK_F16, CPL> {
   u32x4 p[CPL];
 };
 
-// float(half) + b with one rounding: v_fma_mix_f32 h, 1.0, b (the half is converted exactly and
-// multiplied by one exactly, so this is the conversion and the add in one instruction, the same
-// bits). HI selects the upper half of the word.
+// float(half) + b with one rounding: v_fma_mix_f32 h, one, b, the half converted exactly and
+// multiplied by one exactly (the same bits as the conversion and the add). `one` is an opaque fp16
+// 1.0 in a VGPR: with a literal 1.0 the compiler folds the fma into a conversion and an add.
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 template <bool HI>
-__device__ __forceinline__ float add_half(uint32_t w, float b) {
-  float d;
-  if constexpr (HI)
-    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(b));
-  else
-    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(b));
-  return d;
+__device__ __forceinline__ float add_half(uint32_t w, float b, _Float16 one) {
+  const h2v h = __builtin_bit_cast(h2v, w);
+  return __builtin_fmaf(static_cast<float>(HI ? h.y : h.x), static_cast<float>(one), b);
 }
 
-// v[k] = (float(h[k]) + bias[k]) + float(r[k]) for 8 packed halves h and r.
-__device__ __forceinline__ void add2_halves(const u32x4& h, const float (&bias)[8], const u32x4& r,
-                                            float (&v)[8]) {
-  const uint32_t hw[4] = {h.x, h.y, h.z, h.w}, rw[4] = {r.x, r.y, r.z, r.w};
+// t = in + bias as fp32 (the first rounding of the reference's (in + bias) + res).
+template <int DT>
+__device__ __forceinline__ void add_bias(const u32x4& in, const float (&bias)[Store<DT>::VEC],
+                                         float (&t)[Store<DT>::VEC], _Float16 one) {
+  if constexpr (DT == GSVK_F16) {
+    const uint32_t hw[4] = {in.x, in.y, in.z, in.w};
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[2 * k] = add_half<false>(rw[k], add_half<false>(hw[k], bias[2 * k]));
-    v[2 * k + 1] = add_half<true>(rw[k], add_half<true>(hw[k], bias[2 * k + 1]));
+    for (int k = 0; k < 4; ++k) {
+      t[2 * k] = add_half<false>(hw[k], bias[2 * k], one);
+      t[2 * k + 1] = add_half<true>(hw[k], bias[2 * k + 1], one);
+    }
+  } else {
+    Store<DT>::unpack(in, t);
+#pragma unroll
+    for (int k = 0; k < Store<DT>::VEC; ++k) t[k] = t[k] + bias[k];
   }
 }
 
-// y = LN((in + bias) + res) over one row held by the wave: per-lane chunk trees of the values and
-// of their squares added in chunk order, both wave sums at once, mean = float(double(sum) / n),
+// y = LN(t + res), t = in + bias already rounded, over one row held by the wave: per-lane chunk
+// trees of the values and of their squares added in chunk order, both wave sums at once,
 // var = E[x^2] - mean^2 (the centred second moment where that is negative), rstd = rsq(var + eps),
 // y = fmaf((v - mean) rstd, g, b). Stores y and returns its rounded storage value in `yr` (what the
-// next LayerNorm reads back as its residual).
+// next LayerNorm reads back as its residual). The next LayerNorm's nt = nin + nbias (independent of
+// this one) is computed between the steps of the wave reduction, in the issue slots the DPP reads
+// would otherwise wait out.
 template <int DT, int CPL, bool FULL>
-__device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL],
-                                       const float (&bias)[CPL][Store<DT>::VEC],
+__device__ __forceinline__ void ln_row(const StepArgs& a, const float (&t)[CPL][Store<DT>::VEC],
                                        const RowVal<DT, CPL>& res,
                                        const float (&g)[CPL][Store<DT>::VEC],
                                        const float (&b)[CPL][Store<DT>::VEC],
                                        const bool (&on)[CPL], void* y, size_t row_off,
-                                       const uint32_t (&eo)[CPL], RowVal<DT, CPL>& yr) {
+                                       const uint32_t (&eo)[CPL], RowVal<DT, CPL>& yr,
+                                       _Float16 one, const u32x4 (&nin)[CPL],
+                                       const float (&nbias)[CPL][Store<DT>::VEC],
+                                       float (&nt)[CPL][Store<DT>::VEC]) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   float v[CPL][V];
@@ -199,13 +216,15 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
   for (int c = 0; c < CPL; ++c) {
     if (FULL || on[c]) {
       if constexpr (DT == GSVK_F16) {
-        add2_halves(in[c], bias[c], res.p[c], v[c]);
+        const uint32_t rw[4] = {res.p[c].x, res.p[c].y, res.p[c].z, res.p[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[c][2 * k] = add_half<false>(rw[k], t[c][2 * k], one);
+          v[c][2 * k + 1] = add_half<true>(rw[k], t[c][2 * k + 1], one);
+        }
       } else {
-        S::unpack(in[c], v[c]);
 #pragma unroll
-        for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + bias[c][k];
-#pragma unroll
-        for (int k = 0; k < V; ++k) v[c][k] = v[c][k] + res.f[c][k];
+        for (int k = 0; k < V; ++k) v[c][k] = t[c][k] + res.f[c][k];
       }
       s = c == 0 ? chunk_sum(v[c]) : s + chunk_sum(v[c]);
     } else {
@@ -214,32 +233,84 @@ __device__ __forceinline__ void ln_row(const StepArgs& a, const u32x4 (&in)[CPL]
     }
   }
   // One pass, as kern::layernorm (kern.cpp:29-48): the row's sum and sum of squares are reduced
-  // together (two interleaved DPP chains, one reduction latency on the critical path), then
-  // var = E[x^2] - mean^2, and only a row where that comes out negative or NaN (cancellation)
-  // takes the second, centred pass (kern.cpp:49-56).
+  // together (two interleaved DPP chains), then var = E[x^2] - mean^2, and only a row where that
+  // comes out negative or NaN (cancellation) takes the second, centred pass (kern.cpp:49-56).
   // With FULL rows n = 64 * CPL * VEC is a power of two, so scaling by 1/n is exact in fp32 and
   // commutes with every rounding of the sums: the lane partials are scaled before the reduction,
   // and fmaf(-mean, mean, E[x^2]) rounds the exact difference once, as the reference's
   // float(double(sqsum) / n - double(mean)^2) does (mean^2 is exact in double).
+  // The lane's sum of squares is one fma chain (V instructions; a tree takes V + V / 2 - 1): the
+  // chain wave is bound by instruction issue, not by the depth of its dependences.
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
-    if (FULL || on[c]) q = c == 0 ? chunk_sq(v[c]) : q + chunk_sq(v[c]);
+    if (FULL || on[c]) {
+#pragma unroll
+      for (int k = 0; k < V; ++k)
+        q = (c == 0 && k == 0) ? v[c][k] * v[c][k] : __builtin_fmaf(v[c][k], v[c][k], q);
+    }
+  // the wave reduction (wave_sum2's steps) with nt computed in the issue slots between them
+  float ra = FULL ? s * a.inv_n_f : s, rb = FULL ? q * a.inv_n_f : q;
+  if constexpr (DT == GSVK_F16 && CPL == 1 && FULL) {
+    // One block: two DPP chains of six steps (each DPP read two issue slots after the write of its
+    // source, filled by the other chain's step and one conversion of nt) and the eight v_fma_mix
+    // that form nt = float(nin) + nbias. Lane 63 ends with (r3 + r2) + (r1 + r0) of both values.
+    float* o = nt[0];
+    asm volatile(
+        "v_fma_mix_f32 %2, %10, 1.0, %14 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mix_f32 %3, %10, 1.0, %15 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_add_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_fma_mix_f32 %4, %11, 1.0, %16 op_sel_hi:[1,0,0]\n\t"
+        "v_add_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_fma_mix_f32 %5, %11, 1.0, %17 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_fma_mix_f32 %6, %12, 1.0, %18 op_sel_hi:[1,0,0]\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 row_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_fma_mix_f32 %7, %12, 1.0, %19 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 row_bcast:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_fma_mix_f32 %8, %13, 1.0, %20 op_sel_hi:[1,0,0]\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 row_bcast:31 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_fma_mix_f32 %9, %13, 1.0, %21 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "+v"(ra), "+v"(rb), "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]),
+          "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7])
+        : "v"(nin[0].x), "v"(nin[0].y), "v"(nin[0].z), "v"(nin[0].w), "v"(nbias[0][0]),
+          "v"(nbias[0][1]), "v"(nbias[0][2]), "v"(nbias[0][3]), "v"(nbias[0][4]), "v"(nbias[0][5]),
+          "v"(nbias[0][6]), "v"(nbias[0][7]));
+  } else {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) add_bias<DT>(nin[c], nbias[c], nt[c], one);
+    ra += dpp_f32<0xB1>(ra);
+    rb += dpp_f32<0xB1>(rb);
+    ra += dpp_f32<0x4E>(ra);
+    rb += dpp_f32<0x4E>(rb);
+    ra += dpp_f32<0x141>(ra);
+    rb += dpp_f32<0x141>(rb);
+    ra += dpp_f32<0x140>(ra);
+    rb += dpp_f32<0x140>(rb);
+    ra += dpp_f32<0x142>(ra);
+    rb += dpp_f32<0x142>(rb);
+    ra += dpp_f32<0x143>(ra);
+    rb += dpp_f32<0x143>(rb);
+  }
+  const float SA = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ra), 63));
+  const float SB = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rb), 63));
   float mean, var;
   if constexpr (FULL) {
-    float ex2;
-    wave_sum2(s * a.inv_n_f, q * a.inv_n_f, mean, ex2);
-    var = __builtin_fmaf(-mean, mean, ex2);
+    mean = SA;
+    var = __builtin_fmaf(-mean, mean, SB);
   } else {
-    float S, Q;
-    wave_sum2(s, q, S, Q);
-    mean = static_cast<float>(static_cast<double>(S) * a.inv_n);
+    mean = static_cast<float>(static_cast<double>(SA) * a.inv_n);
     const double m = mean;
-    var = static_cast<float>(static_cast<double>(Q) * a.inv_n - m * m);
+    var = static_cast<float>(static_cast<double>(SB) * a.inv_n - m * m);
   }
   if (!(var >= 0.f)) {  // wave-uniform
-    // (mean passed through an empty asm: otherwise the compiler shares this pass's v - mean with
-    // the normalization below and computes it ahead of the branch, on the common path)
     float m2 = mean;
     asm volatile("" : "+v"(m2));
     float q2 = 0.f;
@@ -330,9 +401,15 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   if (!ok && lane == 0 && a.err) *a.err = 1;
 
   RowVal<DT, CPL> hr;
-  auto layer = [&](LayerIn<DT, CPL>& fi) {
-    ln_row<DT, CPL, FULL>(a, fi.att, fi.bo, xr, fi.g1, fi.be1, on, a.h, row_off, eo, hr);
-    ln_row<DT, CPL, FULL>(a, fi.ffo, fi.b2, hr, fi.g2, fi.be2, on, a.x, row_off, eo, xr);
+  _Float16 one = static_cast<_Float16>(1.f);
+  asm volatile("" : "+v"(one));
+  float t[CPL][V], nt[CPL][V];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) add_bias<DT>(f[0].att[c], f[0].bo[c], t[c], one);
+  // fn: the ring slot of the next layer (its attention row + bias is the next LN1's input)
+  auto layer = [&](LayerIn<DT, CPL>& fi, LayerIn<DT, CPL>& fn) {
+    ln_row<DT, CPL, FULL>(a, t, xr, fi.g1, fi.be1, on, a.h, row_off, eo, hr, one, fi.ffo, fi.b2, nt);
+    ln_row<DT, CPL, FULL>(a, nt, hr, fi.g2, fi.be2, on, a.x, row_off, eo, xr, one, fn.att, fn.bo, t);
   };
   // sched_barrier(0) keeps the scheduler from hoisting the next layer's arithmetic (and so its
   // loads' waits) into the current layer's reductions: measured, that put a wait on loads issued
@@ -349,16 +426,16 @@ __device__ __forceinline__ void chain_row(const StepArgs& a, long b) {
   };
   int l = 0;
   for (; l + 2 < L; l += 3) {
-    layer(f[0]);
+    layer(f[0], f[1]);
     refill(f[0], l + 3);
-    layer(f[1]);
+    layer(f[1], f[2]);
     refill(f[1], l + 4);
-    layer(f[2]);
+    layer(f[2], f[0]);
     refill(f[2], l + 5);
   }
   // the last 1 or 2 layers (L mod 3), already in slots 0 and 1
-  if (l < L) layer(f[0]);
-  if (l + 1 < L) layer(f[1]);
+  if (l < L) layer(f[0], f[1]);
+  if (l + 1 < L) layer(f[1], f[2]);
 }
 
 // ReLU wave w of the launch: layer w / waves_per_layer, rows r0 .. r0 + kReluRows - 1, one column
