@@ -149,13 +149,15 @@ def test_decode_step_graph_equals_eager_over_steps():
 
 
 def test_decode_step_t2s_shape_four_layers():
-    """B = 64, D = 512, 16 heads, FF = 2048, four chained layers, 1025-token vocabulary: the real
-    shapes, with the residual path carrying each layer's differences into the next."""
+    """B = 64, D = 512, 16 heads, FF = 2048, four chained layers, 1025-token vocabulary, every
+    sequence at 960-1023 cached keys: the real shapes, with the residual path carrying each layer's
+    differences into the next."""
     FF = 2048
-    m, io = build(B=64, D=512, H=16, FF=FF, L=4, V=1025, max_len=300, seed=3)
+    m, io = build(B=64, D=512, H=16, FF=FF, L=4, V=1025, max_len=1024, seed=3)
+    io["kv_pos"][:] = np.random.default_rng(96).integers(960, 1024, 64)
     md, iod = to_device(m, io, FF)
     x_want, lg_want = oracle_step(m, io)
-    step = gsvk.T2SDecode(md, iod, len_bound=300)
+    step = gsvk.T2SDecode(md, iod, len_bound=1024)
     step.run()
     torch.cuda.synchronize()
     compare(host(iod["x"], F16), host(iod["logits"], F32), x_want, lg_want, "T2S shape")
