@@ -719,8 +719,11 @@ class T2SDecode:
         d.parts = 0 if split else 1
         need = lib().gsvk_t2s_decode_workspace_bytes(B, m["heads"], D // m["heads"],
                                                      len_bound or d.max_len)
+        self._ws = None
         if need:
-            ws = workspace(io["x"].device, need)
+            # A workspace of its own: the recorded graph keeps its address, and the shared scratch
+            # of workspace() is replaced (freed) when a later call needs a larger one.
+            self._ws = ws = torch.empty(need, dtype=torch.uint8, device=io["x"].device)
             d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
         self.desc = d
         self.handle = None
