@@ -436,6 +436,30 @@ def kernel_suite(torch, gsvk, dev, only=None, capture=None):
     st_, rp_, b_, ub_ = prefill_input_case(512)
     run("t2s_prefill_input_pos0_511_2x512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_,
         rows=lambda k: 1024 * k)
+
+    def prefill_distinct_case(rep):
+        """The two-gather form of the same prefill input over the one-launch line's workload: at
+        the stated shape the two gathers at positions 0..511; replicated, 512 * rep positions with
+        a PE table of as many rows, so each PE row comes from HBM as in the one-launch line, and
+        the same floor (ids, both output rows and the PE row per position, the tables once)."""
+        def make(k):
+            n = 512 * k
+            tp, ts = rn(732, D, std=0.02), rn(VOCAB, D, std=0.02)
+            ip = torch.randint(0, 732, (n,), device=dev, generator=g)
+            isem = torch.randint(0, VOCAB, (n,), device=dev, generator=g)
+            pe_k = pe if k == 1 else rn(n, D, dtype=f32)
+            op = torch.empty(n, D, dtype=f16, device=dev)
+            osem = torch.empty(n, D, dtype=f16, device=dev)
+            return lambda: (gsvk.embed_pe(tp, ip, pe_k, 0.93, op, pos0=0),
+                            gsvk.embed_pe(ts, isem, pe_k, 1.07, osem, pos0=0))
+        per = lambda k: 1024 * k * (8 + 2 * D + 4 * D + 2 * D)
+        floor = lambda k: (512 * k * (16 + 2 * 2 * D + 4 * D) + (732 + VOCAB) * D * 2 if k > 1
+                           else per(1))
+        return (lambda: make(1), lambda: (rep, make(rep)), per, floor)
+
+    st_, rp_, b_, ub_ = prefill_distinct_case(512)
+    run("embed_pe_prefill_distinct_pos_2x512x512", 2, st_, rp_, b_, 1, rep_bytes_fn=ub_,
+        rows=lambda k: 1024 * k)
     run_emb("embed_pe_decode_64x512", 64, 8192)
 
     def text_case(rows, rep):
@@ -1028,6 +1052,7 @@ def cpu_kernel_lines():
     lines["embed_pe_prefill_pos0_511_2x512x512"] = (two, 1024 * (8 + 2 * D + 4 * D + 2 * D), 1024)
     lines["t2s_prefill_input_pos0_511_2x512x512"] = (
         two, 1024 * (8 + 2 * D + 2 * D) + 512 * 4 * D, 1024)
+    lines["embed_pe_prefill_distinct_pos_2x512x512"] = (two, 1024 * (8 + 2 * D + 4 * D + 2 * D), 1024)
     gather_line("embed_pe_decode_64x512", 64, VOCAB, rand_pos, embed_bytes(64, D, 2, 2))
     tt = st(O.F16, 732, D, std=0.02)
     it = r.integers(0, 732, 512).astype(np.int64)

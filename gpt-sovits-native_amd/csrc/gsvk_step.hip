@@ -530,7 +530,11 @@ __attribute__((visibility("hidden"))) bool step_fill_rows(const float** zeros, c
 
 using namespace gsvk;
 
-extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
+namespace gsvk {
+namespace {
+
+// Validation of a descriptor, then its launch arguments in `a` (GSVK_OK) or the status.
+int build_step_args(const gsvk_t2s_step_desc* d, StepArgs& a) {
   if (!d || !d->x || !d->h || !d->attn_out || !d->ff || !d->ffn_out || !d->audio_table ||
       !d->ids || !d->pos || !d->pe)
     return GSVK_E_NULL;
@@ -597,7 +601,7 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
     }
   }
 
-  StepArgs a{};
+  a = StepArgs{};
   a.table = d->audio_table;
   a.ids = d->ids;
   a.pos = d->pos;
@@ -636,10 +640,79 @@ extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
                        or_fill(at(d->b2, l), zeros),
                        or_fill(at(d->n2g, l), ones),
                        or_fill(at(d->n2b, l), zeros)};
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (d->dtype) {
+  return GSVK_OK;
+}
+
+// Everything a descriptor's validation and launch arguments depend on: its sizes, types and
+// scalars, every pointer of it and of its per-layer arrays, and the current device (the filler
+// rows' addresses are per device). False when it cannot be keyed (missing arrays, too many
+// layers): the full validation then reports why.
+constexpr int kKeyWords = 20 + 10 * kMaxStepLayers;
+struct StepKey {
+  uint64_t w[kKeyWords];
+  int n = 0;
+};
+
+bool step_key(const gsvk_t2s_step_desc* d, int dev, StepKey& k) {
+  if (!d || !d->attn_out || !d->ff || !d->ffn_out || d->layers == 0 ||
+      d->layers > static_cast<size_t>(kMaxStepLayers))
+    return false;
+  auto u = [](const void* p) { return static_cast<uint64_t>(reinterpret_cast<uintptr_t>(p)); };
+  auto at = [](const float* const* arr, size_t l) { return arr ? arr[l] : nullptr; };
+  uint64_t eps_bits, alpha_bits = __builtin_bit_cast(uint32_t, d->alpha);
+  static_assert(sizeof(d->eps) == 8, "eps is a double");
+  __builtin_memcpy(&eps_bits, &d->eps, 8);
+  const uint64_t head[20] = {static_cast<uint64_t>(d->dtype), static_cast<uint64_t>(d->table_dtype),
+                             static_cast<uint64_t>(d->index_type), d->batch, d->d_model, d->ffn,
+                             d->layers, d->vocab, d->max_pos, eps_bits, alpha_bits,
+                             u(d->audio_table), u(d->ids), u(d->pos), u(d->pe), u(d->err), u(d->x),
+                             u(d->h), static_cast<uint64_t>(dev), 0};
+  int n = 0;
+  for (uint64_t v : head) k.w[n++] = v;
+  for (size_t l = 0; l < d->layers; ++l) {
+    const void* const per[10] = {d->attn_out[l], at(d->bout, l), at(d->n1g, l), at(d->n1b, l),
+                                 d->ff[l], at(d->b1, l), d->ffn_out[l], at(d->b2, l),
+                                 at(d->n2g, l), at(d->n2b, l)};
+    for (const void* p : per) k.w[n++] = u(p);
+  }
+  k.n = n;
+  return true;
+}
+
+int launch_args(int dtype, const StepArgs& a, hipStream_t st) {
+  switch (dtype) {
     case GSVK_F32: return launch_step<GSVK_F32>(a, st);
     case GSVK_F16: return launch_step<GSVK_F16>(a, st);
     default: return launch_step<GSVK_BF16>(a, st);
   }
+}
+
+}  // namespace
+}  // namespace gsvk
+
+// A decode loop launches the same descriptor every token: validating one of 24 layers checks a few
+// thousand pairs of ranges for overlap (microseconds of host time per call), so each host thread
+// keeps the launch arguments of the last descriptor it validated and reuses them when the next
+// call's descriptor has exactly the same contents on the same device.
+extern "C" int gsvk_t2s_step_fused(const gsvk_t2s_step_desc* d, void* stream) {
+  thread_local StepKey last_key;
+  thread_local StepArgs last_args;
+  thread_local int last_dtype = -1;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  StepKey key;
+  const bool keyed = step_key(d, dev, key);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (keyed && last_dtype >= 0 && key.n == last_key.n &&
+      __builtin_memcmp(key.w, last_key.w, sizeof(uint64_t) * key.n) == 0)
+    return launch_args(last_dtype, last_args, st);
+  StepArgs a;
+  const int rc = build_step_args(d, a);
+  if (rc != GSVK_OK) return rc;
+  if (keyed) {
+    last_key = key;
+    last_args = a;
+    last_dtype = d->dtype;
+  }
+  return launch_args(d->dtype, a, st);
 }

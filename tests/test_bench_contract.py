@@ -48,7 +48,8 @@ def _bench():
 KERNEL_LINES = [  # (name, configuration) of every line the suite measures
     ("residual_layernorm_f32_256x512", 1), ("embed_pe_prefill_1024x512", 2),
     ("embed_pe_hot_row_ceiling_1024x512", 2), ("embed_pe_prefill_pos0_511_2x512x512", 2),
-    ("t2s_prefill_input_pos0_511_2x512x512", 2), ("embed_pe_decode_64x512", 2),
+    ("t2s_prefill_input_pos0_511_2x512x512", 2), ("embed_pe_prefill_distinct_pos_2x512x512", 2),
+    ("embed_pe_decode_64x512", 2),
     ("embed_pe_text_rows_512x512", 2), ("residual_layernorm_f16_64x512", 2),
     ("bias_relu_f16_64x2048", 2), ("bias_gelu_f16_512x4096", 3),
     ("residual_layernorm_f16_512x1024_eps1e-12", 3), ("groupnorm_gelu_f32_512x31999", 4),

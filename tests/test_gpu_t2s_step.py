@@ -18,6 +18,8 @@
 4. Constant rows: the one-pass variance is the rounding error of c^2, negative for some c, which
    sends the row through the centred second pass; every such row comes out as beta exactly.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -285,3 +287,40 @@ def test_fused_step_constant_rows(dt):
     g = gh[8:].astype(np.float64)
     w = O.to_f32(dt, want["h"])[8:].astype(np.float64)
     assert (np.abs(g - w) <= chain_bound(dt, w, L)).all()
+
+
+def test_fused_step_revalidates_a_changed_descriptor():
+    """The launch keeps the arguments of the last descriptor it validated and reuses them only for
+    an identical one: after a good call, the same descriptor with one pointer or one size changed
+    is validated again (here rejected), and the good one runs again with the results of its first
+    run."""
+    say("fused step: descriptor changes after a validated call")
+    dt, B, D, FF, L = F16, 8, 512, 256, 3
+    hb = host_bufs(dt, B, D, FF, L, 6300)
+    db = to_dev(hb, dt)
+    step = gsvk.T2SStep(db, graph=False, fused=True)
+    lib, d = gsvk.lib(), step.desc
+    run = lambda: lib.gsvk_t2s_step_fused(ctypes.byref(d), None)
+    assert run() == gsvk.OK
+    torch.cuda.synchronize()
+    first = snapshot(db, dt)
+    h = d.h
+    d.h = d.x + 64                                   # h over x
+    assert run() == gsvk.E_ALIAS
+    d.h = h
+    arr = step._arrays["ff"]
+    ff2 = arr[2]
+    arr[2] = step._arrays["attn_out"][1]             # a layer's FFN buffer over another's input
+    assert run() == gsvk.E_ALIAS
+    arr[2] = ff2
+    d.d_model = 516                                  # a size: rows of partial chunks
+    assert run() == gsvk.E_ARG
+    d.d_model = D
+    reset_ff(db, hb, dt)
+    assert run() == gsvk.OK
+    torch.cuda.synchronize()
+    again = snapshot(db, dt)
+    for name in ("x", "h"):
+        assert np.array_equal(again[name], first[name]), name
+    for a, b in zip(again["ff"], first["ff"]):
+        assert np.array_equal(a, b)
