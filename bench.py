@@ -118,6 +118,7 @@ def headline_line(rec):
     if conv:
         gen = conv.get("generator") or {}
         line["sovits"] = {"conv_frac_mfma": conv["roofline"]["frac"],
+                          "conv_frac_of_bound": conv.get("frac_of_bound_by_stage"),
                           "decoder_graph_us": (gen.get("decoder") or {}).get("us")}
     if rec.get("detail_file"):
         line["detail_file"] = rec["detail_file"]
@@ -666,6 +667,18 @@ def conv_us(torch, fn, iters=10):
     return s.elapsed_time(e) * 1e3 / iters
 
 
+def conv_bound(flops, nbytes, us):
+    """A convolution launch against the resource that bounds it: MFMA when its time at the dense
+    fp16 peak (the fp32 path's hi/lo split doubles the matrix-core work) exceeds its HBM bytes' time
+    at 8 TB/s, else HBM."""
+    t_mfma = 2 * flops / (PEAK_F16_TFLOPS * 1e12)
+    t_hbm = nbytes / (PEAK_GBS * 1e9)
+    bound = "mfma" if t_mfma >= t_hbm else "hbm"
+    frac = max(t_mfma, t_hbm) / (us * 1e-6)
+    return {"bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1), "bound": bound,
+            "frac_of_bound": round(frac, 4)}
+
+
 def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
     """Per decoder stage (C, T): the upsampler (ConvT1d into the stage) and every distinct ResBlock
     convolution timed once (conv1: k x dilation 1 / 3 / 5 with the LeakyReLU epilogue; conv2: k,
@@ -698,19 +711,30 @@ def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
                 conv.dilation = dil
                 us = conv_us(torch, lambda: conv.forward(x, y, epi=epi, cur=cur))
                 us_rx = conv_us(torch, lambda: conv.forward(x, y, epi=epi, cur=cur, round_x=True))
+                # HBM bytes: x read, y written, the residual epilogue's cur read and written, the
+                # fp16 weights and the bias once
+                nb = C * T * 4 * (2 + (2 if epi == gsvk.CONV_EPI_RES_LRELU else 0)) + C * C * k * 2 + C * 4
                 row["convs"].append({"k": k, "dil": dil, "epi": epi, "count": n,
                                      "us": round(us, 2), "us_round_x": round(us_rx, 2),
-                                     "TFLOPs": round(fl / us / 1e6, 1)})
+                                     "TFLOPs": round(fl / us / 1e6, 1),
+                                     **conv_bound(fl, nb, us)})
                 st += n * us
                 st_rx += n * us_rx
                 st_fl += n * fl
         row["upsample"] = {"c_in": cin_up, "stride": u, "k": k_up, "us": round(up_us, 2),
                            "us_round_x": round(up_us_rx, 2),
                            "TFLOPs": round(up_fl / up_us / 1e6, 1),
-                           "out_GBps": round(C * T * 4 / up_us / 1e3, 1)}
+                           "out_GBps": round(C * T * 4 / up_us / 1e3, 1),
+                           **conv_bound(up_fl, cin_up * (T // u) * 4 + C * T * 4 * 2 +
+                                        cin_up * C * k_up * 2 + C * 4, up_us)}
         st, st_rx, st_fl = st + up_us, st_rx + up_us_rx, st_fl + up_fl
+        # the stage's binding resource: the time-weighted mean of its launches' fractions of
+        # their own bound
+        bound_us = sum(c["count"] * c["us"] * c["frac_of_bound"] for c in row["convs"]) + \
+            up_us * row["upsample"]["frac_of_bound"]
         row.update({"stage_us": round(st, 1), "stage_us_round_x": round(st_rx, 1),
-                    "stage_TFLOPs": round(st_fl / st / 1e6, 1)})
+                    "stage_TFLOPs": round(st_fl / st / 1e6, 1),
+                    "stage_frac_of_bound": round(bound_us / st, 4)})
         stages.append(row)
         tot, tot_rx, flops_tot = tot + st, tot_rx + st_rx, flops_tot + st_fl
         log(f"  conv stage {C}x{T}: {st:.1f} us incl. upsampler {up_us:.1f} us (round_x "
@@ -718,8 +742,12 @@ def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
         del x, y, cur, conv
     torch.cuda.empty_cache()
     ach = flops_tot / tot / 1e6
+    log("  conv stages against their binding resource: " + ", ".join(
+        f"{r['C']}x{r['T']} {100 * r['stage_frac_of_bound']:.1f}%" for r in stages))
     return {"geometry": geometry, "stages": stages, "conv_us_per_10s_audio": round(tot, 1),
             "conv_us_per_10s_audio_round_x": round(tot_rx, 1),
+            "frac_of_bound_by_stage": {f"{r['C']}x{r['T']}": r["stage_frac_of_bound"]
+                                       for r in stages},
             "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_F16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(ach / PEAK_F16_TFLOPS, 4),
                          "flops": flops_tot,
