@@ -165,6 +165,10 @@ static __device__ __attribute__((aligned(16))) float kZeros8[8] = {0.f, 0.f, 0.f
                                                                     0.f, 0.f, 0.f, 0.f};
 static __device__ __attribute__((aligned(16))) float kOnes8[8] = {1.f, 1.f, 1.f, 1.f,
                                                                    1.f, 1.f, 1.f, 1.f};
+// An absent addend that must leave every value as it is: x + (-0) == x for all x, -0 included
+// (x + 0 turns -0 into +0).
+static __device__ __attribute__((aligned(16))) float kNegZeros8[8] = {-0.f, -0.f, -0.f, -0.f,
+                                                                       -0.f, -0.f, -0.f, -0.f};
 
 // Address of the 8-float parameter chunk starting at element i, or of a constant row when the
 // vector is absent.
@@ -189,8 +193,11 @@ __device__ __forceinline__ void load_f32x4(const float* p, size_t i, float* v) {
 // Stegun, Handbook of Mathematical Functions, formula 7.1.26, absolute error below 1.5e-7 for every
 // z >= 0. The rounding of 1 - e adds at most |x| 2^-25 absolute. Both stay below the fp32 tolerance
 // of this path (1e-6 + 1e-5 |gelu|) over the whole range; past |x| ~ 13 e underflows to 0 and the
-// result is exactly x (x > 0) or 0 (x < 0). +inf gives inf, -inf and NaN give NaN, like the
-// reference. 12 VALU operations plus two transcendentals (v_rcp_f32, v_exp_f32) per element.
+// result is exactly x (x > 0) or -0 (x < 0). The result takes the sign of x: the reference's
+// product 0.5f * x * (1 + erf) is -0 wherever it is zero for a negative x (x = -0, and every x
+// whose erff rounds to -1), and the sum above would give +0 there. +inf gives inf, -inf and NaN
+// give NaN, like the reference. 13 VALU operations plus two transcendentals (v_rcp_f32,
+// v_exp_f32) per element.
 __device__ __forceinline__ float gelu_erf(float x) {
   const float ax = __builtin_fabsf(x);
   const float zz = ax * 0.84932180028801904f;  // |x| sqrt(log2(e) / 2): exp(-x^2/2) = 2^-(zz^2)
@@ -201,7 +208,7 @@ __device__ __forceinline__ float gelu_erf(float x) {
   p = __builtin_fmaf(p, t, -0.284496736f);
   p = __builtin_fmaf(p, t, 0.254829592f);
   const float e = (p * t) * __builtin_amdgcn_exp2f(-(zz * zz));
-  return 0.5f * __builtin_fmaf(ax, 1.f - e, x);
+  return __builtin_copysignf(0.5f * __builtin_fmaf(ax, 1.f - e, x), x);
 }
 
 // ---- streaming threshold ---------------------------------------------------------------------------

@@ -55,7 +55,8 @@ __global__ __launch_bounds__(kBlock) void bias_act_tile(BaArgs a) {
   const long c = (bx << a.wshift) + tc;
   if (c >= a.nch) return;  // no barriers below: idle lanes of a partial tile just leave
   float bi[V];
-  const float* bp = param_or(a.bias, static_cast<size_t>(c) * V, kZeros8);
+  // no bias: add -0, which changes nothing (the reference applies no bias add at all)
+  const float* bp = param_or(a.bias, static_cast<size_t>(c) * V, kNegZeros8);
 #pragma unroll
   for (int k = 0; k < V; k += 4) load_f32x4(bp, k, &bi[k]);
   const long r0 = by * static_cast<long>(P) * U + tr;
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(kBlock) void bias_act_generic(BaArgs a) {
   for (long i = static_cast<long>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
     const long r = i / a.n, c = i - r * a.n;
     const size_t off = static_cast<size_t>(r) * a.ld + c;
-    const float b = a.bias ? a.bias[c] : 0.f;
+    const float b = a.bias ? a.bias[c] : -0.f;
     S::store1(a.y, off, act_apply<ACT>(S::load1(a.x, off) + b, a.slope));
   }
 }

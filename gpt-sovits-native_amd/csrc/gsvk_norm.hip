@@ -248,6 +248,19 @@ __device__ __forceinline__ double block_sum(float v, double* red) {
 // configuration's [512, 31999] every channel is resident at once: the call is one read of the
 // tensor, the reductions, and one write.
 constexpr int kGrBlock = 512;
+constexpr int kGrWaves = kGrBlock / kWave;
+
+__device__ __forceinline__ double block_sum512(float v, double* red) {
+  const float w_sum = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = static_cast<double>(w_sum);
+  lds_barrier();
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kGrWaves; ++i) t += red[i];
+  lds_barrier();
+  return t;
+}
 
 // A channel row as this thread sees it: head elements up to the first 128-byte boundary, nbody
 // 16-byte chunks (thread t owns chunks t, t + 1024, ...), then fewer than one chunk of tail
@@ -394,44 +407,19 @@ __global__ __launch_bounds__(kGnBlock) void gn_gelu_vec(GnArgs a) {
   }
 }
 
-// A double moved between the lanes of a DPP row (both 32-bit halves by the same control).
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const uint32_t lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u), CTRL, 0xf, 0xf, true);
-  const uint32_t hi =
-      __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, 0xf, 0xf, true);
-  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
-}
-// Sum over the 16 lanes of each row; every lane of the row gets the same bits (each step adds
-// the same two operands in every lane, in either order).
-__device__ __forceinline__ double row_sum_f64(double v) {
-  v += dpp_f64<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f64<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f64<0x141>(v);  // row_half_mirror
-  v += dpp_f64<0x140>(v);  // row_mirror
-  return v;
-}
-
 // One channel per workgroup. The row layout is gn_row's (head to the first 128-byte line, 16-byte
 // body chunks, tail), for 512 threads: thread t owns body chunks t, t + 512, ... and head / tail
 // element t. Chunks past the body load the body's last chunk and count as zero (every load is
-// unconditional, so all of them are in flight together).
-// Statistics with one workgroup barrier: each wave takes its sum s, count n and the second moment
-// q about its own fp32 mean m = s / n with DPP reductions alone (fp32 partial sums per thread, fp32
-// wave sums); after one LDS exchange, lane i of every row holds wave i's triple and the merge runs
-// in double, exactly (Chan et al.'s pairwise update, written for a mean m that is not the wave's
-// exact one): the wave's sum of (x - M)^2 about the row mean M is q + 2 (m - M)(s - n m) + n (m - M)^2.
-// Launch bounds of four waves per SIMD (at most 128 VGPRs; the fp32 16-chunk form needs 120) keep a
-// second channel resident on every CU.
+// unconditional, so all of them are in flight together). The statistics are gn_gelu_vec's: fp32
+// partial sums, wave sums in fp32, the block sum in double, the centred second moment corrected by
+// the fp32 mean's offset. Launch bounds of four waves per SIMD (at most 128 VGPRs) keep a second
+// channel resident on every CU.
 template <int DT, int CPT, bool NT>
 __global__ __launch_bounds__(kGrBlock, 4) void gn_gelu_row(GnArgs a) {
   using S = Store<DT>;
   constexpr int V = S::VEC;
   constexpr int ESZ = DT == GSVK_F32 ? 4 : 2;
-  constexpr int NW = kGrBlock / kWave;
-  static_assert(NW <= 16, "one wave per lane of a DPP row");
-  __shared__ double red[3 * NW];
+  __shared__ double red[kGrWaves];
   const long ch = blockIdx.x;
   const size_t base = static_cast<size_t>(ch) * static_cast<size_t>(a.ld);
   const uintptr_t addr = reinterpret_cast<uintptr_t>(a.x) + base * ESZ;
@@ -464,13 +452,8 @@ __global__ __launch_bounds__(kGrBlock, 4) void gn_gelu_row(GnArgs a) {
     for (int i = 0; i < V; ++i) cs += v[i];
     s += k < nbody ? cs : 0.f;
   }
-  // this thread's element count: its chunks below nbody, and its head / tail element
-  long nk = (nbody - t + kGrBlock - 1) / kGrBlock;
-  nk = nk < 0 ? 0 : (nk > CPT ? CPT : nk);
-  const float cnt = static_cast<float>(nk * V + (e_idx >= 0 ? 1 : 0));
-  float ws, wn;
-  wave_sum2(s, cnt, ws, wn);
-  const float m = wn > 0.f ? ws / wn : 0.f;
+  const double mean_d = block_sum512(s, red) / static_cast<double>(a.T);
+  const float mean = static_cast<float>(mean_d);
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
@@ -480,37 +463,20 @@ __global__ __launch_bounds__(kGrBlock, 4) void gn_gelu_row(GnArgs a) {
     float cq = 0.f;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      const float d = v[i] - m;
+      const float d = v[i] - mean;
       cq = __builtin_fmaf(d, d, cq);
     }
     q += k < nbody ? cq : 0.f;
   }
   if (e_idx >= 0) {
-    const float d = e - m;
+    const float d = e - mean;
     q = __builtin_fmaf(d, d, q);
   }
-  const float wq = wave_sum(q);
-  if ((t & (kWave - 1)) == 0) {
-    const int w = t / kWave;
-    red[3 * w] = static_cast<double>(wn);
-    red[3 * w + 1] = static_cast<double>(ws);
-    red[3 * w + 2] = static_cast<double>(wq);
-  }
-  lds_barrier();
-  const int r = t & 15;
-  const double n = r < NW ? red[3 * r] : 0.0, sw = r < NW ? red[3 * r + 1] : 0.0;
-  const double qw = r < NW ? red[3 * r + 2] : 0.0;
-  const double mean_d = row_sum_f64(sw) / static_cast<double>(a.T);
-  // the wave's m, recomputed from the same fp32 operands
-  const double mw =
-      n > 0.0 ? static_cast<double>(static_cast<float>(sw) / static_cast<float>(n)) : 0.0;
-  const double dm = mw - mean_d;
-  const double var =
-      row_sum_f64(qw + 2.0 * dm * (sw - n * mw) + n * dm * dm) / static_cast<double>(a.T);
-  const float mean = static_cast<float>(mean_d);
+  const double dm = mean_d - static_cast<double>(mean);
+  const double var = block_sum512(q, red) / static_cast<double>(a.T) - dm * dm;
   const float rstd = static_cast<float>(1.0 / sqrt((var > 0.0 ? var : 0.0) + a.eps));
-  // Every thread has read all of its elements before any thread writes (the statistics end in a
-  // workgroup barrier), so y == x in place is safe.
+  // Every thread has read all of its elements before any thread writes (the reductions above end
+  // in workgroup barriers), so y == x in place is safe.
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     const long k = t + static_cast<long>(c) * kGrBlock;

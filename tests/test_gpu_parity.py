@@ -182,6 +182,9 @@ def test_gelu_special_values():
     fin = np.isfinite(want)
     assert_close(F32, got[fin], want[fin], "gelu special")
     assert got[0, 0] == 0 and got[0, 6] == 30.0 and got[0, 7] == 0
+    # the reference's 0.5f * x * (1 + erff) keeps the sign of x on zero results: -0 -> -0, -30 -> -0
+    np.testing.assert_array_equal(np.signbit(got[fin]), np.signbit(want[fin]))
+    assert np.signbit(got[0, 1]) and np.signbit(got[0, 7]) and not np.signbit(got[0, 0])
     assert got[0, 8] == np.inf and np.isnan(got[0, 9])  # 0.5f*x*(1+erff(x)) at +-inf
 
 
@@ -198,7 +201,11 @@ def test_gelu_dense_sweep(dt):
     X = dev(x, dt)
     gsvk.bias_act(gsvk.ACT_GELU_ERF, X, X)
     sync()
-    assert_close(dt, host(X, dt), want, "gelu sweep")
+    got = host(X, dt)
+    assert_close(dt, got, want, "gelu sweep")
+    # signs agree everywhere, zeros included (x <= -5.5 rounds erff to -1: the reference gives -0)
+    g32, w32 = O.to_f32(dt, got), O.to_f32(dt, want)
+    np.testing.assert_array_equal(np.signbit(g32), np.signbit(w32))
 
 
 # ---- GroupNorm + GELU --------------------------------------------------------------------------

@@ -266,6 +266,10 @@ def test_gelu_erf_closed_form_and_identities():
         exact = 0.5 * x * (1 + math.erf(x / math.sqrt(2)))
         assert abs(g - exact) <= 1e-6 + 1e-5 * abs(exact), (x, g, exact)
     assert O.gelu_erf(np.array([0.0], np.float32))[0] == 0
+    # 0.5f * x * (1 + erff(.)) is a product: a zero result carries the sign of x (IEEE 754 product
+    # sign rule), so -0 stays -0 and erff(-30 / sqrt2) = -1 gives (-15) * 0 = -0
+    z = O.gelu_erf(np.array([0.0, -0.0, -30.0, -8.0], np.float32))
+    assert list(np.signbit(z)) == [False, True, True, True] and z[2] == 0
     # GELU(x) - GELU(-x) = x (the erf part is odd)
     pos = O.gelu_erf(xs)
     neg = O.gelu_erf(-xs)
