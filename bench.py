@@ -1321,6 +1321,72 @@ def copy_bandwidth(torch, dev, nbytes=1 << 30):
     return round(gbs, 1)
 
 
+DIAG_COPY = ("row_resident_nt_stores", "row_resident_cached_stores", "block_nt_stores",
+             "block_cached_stores")
+DIAG_READ = ("gemv_fragment_loads", "contiguous_rows", "direct_to_lds_depth2",
+             "direct_to_lds_depth4", "block_read")
+
+
+def diag_forms(torch, dev):
+    """Ceilings of the access patterns the streaming kernels use, from the measurement kernels of
+    gpt-sovits-native_amd/diag/gsvk_diag.hip (libgsvk_diag.so):
+
+    - copy forms over a [4096, 32000] fp32-sized tensor (524 MB read + 524 MB written), as a whole
+      row per workgroup (all of a row's loads before any store: GroupNorm's order) and as one-shot
+      32 KiB blocks (the element-wise streams' order), each with non-temporal or cached stores;
+    - read forms of a 128 MiB weight stream in 32-row batches, one 4-wave workgroup per CU (the
+      long-stream GEMV's partition): its fragment loads, contiguous rows, direct-to-LDS loads at
+      two and four batches in flight, and a plain one-shot read.
+
+    Each form: the median of 9 launches with the MALL cleared before each (how every suite line is
+    timed), and 10 launches back to back (per launch; no clearing: a launch then also pays for the
+    write-back of the dirty lines the one before it left in the MALL)."""
+    import ctypes
+    path = os.path.join(ROOT, "gpt-sovits-native_amd", "libgsvk_diag.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run make -C gpt-sovits-native_amd libgsvk_diag.so")
+    lib = ctypes.CDLL(path)
+    lib.gsvk_diag_copy.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                   ctypes.c_size_t, ctypes.c_void_p]
+    lib.gsvk_diag_stream_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                          ctypes.c_void_p, ctypes.c_void_p]
+    flush = Flusher(torch, dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    out = {"copy": {}, "read": {}}
+
+    def timed(call, nbytes):
+        rc = call()
+        if rc != 0:
+            raise RuntimeError(f"diag call returned {rc}")
+        one = measure_reps(torch, call, flush)
+        flush()
+        ten = time_loop(torch, call, 10, warmup=0)
+        return {"one_us": round(one * 1e3, 1), "one_frac": round(nbytes / one / 1e6 / PEAK_GBS, 4),
+                "x10_us": round(ten * 1e3, 1), "x10_frac": round(nbytes / ten / 1e6 / PEAK_GBS, 4)}
+
+    rows, row_bytes = 4096, 128000
+    x = torch.ones(rows * row_bytes, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    for f, name in enumerate(DIAG_COPY):
+        out["copy"][name] = timed(
+            lambda f=f: lib.gsvk_diag_copy(f, x.data_ptr(), y.data_ptr(), rows, row_bytes, stream),
+            2 * rows * row_bytes)
+        progress(f"diag copy {name}: {out['copy'][name]}")
+    del x, y
+    torch.cuda.empty_cache()
+    wrows = 131072
+    w = torch.ones(wrows * 1024, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    for f, name in enumerate(DIAG_READ):
+        out["read"][name] = timed(
+            lambda f=f: lib.gsvk_diag_stream_read(f, w.data_ptr(), wrows, sink.data_ptr(), stream),
+            wrows * 1024)
+        progress(f"diag read {name}: {out['read'][name]}")
+    del w
+    torch.cuda.empty_cache()
+    return out
+
+
 def write_bandwidth(torch, dev, nbytes=1 << 30):
     """A write-only stream of 1 GiB (torch's fill kernel: 16-byte stores, nothing read), timed like
     the replicated kernels: the achievable HBM write bandwidth, the ceiling of write-dominated
@@ -1563,6 +1629,9 @@ def main():
     ap.add_argument("--line-traffic", default=None, metavar="LINES",
                     help="FETCH_SIZE / WRITE_SIZE per replicated launch of the named suite lines "
                          "(comma-separated, or 'all'), each from two rocprofv3 --pmc child runs")
+    ap.add_argument("--diag", action="store_true",
+                    help="the copy and weight-stream read forms of libgsvk_diag.so (access-pattern "
+                         "ceilings) and exit")
     ap.add_argument("--cpu-lines", action="store_true",
                     help="the oracle's CPU baseline of every suite line only")
     ap.add_argument("--detail", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
@@ -1604,6 +1673,9 @@ def main():
         return
     if a.only == "write_bandwidth":
         write_bandwidth(torch, dev)
+        return
+    if a.diag:
+        print(json.dumps(diag_forms(torch, dev)), flush=True)
         return
     if a.only:
         kernel_suite(torch, gsvk, dev, only=a.only)
