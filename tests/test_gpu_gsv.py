@@ -32,6 +32,25 @@ def test_upload_arenas_bit_exact(tmp_path):
             assert name not in v16
 
 
+def test_upload_reference_converter_file_bit_exact():
+    """The arenas of a file the reference's convert.py wrote (tests/golden/convert_gsv1_small.gsv)
+    arrive bit for bit: every device view equals the file's bytes at the directory's offsets."""
+    from test_gsv_loader import GOLDEN_GSV
+    raw = open(GOLDEN_GSV, "rb").read()
+    g = gsvk.GsvFile(GOLDEN_GSV)
+    a16, v16 = g.upload(gsvk.F16)
+    a32, v32 = g.upload(gsvk.F32)
+    torch.cuda.synchronize()
+    assert set(v32) == set(g.tensors) and set(v16) == {"enc.weight", "dec.lin.weight"}
+    for name, info in g.tensors.items():
+        want = np.frombuffer(raw, np.uint32, info["numel"], info["f32_offset"])
+        assert np.array_equal(v32[name].cpu().numpy().view(np.uint32).ravel(), want), name
+        if info["f16_nbytes"]:
+            want = np.frombuffer(raw, np.uint16, info["numel"], info["f16_offset"])
+            assert np.array_equal(v16[name].cpu().numpy().view(np.uint16).ravel(), want), name
+    g.close()
+
+
 def test_decode_step_from_gsv_matches_oracle(tmp_path):
     D, H, FF, L, V, B, max_len = 128, 4, 256, 2, 50, 5, 64
     t, cfg = t2s_tensors(D, H, FF, L, V, seed=5)

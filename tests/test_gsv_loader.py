@@ -3,6 +3,7 @@ test_gpu_gsv.py. Mirrors the reference's tests/test_gsv_header.cpp and test_gsv_
 synthetic ar_s1-shaped file in place of weights/ar_s1v3.gsv (not available here), plus every
 malformed-directory rule gsv_loader.cpp:46-108 enforces."""
 import ctypes
+import os
 import struct
 
 import numpy as np
@@ -155,3 +156,100 @@ def test_bad_config_json_and_missing_file(tmp_path):
     with pytest.raises(gsvk.GsvkError) as e:
         gsvk.GsvFile(str(tmp_path / "missing.gsv"))
     assert e.value.status == gsvk.E_IO
+
+
+# ---- a file the reference's converter wrote (tests/golden/make_gsv_fixture.py) ----------------
+
+GOLDEN_GSV = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                          "convert_gsv1_small.gsv")
+
+
+def converter_inputs(seed=20261202):
+    """The state dict make_gsv_fixture.py gave the converter, as numpy arrays (same seed and draw
+    order), keyed by name after the converter's prefix stripping."""
+    r = np.random.default_rng(seed)
+    f32 = lambda *s: r.standard_normal(s).astype(np.float32)
+    f16 = lambda *s: r.standard_normal(s).astype(np.float16)
+    return {"enc.weight": f32(64, 64), "enc.bias": f32(64), "dec.lin.weight": f16(32, 160),
+            "dec.lin.bias": f16(32), "dec.conv.weight_g": f16(16, 1, 1),
+            "dec.conv.weight_v": f16(16, 8, 3), "big.weight_g": f32(64, 1, 1),
+            "big.weight_v": f32(64, 16, 4), "enc.pos_conv_embed.conv.weight_g": f32(1, 1, 5),
+            "enc.pos_conv_embed.conv.weight_v": f32(8, 4, 5)}
+
+
+def converter_expected():
+    """What the converter's rules (convert.py:58-100, 102-183) make of those inputs, restated:
+    prefixes stripped; weight = g v / ||v|| over every dim but 0 (over dims 0 and 1 for
+    pos_conv_embed.conv.), in float64 here; integer tensors dropped; an fp16 copy for every tensor of
+    >= 4096 elements that is not a fused weight-norm product. name -> (fp32 values, src dtype,
+    has fp16 copy)."""
+    x = converter_inputs()
+
+    def fuse(base, dims):
+        g = x[base + "weight_g"].astype(np.float64)
+        v = x[base + "weight_v"].astype(np.float64)
+        return g * v / np.sqrt((v * v).sum(axis=dims, keepdims=True))
+
+    exp = {}
+    for name in ("enc.weight", "enc.bias", "dec.lin.weight", "dec.lin.bias"):
+        a = x[name]
+        exp[name] = (a.astype(np.float64), 1 if a.dtype == np.float32 else 2, a.size >= 4096)
+    exp["dec.conv.weight"] = (fuse("dec.conv.", (1, 2)), 1, False)
+    exp["big.weight"] = (fuse("big.", (1, 2)), 1, False)
+    exp["enc.pos_conv_embed.conv.weight"] = (fuse("enc.pos_conv_embed.conv.", (0, 1)), 1, False)
+    return exp
+
+
+def test_reference_converter_file_directory():
+    """The loader's view of a file written by the reference's convert.py: header, config, every
+    directory field, and the converter's layout (64-byte aligned segments, all fp32 blocks in
+    directory order before all fp16 blocks)."""
+    g = gsvk.GsvFile(GOLDEN_GSV)
+    exp = converter_expected()
+    assert (g.version, g.name, g.n_tensors, g.flags) == (1, "fixture_small", len(exp), 1)
+    meta = g.config["meta"]
+    assert g.config["model_config"] is None
+    assert (meta["model"], meta["converter"], meta["weight_norm_fused"]) == \
+        ("fixture_small", "convert.py GSV1", 3)
+    assert set(g.tensors) == set(exp)  # prefixes stripped, pairs fused, integer tensors dropped
+    ends32, f16_starts = [], []
+    for name, (vals, src, has16) in exp.items():
+        info = g.tensors[name]
+        assert info["dims"] == vals.shape and info["numel"] == vals.size, name
+        assert info["src_dtype"] == src, name
+        assert info["f32_nbytes"] == 4 * vals.size and info["f32_offset"] % 64 == 0, name
+        assert (info["f16_nbytes"] == 2 * vals.size) if has16 else (info["f16_nbytes"] == 0), name
+        ends32.append(info["f32_offset"] + info["f32_nbytes"])
+        if has16:
+            assert info["f16_offset"] % 64 == 0
+            f16_starts.append(info["f16_offset"])
+    assert min(f16_starts) >= max(ends32)
+    offs = [g.tensors[n]["f32_offset"] for n in g.tensors]
+    assert offs == sorted(offs)
+    g.close()
+
+
+def test_reference_converter_file_values():
+    """Every tensor read at the loader's offsets: fp32 copies of the sources exactly, the fused
+    weight-norm products within fp32 rounding of the float64 closed form (and the pos_conv tensor
+    fused over dims 0 and 1: the default dims give values far from it), fp16 copies as the fp32
+    sources rounded to nearest even."""
+    raw = open(GOLDEN_GSV, "rb").read()
+    g = gsvk.GsvFile(GOLDEN_GSV)
+    x = converter_inputs()
+    for name, (vals, src, has16) in converter_expected().items():
+        info = g.tensors[name]
+        got = np.frombuffer(raw, np.float32, vals.size, info["f32_offset"]).reshape(vals.shape)
+        if name in x:
+            np.testing.assert_array_equal(got, x[name].astype(np.float32))
+        else:
+            np.testing.assert_allclose(got, vals, rtol=2e-6, atol=1e-7, err_msg=name)
+        if has16:
+            h = np.frombuffer(raw, np.uint16, vals.size, info["f16_offset"])
+            assert np.array_equal(h, x[name].astype(np.float16).view(np.uint16).ravel()), name
+    v = x["enc.pos_conv_embed.conv.weight_v"].astype(np.float64)
+    default = x["enc.pos_conv_embed.conv.weight_g"] * v / np.sqrt((v * v).sum(axis=(1, 2), keepdims=True))
+    info = g.tensors["enc.pos_conv_embed.conv.weight"]
+    got = np.frombuffer(raw, np.float32, v.size, info["f32_offset"]).reshape(v.shape)
+    assert np.abs(got - default).max() > 0.1
+    g.close()
