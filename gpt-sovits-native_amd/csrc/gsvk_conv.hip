@@ -318,7 +318,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
   };
-  auto stage = [&](int c) {
+  // Tiles whose staged columns all lie inside [0, T), with a whole channel group, skip the
+  // per-element zeroing of padding columns and channels; the input LeakyReLU is chosen once per
+  // chunk. The values staged are the same either way.
+  const bool interior = t0 + m.xoff >= 0 && t0 + m.xoff + TTH <= a.T;
+  auto stage_rows = [&](auto fast, auto act, int c) {
     const long ch0 = static_cast<long>(c) * kChunk + 8 * g;
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
@@ -328,9 +332,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       h8 hi, lo;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float xv = DT == GSVK_F32 ? __builtin_bit_cast(float, raw[u][j]) : h2f(raw[u][j]);
-        float v = tok && ch0 + j < a.cin ? xv : 0.f;
-        if (a.xact) v = lrelu_ref(v, a.slope);  // the input pre-activation (0 stays 0)
+        float v = DT == GSVK_F32 ? __builtin_bit_cast(float, raw[u][j]) : h2f(raw[u][j]);
+        if constexpr (!decltype(fast)::value) v = tok && ch0 + j < a.cin ? v : 0.f;
+        if constexpr (decltype(act)::value) v = lrelu_ref(v, a.slope);  // the input pre-activation
         hi[j] = static_cast<_Float16>(v);
         if constexpr (P == 2) {  // an infinite x leaves inf - inf: its remainder is 0
           const float rest = v - static_cast<float>(hi[j]);
@@ -340,6 +344,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       *reinterpret_cast<h8*>(xs + (static_cast<size_t>(g) * TTH + tp) * 8) = hi;
       if constexpr (P == 2)
         *reinterpret_cast<h8*>(xs + (static_cast<size_t>(4 + g) * TTH + tp) * 8) = lo;
+    }
+  };
+  auto stage = [&](int c) {
+    if (interior && static_cast<long>(c) * kChunk + 8 * g + 8 <= a.cin) {
+      if (a.xact) stage_rows(std::true_type{}, std::true_type{}, c);
+      else stage_rows(std::true_type{}, std::false_type{}, c);
+    } else {
+      if (a.xact) stage_rows(std::false_type{}, std::true_type{}, c);
+      else stage_rows(std::false_type{}, std::false_type{}, c);
     }
   };
 
