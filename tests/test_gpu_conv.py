@@ -388,6 +388,27 @@ def test_wide_tiles_transposed():
 
 
 @pytest.mark.parametrize("dt,round_x", [(F32, False), (F32, True), (F16, False)])
+def test_partial_channel_groups_on_interior_tiles(dt, round_x):
+    """C_in = 45 over 5003 columns: most time tiles lie inside the sequence, and the second 32-channel
+    chunk holds 13 channels, one whole 8-channel group and one partial (and two empty). Staging takes
+    its interior path for the whole groups and the zeroing path for the others in the same tile.
+    Against the oracle with the residual epilogue, and, reading lrelu(x) as it loads, bit for bit
+    the convolution of the materialised lrelu(x)."""
+    check_case(dt, 45, 40, 5003, 5, 2, epi=gsvk.CONV_EPI_RES_LRELU, round_x=round_x,
+               seed=640 + dt + 2 * round_x, what="partial groups")
+    r = rng(650 + dt + 2 * round_x)
+    x, w, b, _ = make(r, 45, 40, 5003, 5, dt)
+    xd = dev(x, dt)
+    conv = gsvk.Conv1d(dev(w, F16), devf(b), 2)
+    ya = conv.forward(xd, epi=gsvk.CONV_EPI_LRELU | gsvk.CONV_X_LRELU, slope=0.1, round_x=round_x)
+    xl = torch.empty_like(xd)
+    gsvk.leaky_relu(xd, xl, 0.1)
+    yb = conv.forward(xl, epi=gsvk.CONV_EPI_LRELU, slope=0.1, round_x=round_x)
+    torch.cuda.synchronize()
+    assert torch.equal(ya.view(torch.int16), yb.view(torch.int16))
+
+
+@pytest.mark.parametrize("dt,round_x", [(F32, False), (F32, True), (F16, False)])
 def test_x_lrelu_input_equals_materialized_lrelu(dt, round_x):
     """GSVK_CONV_X_LRELU reads lrelu(x, slope) as the convolution loads x: bit for bit the same as
     materialising lrelu(x) first (gsvk_leaky_relu, one rounding to the storage type) and convolving
