@@ -679,6 +679,25 @@ def conv_bound(flops, nbytes, us):
             "frac_of_bound": round(frac, 4)}
 
 
+def conv_one(torch, gsvk, dev, spec, launches=20):
+    """One SoVITS ResBlock convolution, C -> C channels over T frames with kernel k, dilation dil and
+    epilogue epi (spec "C,T,k,dil,epi"; fp32 activations, exact): 2 warm-up launches, then
+    `launches` timed ones. For rocprofv3 --pmc runs on one convolution shape."""
+    C, T, k, dil, epi = (int(v) for v in spec.split(","))
+    x = torch.randn(C, T, device=dev)
+    y = torch.empty(C, T, device=dev)
+    cur = torch.randn(C, T, device=dev)
+    conv = gsvk.Conv1d((torch.randn(C, C, k, device=dev) / (C * k) ** 0.5).half(),
+                       torch.randn(C, device=dev) * 0.05, dil)
+    fn = lambda: conv.forward(x, y, epi=epi, cur=cur)
+    us = time_loop(torch, fn, launches, warmup=2) * 1e3
+    fl = 2.0 * C * C * k * T
+    res = (epi in (gsvk.CONV_EPI_RES_LRELU, gsvk.CONV_EPI_RES))
+    nb = C * T * 4 * (2 + (2 if res else 0)) + C * C * k * 2 + C * 4
+    return {"conv": spec, "launches": launches, "us_per_launch": round(us, 2),
+            "TFLOPs": round(fl / us / 1e6, 1), **conv_bound(fl, nb, us)}
+
+
 def sovits_conv(torch, gsvk, dev, geometry="reference_768"):
     """Per decoder stage (C, T): the upsampler (ConvT1d into the stage) and every distinct ResBlock
     convolution timed once (conv1: k x dilation 1 / 3 / 5 with the LeakyReLU epilogue; conv2: k,
@@ -1629,6 +1648,8 @@ def main():
     ap.add_argument("--line-traffic", default=None, metavar="LINES",
                     help="FETCH_SIZE / WRITE_SIZE per replicated launch of the named suite lines "
                          "(comma-separated, or 'all'), each from two rocprofv3 --pmc child runs")
+    ap.add_argument("--conv-one", default=None, metavar="C,T,K,DIL,EPI",
+                    help="one SoVITS ResBlock convolution shape, 22 launches (rocprofv3 --pmc runs)")
     ap.add_argument("--diag", action="store_true",
                     help="the copy and weight-stream read forms of libgsvk_diag.so (access-pattern "
                          "ceilings) and exit")
@@ -1676,6 +1697,9 @@ def main():
         return
     if a.diag:
         print(json.dumps(diag_forms(torch, dev)), flush=True)
+        return
+    if a.conv_one:
+        print(json.dumps(conv_one(torch, gsvk, dev, a.conv_one)), flush=True)
         return
     if a.only:
         kernel_suite(torch, gsvk, dev, only=a.only)
