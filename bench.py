@@ -1234,67 +1234,100 @@ def cpu_kernel_baselines(names=None):
     return out, tall
 
 
-def next_tier_cpu(reps=3):
-    """Bounded CPU samples of the next-tier rows on the oracle's C restatement (one thread; the
-    reference's own NEON / Accelerate code does not build on x86): one T2S decoder layer of the
-    whole decode step at B = 64, kv_len 1024 (scaled to 24 layers + the logits GEMV), and a
-    1,000-column window of the 192 x 40000, k 11, dilation 5 ResBlock convolution (scaled to 40,000
-    columns). Median of `reps` runs each."""
+def next_tier_cpu(reps=3, which=("step", "conv")):
+    """The next-tier rows whole, on the oracle's C restatement (the reference's own NEON /
+    Accelerate code does not build on x86), on every allowed host thread (cpu_threads_all; ctypes
+    releases the interpreter lock for each oracle call):
+    - the whole T2S decode step at B = 64, kv_len 1024: 24 decoder layers, each with its own
+      weights and fp16 K / V caches (3.2 GB in all), and the logits GEMV; the sequences split into
+      one band per thread, each band running every layer on its sequences;
+    - the 192 x 40000, k 11, dilation 5 ResBlock convolution with the LeakyReLU epilogue, its
+      columns split into one band per thread, each band with its halo of (k - 1) dil columns.
+    Median of `reps` runs each (after one untimed run); `which` picks the rows."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
 
     import oracle as O
     r = np.random.default_rng(SEED + 11)
+    threads = cpu_threads_all()
+
+    def filled(shape):
+        # fp16 storage tiled from a block of random values: every element finite, quick to build
+        return np.resize(O.to_storage(O.F16, r.standard_normal(1 << 20).astype(np.float32)), shape)
+
     w = lambda n, k: (0.05 * r.standard_normal((n, k))).astype(np.float16).view(np.uint16)
     vec = lambda n, m=0.0: (m + 0.02 * r.standard_normal(n)).astype(np.float32)
     H, KV = 16, 1024
-    x = O.to_storage(O.F16, r.standard_normal((B, D)).astype(np.float32))
-    ly = dict(wqkv=w(3 * D, D), bqkv=vec(3 * D), wout=w(D, D), bout=vec(D), n1g=vec(D, 1.0),
-              n1b=vec(D), w1=w(FF, D), b1=vec(FF), w2=w(D, FF), b2=vec(D), n2g=vec(D, 1.0),
-              n2b=vec(D))
-    kc = O.to_storage(O.F16, r.standard_normal((B, KV + 1, D)).astype(np.float32))
-    vc = O.to_storage(O.F16, r.standard_normal((B, KV + 1, D)).astype(np.float32))
+    layers = [] if "step" not in which else [dict(wqkv=w(3 * D, D), bqkv=vec(3 * D), wout=w(D, D), bout=vec(D),
+                   n1g=vec(D, 1.0), n1b=vec(D), w1=w(FF, D), b1=vec(FF), w2=w(D, FF), b2=vec(D),
+                   n2g=vec(D, 1.0), n2b=vec(D),
+                   kc=filled((B, KV + 1, D)), vc=filled((B, KV + 1, D)))
+              for _ in range(LAYERS)]
+    x0 = O.to_storage(O.F16, r.standard_normal((B, D)).astype(np.float32))
     kv_pos = np.full(B, KV, np.int64)
     w_logits = w(VOCAB, D)
 
-    def layer():
-        qkv = O.gemv_f16w(O.F16, x, ly["wqkv"], O.F32, bias=ly["bqkv"])
-        attn = O.to_storage(O.F16, O.decode_attention(O.F16, qkv, kc, vc, kv_pos, H, D // H))
-        z = O.gemv_f16w(O.F16, attn, ly["wout"], O.F16, bias=ly["bout"], residual=x)
-        h = O.add_layernorm(O.F16, z, ly["n1g"], ly["n1b"], 1e-5)
-        ff = O.gemv_f16w(O.F16, h, ly["w1"], O.F16, bias=ly["b1"], act=1)
-        z = O.gemv_f16w(O.F16, ff, ly["w2"], O.F16, bias=ly["b2"], residual=h)
-        return O.add_layernorm(O.F16, z, ly["n2g"], ly["n2b"], 1e-5)
+    def step_band(lo, hi):
+        x = x0[lo:hi]
+        for ly in layers:
+            qkv = O.gemv_f16w(O.F16, x, ly["wqkv"], O.F32, bias=ly["bqkv"])
+            attn = O.to_storage(O.F16, O.decode_attention(O.F16, qkv, ly["kc"][lo:hi],
+                                                          ly["vc"][lo:hi], kv_pos[lo:hi], H,
+                                                          D // H))
+            z = O.gemv_f16w(O.F16, attn, ly["wout"], O.F16, bias=ly["bout"], residual=x)
+            h = O.add_layernorm(O.F16, z, ly["n1g"], ly["n1b"], 1e-5)
+            ff = O.gemv_f16w(O.F16, h, ly["w1"], O.F16, bias=ly["b1"], act=1)
+            z = O.gemv_f16w(O.F16, ff, ly["w2"], O.F16, bias=ly["b2"], residual=h)
+            x = O.add_layernorm(O.F16, z, ly["n2g"], ly["n2b"], 1e-5)
+        return O.gemv_f16w(O.F16, x, w_logits, O.F32)
 
-    def med(fn):
+    C, T, k, dil = 192, 40000, 11, 5
+    halo = (k - 1) * dil
+    xs = r.standard_normal((C, T + halo)).astype(np.float32)
+    wc = (r.standard_normal((C, C, k)) / np.sqrt(C * k)).astype(np.float16).view(np.uint16)
+    bc = vec(C)
+    conv_bands = _bands(T, threads)
+
+    def conv_band(lo, hi):
+        return O.conv1d(O.F32, np.ascontiguousarray(xs[:, lo:hi + halo]), wc, bc, dil, epi=1)
+
+    def med(pool, calls):
+        run = lambda: [f.result() for f in [pool.submit(c) for c in calls]]
+        run()
         ts = []
         for _ in range(reps):
             t0 = time.perf_counter()
-            fn()
+            run()
             ts.append(time.perf_counter() - t0)
         return statistics.median(ts)
 
-    t_layer = med(layer)
-    t_logits = med(lambda: O.gemv_f16w(O.F16, x, w_logits, O.F32))
-    step_s = LAYERS * t_layer + t_logits
-    C, T, k, dil, win = 192, 40000, 11, 5, 1000
-    xs = r.standard_normal((C, win + (k - 1) * dil)).astype(np.float32)
-    wc = (r.standard_normal((C, C, k)) / np.sqrt(C * k)).astype(np.float16).view(np.uint16)
-    t_conv = med(lambda: O.conv1d(O.F32, xs, wc, vec(C), dil, epi=1)) * T / xs.shape[1]
+    out = {}
     model = cpu_model()
-    return {
-        "t2s_whole_decode_step": {
-            "value": round(B / step_s, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        if "step" in which:
+            step_s = med(pool, [lambda lo=lo, hi=hi: step_band(lo, hi)
+                                for lo, hi in _bands(B, threads)])
+        if "conv" in which:
+            t_conv = med(pool, [lambda lo=lo, hi=hi: conv_band(lo, hi) for lo, hi in conv_bands])
+    del layers
+    if "step" in which:
+        out["t2s_whole_decode_step"] = {
+            "value": round(B / step_s, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "us_per_step": round(step_s * 1e6, 0),
-            "sample": f"one decoder layer (QKV GEMV, attention over {KV} cached fp16 rows, out-proj, "
-                      f"LN1, W1 + ReLU, W2, LN2) at B={B} x {LAYERS} + the logits GEMV; median of "
-                      f"{reps}", "cpu_model": model},
-        "sovits_conv_192x40000_k11_d5": {
-            "value": round(2.0 * C * C * k * T / t_conv / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
-            "kind": "port", "us": round(t_conv * 1e6, 0),
-            "sample": f"a {xs.shape[1]}-column window scaled by {T / xs.shape[1]:.1f} to {T} "
-                      f"columns, fp32 (the oracle multiplies exactly) with the LeakyReLU epilogue; median of {reps}",
-            "cpu_model": model},
-    }
+            "sample": f"the whole step: {LAYERS} decoder layers (QKV GEMV, attention over {KV} "
+                      f"cached fp16 rows, out-proj, LN1, W1 + ReLU, W2, LN2), each with its own "
+                      f"weights and caches, and the logits GEMV, at B={B}; sequences in {threads} "
+                      f"bands; median of {reps}", "cpu_model": model}
+    if "conv" in which:
+        out["sovits_conv_192x40000_k11_d5"] = {
+            "value": round(2.0 * C * C * k * T / t_conv / 1e12, 4), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port", "us": round(t_conv * 1e6, 0),
+            "sample": f"all {T} columns in {len(conv_bands)} bands, each with its {halo}-column "
+                      f"halo ({len(conv_bands) * halo} halo columns computed in all), fp32 (the "
+                      f"oracle multiplies exactly) with the LeakyReLU epilogue; median of {reps}",
+            "cpu_model": model}
+    return out
 
 
 # ---- decode-step ops, copy reference, counter workload ---------------------------------------------
@@ -1714,7 +1747,7 @@ def main():
         res = sovits_conv(torch, gsvk, dev)
         res["generator"] = sovits_generator(torch, gsvk, dev)
         if not a.no_cpu:
-            res["cpu_baseline"] = next_tier_cpu()["sovits_conv_192x40000_k11_d5"]
+            res["cpu_baseline"] = next_tier_cpu(which=("conv",))["sovits_conv_192x40000_k11_d5"]
         print(json.dumps(res), flush=True)
         return
 
