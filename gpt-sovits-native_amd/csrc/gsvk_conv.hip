@@ -118,6 +118,43 @@ __device__ __forceinline__ Map block_map(const ConvArgs& a) {
 template <int XM>
 constexpr int planes() { return XM == kXSplit ? 2 : 1; }
 
+// The staging conversions below cost a few VALU instructions per staged value, and they sit
+// between a workgroup's barriers, on the path of every chunk.
+//
+// lrelu(v, s) for 0 < s <= 1 as max(v, v s): the same bits as lrelu_ref (v < 0: v s > v; v >= 0:
+// v s <= v; -0 and +-inf give themselves; NaN stays NaN). One v_max_f32: fmaxf would first quiet
+// each operand with an instruction of its own.
+__device__ __forceinline__ float lrelu_max(float v, float s) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(v * s));
+  return r;
+}
+
+// Two values to one packed fp16 word (RNE), v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t pack_h2(float v0, float v1) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  const f2v p = {v0, v1};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(p, h2v));
+}
+
+// The remainders of the hi / lo split of two values, hi = pack_h2(v0, v1): f16(v0 - hi.lo) |
+// f16(v1 - hi.hi) << 16. Each is one v_fma_mix (the half converted, multiplied by m1 = -1, added
+// to v and the sum rounded to f16): v - hi is exact in fp32, so that is the value of a separate
+// conversion, subtraction and rounding. m1 is -1 held where the compiler cannot see it (a
+// constant -1 would turn the fma into a subtraction, which is not matched to v_fma_mix). An
+// infinite v leaves inf - inf = NaN there, which the packed max with -65504 (maxNum: the non-NaN
+// operand) turns into -65504: hi w + lo w is then still inf w (NaN for w = 0), as with a zero
+// remainder. Finite remainders are far inside +-65504.
+__device__ __forceinline__ uint32_t split_rest2(uint32_t hi, float v0, float v1, float m1) {
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  const h2v h = __builtin_bit_cast(h2v, hi);
+  const h2v r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h[0]), m1, v0)),
+                 static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h[1]), m1, v1))};
+  const h2v lim = {static_cast<_Float16>(-65504.f), static_cast<_Float16>(-65504.f)};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(r, lim));
+}
+
 template <int XM>
 constexpr int storage_dt() { return XM == kXF16 ? GSVK_F16 : GSVK_F32; }
 
@@ -319,9 +356,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
   };
   // Tiles whose staged columns all lie inside [0, T), with a whole channel group, skip the
-  // per-element zeroing of padding columns and channels; the input LeakyReLU is chosen once per
-  // chunk. The values staged are the same either way.
+  // per-element zeroing of padding columns and channels; the input LeakyReLU (act 1: the max form
+  // for slopes in (0, 1], 2: lrelu_ref) is chosen once per chunk. The values staged are the same
+  // either way.
   const bool interior = t0 + m.xoff >= 0 && t0 + m.xoff + TTH <= a.T;
+  float m1 = -1.f;
+  asm("" : "+s"(m1));
   auto stage_rows = [&](auto fast, auto act, int c) {
     const long ch0 = static_cast<long>(c) * kChunk + 8 * g;
 #pragma unroll
@@ -329,30 +369,47 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       const int tp = lane + kWave * u;
       const long t = t0 + m.xoff + tp;
       const bool tok = t >= 0 && t < a.T;
-      h8 hi, lo;
+      float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float v = DT == GSVK_F32 ? __builtin_bit_cast(float, raw[u][j]) : h2f(raw[u][j]);
-        if constexpr (!decltype(fast)::value) v = tok && ch0 + j < a.cin ? v : 0.f;
-        if constexpr (decltype(act)::value) v = lrelu_ref(v, a.slope);  // the input pre-activation
-        hi[j] = static_cast<_Float16>(v);
-        if constexpr (P == 2) {  // an infinite x leaves inf - inf: its remainder is 0
-          const float rest = v - static_cast<float>(hi[j]);
-          lo[j] = static_cast<_Float16>(rest == rest ? rest : 0.f);
-        }
+        v[j] = DT == GSVK_F32 ? __builtin_bit_cast(float, raw[u][j]) : h2f(raw[u][j]);
+        if constexpr (!decltype(fast)::value) v[j] = tok && ch0 + j < a.cin ? v[j] : 0.f;
+        if constexpr (decltype(act)::value == 1) v[j] = lrelu_max(v[j], a.slope);
+        else if constexpr (decltype(act)::value == 2) v[j] = lrelu_ref(v[j], a.slope);
       }
-      *reinterpret_cast<h8*>(xs + (static_cast<size_t>(g) * TTH + tp) * 8) = hi;
-      if constexpr (P == 2)
-        *reinterpret_cast<h8*>(xs + (static_cast<size_t>(4 + g) * TTH + tp) * 8) = lo;
+      if constexpr (P == 2) {  // the exact split: hi and lo planes
+        const u32x4 hi = {pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), pack_h2(v[4], v[5]),
+                          pack_h2(v[6], v[7])};
+        const u32x4 lo = {split_rest2(hi[0], v[0], v[1], m1), split_rest2(hi[1], v[2], v[3], m1),
+                          split_rest2(hi[2], v[4], v[5], m1), split_rest2(hi[3], v[6], v[7], m1)};
+        *reinterpret_cast<u32x4*>(xs + (static_cast<size_t>(g) * TTH + tp) * 8) = hi;
+        *reinterpret_cast<u32x4*>(xs + (static_cast<size_t>(4 + g) * TTH + tp) * 8) = lo;
+      } else {
+        // f2h2 rounds the LeakyReLU's product to fp32 before the rounding to fp16, as a LeakyReLU
+        // stored first would: with fp16 x the compiler would otherwise fuse both into one
+        // v_fma_mixlo (rounded once), another value where the fp32 product is an fp16 halfway case
+        // (slope 0.1: products in the fp16 subnormal range).
+        const u32x4 hi = {f2h2(v[0], v[1]), f2h2(v[2], v[3]), f2h2(v[4], v[5]), f2h2(v[6], v[7])};
+        *reinterpret_cast<u32x4*>(xs + (static_cast<size_t>(g) * TTH + tp) * 8) = hi;
+      }
     }
   };
+  // The max form pays off in the exact split, where the staging is longest; the one-plane modes
+  // (round_x, fp16 storage) measured faster with lrelu_ref.
+  const int actk = !a.xact ? 0 : P == 2 && a.slope > 0.f && a.slope <= 1.f ? 1 : 2;
   auto stage = [&](int c) {
+    using A0 = std::integral_constant<int, 0>;
+    using A1 = std::integral_constant<int, 1>;
+    using A2 = std::integral_constant<int, 2>;
     if (interior && static_cast<long>(c) * kChunk + 8 * g + 8 <= a.cin) {
-      if (a.xact) stage_rows(std::true_type{}, std::true_type{}, c);
-      else stage_rows(std::true_type{}, std::false_type{}, c);
+      if constexpr (P == 2) {
+        if (actk == 1) return stage_rows(std::true_type{}, A1{}, c);
+      }
+      if (actk) stage_rows(std::true_type{}, A2{}, c);
+      else stage_rows(std::true_type{}, A0{}, c);
     } else {
-      if (a.xact) stage_rows(std::false_type{}, std::true_type{}, c);
-      else stage_rows(std::false_type{}, std::false_type{}, c);
+      if (actk) stage_rows(std::false_type{}, A2{}, c);
+      else stage_rows(std::false_type{}, A0{}, c);
     }
   };
 

@@ -439,3 +439,58 @@ def test_x_lrelu_input_equals_materialized_lrelu(dt, round_x):
     yb = up.forward(xl, round_x=round_x)
     torch.cuda.synchronize()
     assert torch.equal(ya.view(torch.int16), yb.view(torch.int16))
+
+
+def split_values(r, n):
+    """fp32 values over the whole range the hi / lo split covers: magnitudes 2^-40 .. 2^15 (many
+    with an fp16-subnormal remainder, every one below 2^-3), the end of the fp16 range
+    (65504 <= |x| < 65520 rounds hi to 65504), both zeros and both signs."""
+    e = r.uniform(-40.0, 15.99, n)
+    x = np.exp2(e) * np.where(r.random(n) < 0.5, -1.0, 1.0)
+    x[: n // 64] = r.uniform(65504.0, 65519.99, n // 64) * np.where(r.random(n // 64) < 0.5, -1, 1)
+    x[n // 64: n // 64 + 16] = 0.0
+    x[n // 64 + 16: n // 64 + 32] = -0.0
+    return r.permutation(x.astype(np.float32))
+
+
+@pytest.mark.parametrize("C", [64, 45])
+@pytest.mark.parametrize("dt,round_x,xact", [(F32, False, False), (F32, False, True),
+                                             (F32, True, False), (F32, True, True),
+                                             (F16, False, True)])
+def test_staging_split_with_identity_weights(C, dt, round_x, xact):
+    """Identity weights (k 1, w[o, i] = 1 if o == i else 0) make each output the staged value itself:
+    in the exact mode hi + lo of v, hi = f16(v), lo = f16(v - hi), added in fp32 (exact: at most 22
+    significant bits), v = x or, with the input LeakyReLU (slope 0.1), lrelu(x); in round_x mode
+    f16(v); with fp16 storage f16(v). The expected values come from numpy's fp16 rounding, so this
+    pins the split bit for bit, fp16-subnormal remainders included. Zeros are compared as numbers
+    (the other channels' zero products decide a zero sum's sign). T leaves a partial last tile and
+    C = 45 a partial channel group, so both staging paths run."""
+    r = rng(700 + C + 10 * dt + 2 * round_x + xact)
+    T = 4096 + 37
+    x = split_values(r, C * T).reshape(C, T)
+    if dt == F16:
+        x = np.clip(x, -60000, 60000).astype(np.float16).view(np.uint16)
+    w = np.zeros((C, C, 1), np.float16)
+    w[np.arange(C), np.arange(C), 0] = 1.0
+    xd = dev(x, dt)
+    conv = gsvk.Conv1d(dev(w.view(np.uint16), F16), None, 1)
+    conv.b = None
+    epi = gsvk.CONV_EPI_BIAS | (gsvk.CONV_X_LRELU if xact else 0)
+    y = host(conv.forward(xd, epi=epi, slope=0.1, round_x=round_x), dt)
+    torch.cuda.synchronize()
+    v = O.to_f32(dt, x)
+    if xact:
+        v = np.where(v < 0, v * np.float32(0.1), v).astype(np.float32)
+    hi = v.astype(np.float16)
+    if dt == F16:
+        want = hi.astype(np.float32)
+    elif round_x:
+        want = hi.astype(np.float32)
+    else:
+        lo = (v - hi.astype(np.float32)).astype(np.float16)
+        want = hi.astype(np.float32) + lo.astype(np.float32)
+    got = O.to_f32(dt, y)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} differ, first {bad[:3].tolist()}: " \
+                          f"x {v[tuple(bad[0])]!r} got {got[tuple(bad[0])]!r} want {want[tuple(bad[0])]!r}"
+    say(f"identity split C={C} dt={dt} round_x={round_x} xact={xact}: {C * T} values exact")
