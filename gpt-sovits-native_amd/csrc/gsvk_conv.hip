@@ -467,17 +467,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   _Float16* ws = xs + static_cast<size_t>(P) * 4 * TTH * 8;  // [kTapGroup][4][TO][8]
   const int ng = (m.kn + kTapGroup - 1) / kTapGroup;
   const int Q = a.nch * ng;
+  // The packed weights as a buffer: a group's first tap as the scalar offset, each item's place
+  // in the group (tap slot, channel group, row) as a 32-bit vector offset fixed for the launch;
+  // only a chunk's short last group clamps the tap slot. (The entry points keep the packed weights
+  // under 2 GiB.)
+  const int tap_bytes = static_cast<int>(a.opad) * 4 * 16;  // one tap of a chunk: 4 x opad rows
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(m.wp), 0, 0x7FFFFFFF, 0x00020000);
+  int wofs[WPT], wtap[WPT];
+#pragma unroll
+  for (int u = 0; u < WPT; ++u) {
+    const int it = min(tid + kThreads * u, WITEMS - 1);
+    wtap[u] = it / (4 * TO);
+    wofs[u] = (((it / TO) & 3) * static_cast<int>(a.opad) + static_cast<int>(o0) + it % TO) * 16;
+  }
   u32x4 wraw[WPT];
   auto wload = [&](int q) {
     const int c = q / ng, kk0 = (q - c * ng) * kTapGroup, nt = min(kTapGroup, m.kn - kk0);
-    const size_t s0 = static_cast<size_t>(c) * m.kn + kk0;
+    const int s0 = (c * m.kn + kk0) * tap_bytes;
 #pragma unroll
-    for (int u = 0; u < WPT; ++u) {
-      const int it = min(tid + kThreads * u, WITEMS - 1);
-      const int tap = it / (4 * TO), gq = (it / TO) & 3, row = it % TO;
-      const size_t r = ((s0 + min(tap, nt - 1)) * 4 + gq) * a.opad + o0 + row;
-      wraw[u] = ld16<false>(m.wp + r * 8);
-    }
+    for (int u = 0; u < WPT; ++u)
+      wraw[u] = __builtin_amdgcn_raw_buffer_load_b128(
+          wrs, wofs[u] + min(wtap[u], nt - 1) * tap_bytes, s0, 0);
   };
   auto wstage = [&]() {
 #pragma unroll
@@ -758,6 +769,7 @@ int conv_entry(ConvArgs a, int dtype, int round_x, size_t T, size_t Tout, size_t
                ldc = static_cast<size_t>(a.ldc);
   if (ldx < T || (has_y && ldy < Tout) || (has_cur && ldc < Tout)) return GSVK_E_SIZE;
   if (kChunk * ldx * dtype_size(dtype) >= (1ul << 31)) return GSVK_E_SIZE;
+  if (wb >= (1ul << 31)) return GSVK_E_SIZE;  // packed weights: 32-bit buffer offsets
   if (!aligned16(a.wp)) return GSVK_E_ARG;
   if (!has_y) a.y = nullptr, a.ldy = 0;
   if (!has_cur) a.cur = nullptr, a.ldc = 0;
