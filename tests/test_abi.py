@@ -243,6 +243,7 @@ def test_conv_validation(gsvk_lib):
     assert call(k=11, dil=26) == gsvk.E_ARG      # halo (k - 1) dil above 256
     assert call(w=B + 8) == gsvk.E_ARG           # packed weights not 16-byte aligned
     assert call(ldx=1 << 26, T=100) == gsvk.E_SIZE  # 32 rows beyond 32-bit offsets
+    assert call(cin=16384, cout=16384, k=4) == gsvk.E_SIZE  # 2 GiB of packed weights
     assert call(y=A + 64) == gsvk.E_ALIAS        # output over x
     assert call(y=B + 64) == gsvk.E_ALIAS        # output over the weights
     assert call(bias=C + 16) == gsvk.E_ALIAS     # bias inside y
