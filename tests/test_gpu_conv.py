@@ -142,6 +142,8 @@ def test_round_x_mode(C, k, dil):
     (70, 100, 257, 4, 3),   # even k: pad (k - 1) dil / 2 rounds down
     (50, 40, 300, 1, 1),    # k = 1: a matrix product
     (40, 24, 400, 11, 20),  # halo 200 > 64: the wide-halo tile
+    (40, 36, 700, 5, 4),    # halo 16: the largest the 16-column halo slab takes
+    (40, 36, 700, 3, 9),    # halo 18: the first past it (64-column halo block)
     (192, 768, 50, 7, 1),   # conv_pre (192 -> 768, k 7) at 50 frames
 ])
 def test_shapes_and_edges(cin, cout, T, k, dil):
@@ -368,6 +370,7 @@ def test_tanh_epilogue_conv_post(dt):
     (64, 98304, 3, 1, gsvk.CONV_EPI_RES_LRELU),    # whole tiles only; residual + next LeakyReLU
     (120, 51201, 7, 3, gsvk.CONV_EPI_RES),          # 120 of 128 rows: a ragged second block
     (64, 98305, 11, 1, gsvk.CONV_EPI_BIAS),
+    (64, 98305, 5, 4, gsvk.CONV_EPI_LRELU),  # halo 16: the slab's limit
 ])
 def test_wide_tiles_fp32(C, T, k, dil, epi):
     check_case(F32, C, C, T, k, dil, epi=epi, seed=500 + C + k, what="wide")
