@@ -715,9 +715,17 @@ int launch_plan(const ConvArgs& a, hipStream_t st) {
     // (alternating on one box): exact 3955-4035 -> 3767-3852 us, round_x 3090-3106 -> 2981-2987,
     // fp16 storage 2946-2959 -> 2864. Smaller time tiles instead (32 columns per workgroup) or
     // both were slower.
+    // With the exact split (two staged planes per chunk), such grids instead take 64-column time
+    // tiles at the full fragment count: about as many workgroups, half the staging per product.
+    // Alternating on one box: the 384-channel stage 5% faster exact, the decoder graph 3506-3518
+    // -> 3465-3474 us; with one plane (round_x, fp16 storage) the same tiles were 7% slower there.
     const long npos = a.up ? a.T + 1 : a.T;
     const long groups =
         (npos + 127) / 128 * ((a.cout + 16 * no - 1) / (16 * no)) * (a.up ? a.up : 1);
+    if constexpr (XM == kXSplit) {
+      if (groups < 512)
+        return halo <= 16 ? launch_no<XM, 1, 16>(a, no, st) : launch_no<XM, 1, 64>(a, no, st);
+    }
     if (groups < 512 && no > 2 && (a.cout + 31) / 32 * 32 <= a.opad) no = 2;
     return halo <= 16 ? launch_no<XM, 2, 16>(a, no, st) : launch_no<XM, 2, 64>(a, no, st);
   }
