@@ -227,7 +227,8 @@ int gsvk_decode_attention_noalloc(int kv_dtype, int out_dtype, const float* qkv,
  * halves, x to about 2^-22 relative, not exactly (round_x = 0, the reference's sgemm path;
  * |x| < 65504), or rounds them to fp16 (round_x = 1, as the reference's AMX path packs them,
  * conv1d.hpp:130-151); F16 storage rounds each output once.
- * (k - 1) * dilation <= 256. y and cur must not overlap x, the weights, the bias or each other
+ * (k - 1) * dilation <= 256; 32 rows of x and the packed weights each under 2 GiB (GSVK_E_SIZE
+ * otherwise). y and cur must not overlap x, the weights, the bias or each other
  * (the reference's in-place x == y goes through a copy; here the caller keeps them apart); res may
  * equal cur but must not otherwise overlap an output.
  * The sum is formed in the matrix cores' order: |y - ref| <= 1e-5 * max(1, max_t |ref[o, t]|)
