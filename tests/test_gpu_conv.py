@@ -174,6 +174,25 @@ def test_nonfinite_inputs():
     assert_conv_close(F32, y, want, want, "non-finite")
 
 
+@pytest.mark.parametrize("round_x", [False, True])
+def test_nonfinite_inputs_in_the_halo_slab(round_x):
+    """k 3: the 16-column halo slab stages the columns past each 128-column tile (here 127 .. 142 of
+    the first tile, 255 .. 270 of the second): inf / NaN placed there, and at a tile's first column,
+    must reach exactly the outputs the oracle's sums reach."""
+    r = rng(85 + round_x)
+    cin, cout, T, k, dil = 40, 20, 600, 3, 1
+    x, w, b, _ = make(r, cin, cout, T, k)
+    x[3, 128] = np.inf
+    x[7, 129] = np.nan
+    x[12, 255] = -np.inf
+    x[33, 256] = np.inf
+    x[39, 142] = -np.inf
+    xo = O.to_storage(F32, O.to_f32(F16, O.to_storage(F16, x))) if round_x else x
+    want = O.conv1d(F32, xo, w, b, dil)
+    y, _ = run_gpu(F32, x, w, b, dil, 0, round_x=round_x)
+    assert_conv_close(F32, y, want, want, f"non-finite slab rx={round_x}")
+
+
 def test_deterministic():
     r = rng(90)
     x, w, b, _ = make(r, 96, 96, 3000, 11)
