@@ -14,12 +14,27 @@ constexpr size_t kAlign = 256;  // bytes: alignment of every workspace region
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout: the folded bias (c0 floats), then 6 activation slots of `slot` elements of the
+// Workspace layout: the folded bias (c0 floats), then 8 activation slots of `slot` elements of the
 // activation dtype each: X (stage input, then the stage output), Y (upsampler output, the first
-// residual), TA (the pair's middle activation) and CUR0..CUR2 (the three branch accumulators).
-// The pairs' LeakyReLU inputs are not stored: the first conv of a pair reads lrelu(cur) as it
-// loads (GSVK_CONV_X_LRELU).
-enum Slot { kX, kY, kTa, kCur0, kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS };
+// residual), TA0..TA2 (each ResBlock's pair middle activation, so the three ResBlocks can run
+// side by side) and CUR0..CUR2 (the three branch accumulators). The pairs' LeakyReLU inputs are
+// not stored: the first conv of a pair reads lrelu(cur) as it loads (GSVK_CONV_X_LRELU).
+enum Slot {
+  kX,
+  kY,
+  kTa0,
+  kCur0 = kTa0 + GSVK_SOVITS_RESBLOCKS,
+  kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS
+};
+
+// In a recorded graph, ResBlocks 1 and 2 of every stage run on two more streams, concurrent with
+// ResBlock 0 on the main one (they share only the upsampler's output, which they read); the branch
+// mean waits for all three. nullptr: every launch on the one stream.
+struct Branches {
+  const hipStream_t* side;  // GSVK_SOVITS_RESBLOCKS - 1 streams
+  hipEvent_t fork;
+  const hipEvent_t* join;
+};
 
 struct Layout {
   size_t vec_bytes = 0;   // bytes of the folded bias (c0 floats, rounded up)
@@ -84,7 +99,7 @@ int count_launches(const gsvk_sovits_decoder_desc* d) {
 }
 
 // The launches of one decoder pass in Generator::forward's order.
-int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
+int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st, const Branches* br) {
   const int dt = d->dtype, rx = d->round_x;
   const float slope = 0.1f;  // LRELU_SLOPE (dec.hpp:284, 322, 324)
   char* ws = static_cast<char*>(d->workspace);
@@ -92,7 +107,7 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
   void* slot[kSlots];
   for (int i = 0; i < kSlots; ++i)
     slot[i] = ws + lay.vec_bytes + static_cast<size_t>(i) * lay.slot_bytes;
-  int rc;
+  int rc = GSVK_OK;
 
   // x = lrelu(conv_pre(z) + b_pre + cond(ge)[:, 0], 0.1): the broadcast add of dec.hpp:275-279
   // folded into the bias, the stage-0 leaky_relu_io (dec.hpp:284) into the store. cond is a k = 1
@@ -118,9 +133,17 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
                            nullptr, 0, slot[kY], Tu, S.c_in, C, T, S.ups_k, S.ups_u, st)))
       return rc;
     T = Tu;
+    constexpr int kSide = GSVK_SOVITS_RESBLOCKS - 1;
+    if (br) {
+      if (hipEventRecord(br->fork, static_cast<hipStream_t>(st)) != hipSuccess) return GSVK_E_HIP;
+      for (int i = 0; i < kSide; ++i)
+        if (hipStreamWaitEvent(br->side[i], br->fork, 0) != hipSuccess) return GSVK_E_HIP;
+    }
     const void* curs[GSVK_SOVITS_RESBLOCKS];
-    for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS; ++j) {
+    for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS && rc == GSVK_OK; ++j) {
+      void* bst = br && j > 0 ? br->side[j - 1] : st;
       void* cur = slot[kCur0 + j];
+      void* ta = slot[kTa0 + j];
       curs[j] = cur;
       const void* src = slot[kY];  // cur_j starts as a copy of y (dec.hpp:316): read it in place
       const void* res = slot[kY];
@@ -129,16 +152,23 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
         // convolution reads its input, leaky_relu_io in its store)
         if ((rc = gsvk_conv1d(dt, rx, src, T, S.w1[j][m], S.b1[j][m],
                               GSVK_CONV_EPI_LRELU | GSVK_CONV_X_LRELU, slope, nullptr, nullptr, 0,
-                              slot[kTa], T, C, C, T, S.res_k[j], S.res_dil[m], st)))
-          return rc;
+                              ta, T, C, C, T, S.res_k[j], S.res_dil[m], bst)))
+          break;
         // cur_j = res + convs2[m](t_a)  (dec.hpp:325-326)
-        if ((rc = gsvk_conv1d(dt, rx, slot[kTa], T, S.w2[j][m], S.b2[j][m], GSVK_CONV_EPI_RES, slope,
-                              cur, res, T, nullptr, T, C, C, T, S.res_k[j], 1, st)))
-          return rc;
+        if ((rc = gsvk_conv1d(dt, rx, ta, T, S.w2[j][m], S.b2[j][m], GSVK_CONV_EPI_RES, slope, cur,
+                              res, T, nullptr, T, C, C, T, S.res_k[j], 1, bst)))
+          break;
         src = cur;
         res = nullptr;  // in place from the second pair on
       }
     }
+    if (br)  // every side stream joins back, also after an error (a capture must end joined)
+      for (int i = 0; i < kSide; ++i)
+        if ((hipEventRecord(br->join[i], br->side[i]) != hipSuccess ||
+             hipStreamWaitEvent(static_cast<hipStream_t>(st), br->join[i], 0) != hipSuccess) &&
+            rc == GSVK_OK)
+          rc = GSVK_E_HIP;
+    if (rc) return rc;
     // x = lrelu(mean_j cur_j): mul_write / add_scaled_inplace (dec.hpp:328-333) with the next
     // stage's leaky_relu_io (dec.hpp:284, 0.1) or the final one (dec.hpp:342, 0.01).
     const float next_slope = s + 1 < d->n_stages ? slope : 0.01f;
@@ -155,9 +185,9 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st) {
 }  // namespace
 
 // The graph handle and its recorder live in t2s_decode_step.cpp.
-__attribute__((visibility("hidden"))) int gsvk_record_graph_(
-    int (*issue_fn)(const void*, hipStream_t), const void* ctx, int launches,
-    gsvk_t2s_step** out);
+__attribute__((visibility("hidden"))) int gsvk_record_graph_branches_(
+    int (*issue_fn)(const void*, hipStream_t, const hipStream_t*, hipEvent_t, const hipEvent_t*),
+    const void* ctx, int nside, int launches, gsvk_t2s_step** out);
 
 extern "C" size_t gsvk_sovits_decoder_workspace_bytes(const gsvk_sovits_decoder_desc* desc) {
   Layout lay;
@@ -167,7 +197,7 @@ extern "C" size_t gsvk_sovits_decoder_workspace_bytes(const gsvk_sovits_decoder_
 extern "C" int gsvk_sovits_decoder_eager(const gsvk_sovits_decoder_desc* desc, void* stream) {
   Layout lay;
   const int rc = check_workspace(desc, &lay);
-  return rc ? rc : issue(desc, lay, stream);
+  return rc ? rc : issue(desc, lay, stream, nullptr);
 }
 
 extern "C" int gsvk_sovits_decoder_create(const gsvk_sovits_decoder_desc* desc,
@@ -181,10 +211,12 @@ extern "C" int gsvk_sovits_decoder_create(const gsvk_sovits_decoder_desc* desc,
     const gsvk_sovits_decoder_desc* d;
     Layout lay;
   } ctx{desc, lay};
-  return gsvk_record_graph_(
-      [](const void* c, hipStream_t st) {
+  return gsvk_record_graph_branches_(
+      [](const void* c, hipStream_t st, const hipStream_t* side, hipEvent_t fork,
+         const hipEvent_t* join) {
         const Ctx* x = static_cast<const Ctx*>(c);
-        return issue(x->d, x->lay, st);
+        const Branches br{side, fork, join};
+        return issue(x->d, x->lay, st, &br);
       },
-      &ctx, count_launches(desc), out);
+      &ctx, GSVK_SOVITS_RESBLOCKS - 1, count_launches(desc), out);
 }

@@ -275,14 +275,58 @@ int record(Issue issue, int launches, gsvk_t2s_step** out) {
                  out);
 }
 
-// The recorder for other drivers of this library (the SoVITS decoder): issue_fn(ctx, stream)
-// makes the launches.
-__attribute__((visibility("hidden"))) int gsvk_record_graph_(
-    int (*issue_fn)(const void*, hipStream_t), const void* ctx, int launches,
-    gsvk_t2s_step** out) {
+// The recorder with concurrent branches (the SoVITS decoder's ResBlocks): issue_fn(ctx, cap, side,
+// fork, join) launches on cap and on the nside streams side[0 .. nside - 1]; it uses fork (to be
+// recorded on cap) and join[i] (on side[i]) to make the side streams' work depend on cap's and
+// cap's on theirs, and must join every side stream back into cap before it returns (also after an
+// error), or the capture cannot end.
+__attribute__((visibility("hidden"))) int gsvk_record_graph_branches_(
+    int (*issue_fn)(const void*, hipStream_t, const hipStream_t*, hipEvent_t, const hipEvent_t*),
+    const void* ctx, int nside, int launches, gsvk_t2s_step** out) {
+  constexpr int kMaxSide = 4;
   if (!out) return GSVK_E_NULL;
   *out = nullptr;
-  return record([issue_fn, ctx](hipStream_t st) { return issue_fn(ctx, st); }, launches, out);
+  if (nside < 1 || nside > kMaxSide) return GSVK_E_ARG;
+  hipStream_t cap = nullptr, side[kMaxSide] = {};
+  hipEvent_t fork = nullptr, join[kMaxSide] = {};
+  auto release = [&]() {
+    if (fork) (void)hipEventDestroy(fork);
+    for (int i = 0; i < nside; ++i) {
+      if (join[i]) (void)hipEventDestroy(join[i]);
+      if (side[i]) (void)hipStreamDestroy(side[i]);
+    }
+    if (cap) (void)hipStreamDestroy(cap);
+  };
+  bool ok = hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) == hipSuccess &&
+            hipEventCreateWithFlags(&fork, hipEventDisableTiming) == hipSuccess;
+  for (int i = 0; ok && i < nside; ++i)
+    ok = hipStreamCreateWithFlags(&side[i], hipStreamNonBlocking) == hipSuccess &&
+         hipEventCreateWithFlags(&join[i], hipEventDisableTiming) == hipSuccess;
+  auto* s = ok ? new (std::nothrow) gsvk_t2s_step : nullptr;
+  if (!s) {
+    release();
+    return GSVK_E_HIP;
+  }
+  int rc = GSVK_OK;
+  if (hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    rc = GSVK_E_HIP;
+  } else {
+    rc = issue_fn(ctx, cap, side, fork, join);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(cap, &g);
+    if (rc == GSVK_OK && e != hipSuccess) rc = GSVK_E_HIP;
+    s->graph = g;
+  }
+  if (rc == GSVK_OK && hipGraphInstantiate(&s->exec, s->graph, nullptr, nullptr, 0) != hipSuccess)
+    rc = GSVK_E_HIP;
+  release();
+  if (rc != GSVK_OK) {
+    gsvk_t2s_step_destroy(s);
+    return rc;
+  }
+  s->launches = launches;
+  *out = s;
+  return GSVK_OK;
 }
 
 extern "C" int gsvk_t2s_step_create(const gsvk_t2s_step_desc* desc, gsvk_t2s_step** out) {

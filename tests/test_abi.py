@@ -445,8 +445,8 @@ def _decoder_desc(frames=500, c0=768, n_stages=5, fake=0x1000):
 
 def test_sovits_decoder_workspace_and_validation(gsvk_lib):
     d, keep = _decoder_desc()
-    # the folded bias (768 floats), 6 slots of the largest stage tensor (192 x 40000 = 7.68M)
-    want = (768 + 6 * 7_680_000) * 4
+    # the folded bias (768 floats), 8 slots of the largest stage tensor (192 x 40000 = 7.68M)
+    want = (768 + 8 * 7_680_000) * 4
     assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(ctypes.byref(d)) == want
     assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(None) == 0
     h = ctypes.c_void_p()
@@ -475,7 +475,7 @@ def test_sovits_decoder_workspace_and_validation(gsvk_lib):
     e, k2 = _decoder_desc()
     e.dtype = gsvk.F16  # fp16 activation slots (2 bytes); the folded bias stays fp32
     assert gsvk_lib.gsvk_sovits_decoder_workspace_bytes(ctypes.byref(e)) == 768 * 4 + \
-        6 * 7_680_000 * 2
+        8 * 7_680_000 * 2
     assert bad(frames=0) == gsvk.E_SIZE
     assert bad(n_stages=0) == gsvk.E_SIZE
     assert bad(n_stages=9) == gsvk.E_SIZE
