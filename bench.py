@@ -117,9 +117,15 @@ def headline_line(rec):
     conv = rec.get("sovits_conv")
     if conv:
         gen = conv.get("generator") or {}
+        dec_us = (gen.get("decoder") or {}).get("us")
         line["sovits"] = {"conv_frac_mfma": conv["roofline"]["frac"],
                           "conv_frac_of_bound": conv.get("frac_of_bound_by_stage"),
-                          "decoder_graph_us": (gen.get("decoder") or {}).get("us")}
+                          "decoder_graph_us": dec_us}
+        # the same algorithmic flops over the decoder graph's time (its ResBlocks run side by
+        # side, so the graph takes less than the convolutions' one-at-a-time sum)
+        if dec_us and conv["roofline"].get("flops"):
+            line["sovits"]["decoder_frac_mfma"] = round(
+                conv["roofline"]["flops"] / dec_us / 1e6 / conv["roofline"]["peak"], 4)
     if rec.get("detail_file"):
         line["detail_file"] = rec["detail_file"]
     s = json.dumps(line, separators=(",", ":"))
