@@ -846,6 +846,13 @@ def sovits_generator(torch, gsvk, dev, geometry="reference_768", reps=5, frames=
                      "workspace_bytes": dec.ws.numel(),
                      "activations": "f16" if zz.dtype == torch.float16 else "f32",
                      "round_x": rx}
+        if name == "decoder":  # the same launches issued directly (gsvk_sovits_decoder_eager)
+            eager = gsvk.SovitsDecoder(pre, cond, stages, post, zz, ge, wav, round_x=rx,
+                                       graph=False)
+            eus = timed(eager.run)
+            log(f"  whole {name} (eager, {eager.launches} launches): {eus:.1f} us")
+            res[name]["eager_us"] = round(eus, 1)
+            del eager
         del dec, wav
         torch.cuda.empty_cache()
     del stages, pre, cond, post, z, ge

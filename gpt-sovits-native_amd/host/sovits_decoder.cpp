@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "gsvk.h"
 #include "gsvk_sovits.h"
@@ -27,11 +28,13 @@ enum Slot {
   kSlots = kCur0 + GSVK_SOVITS_RESBLOCKS
 };
 
-// In a recorded graph, ResBlocks 1 and 2 of every stage run on two more streams, concurrent with
-// ResBlock 0 on the main one (they share only the upsampler's output, which they read); the branch
-// mean waits for all three. nullptr: every launch on the one stream.
+// ResBlocks 1 and 2 of every stage run on two more streams, concurrent with ResBlock 0 on the main
+// one (they share only the upsampler's output, which they read); the branch mean waits for all
+// three. In a recorded graph the streams and events are the capture's; eagerly, the side streams
+// are the device's own (below) and the events the call's.
+constexpr int kSide = GSVK_SOVITS_RESBLOCKS - 1;
 struct Branches {
-  const hipStream_t* side;  // GSVK_SOVITS_RESBLOCKS - 1 streams
+  const hipStream_t* side;  // kSide streams
   hipEvent_t fork;
   const hipEvent_t* join;
 };
@@ -133,7 +136,6 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st, const 
                            nullptr, 0, slot[kY], Tu, S.c_in, C, T, S.ups_k, S.ups_u, st)))
       return rc;
     T = Tu;
-    constexpr int kSide = GSVK_SOVITS_RESBLOCKS - 1;
     if (br) {
       if (hipEventRecord(br->fork, static_cast<hipStream_t>(st)) != hipSuccess) return GSVK_E_HIP;
       for (int i = 0; i < kSide; ++i)
@@ -182,6 +184,27 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st, const 
                      st);
 }
 
+// The eager form's side streams: two per device, created on its first eager call and kept for the
+// process (default priority, non-blocking). Calls that overlap on one device share them; each
+// call's own events order its launches, so sharing only serializes the calls' side work.
+constexpr int kMaxDevices = 64;
+int device_side_streams(hipStream_t (&side)[kSide]) {
+  static std::mutex mu;
+  static hipStream_t streams[kMaxDevices][kSide];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GSVK_E_HIP;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < kSide; ++i) {
+    if (!streams[dev][i] &&
+        hipStreamCreateWithFlags(&streams[dev][i], hipStreamNonBlocking) != hipSuccess) {
+      streams[dev][i] = nullptr;
+      return GSVK_E_HIP;
+    }
+    side[i] = streams[dev][i];
+  }
+  return GSVK_OK;
+}
+
 }  // namespace
 
 // The graph handle and its recorder live in t2s_decode_step.cpp.
@@ -196,8 +219,24 @@ extern "C" size_t gsvk_sovits_decoder_workspace_bytes(const gsvk_sovits_decoder_
 
 extern "C" int gsvk_sovits_decoder_eager(const gsvk_sovits_decoder_desc* desc, void* stream) {
   Layout lay;
-  const int rc = check_workspace(desc, &lay);
-  return rc ? rc : issue(desc, lay, stream, nullptr);
+  int rc = check_workspace(desc, &lay);
+  if (rc) return rc;
+  hipStream_t side[kSide];
+  hipEvent_t fork = nullptr, join[kSide] = {};
+  rc = device_side_streams(side);
+  if (rc == GSVK_OK && hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess)
+    rc = GSVK_E_HIP;
+  for (int i = 0; i < kSide && rc == GSVK_OK; ++i)
+    if (hipEventCreateWithFlags(&join[i], hipEventDisableTiming) != hipSuccess) rc = GSVK_E_HIP;
+  if (rc == GSVK_OK) {
+    const Branches br{side, fork, join};
+    rc = issue(desc, lay, stream, &br);
+  }
+  // (an event destroyed while its record is pending is released once that work completes)
+  if (fork) (void)hipEventDestroy(fork);
+  for (int i = 0; i < kSide; ++i)
+    if (join[i]) (void)hipEventDestroy(join[i]);
+  return rc;
 }
 
 extern "C" int gsvk_sovits_decoder_create(const gsvk_sovits_decoder_desc* desc,
