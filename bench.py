@@ -120,7 +120,8 @@ def headline_line(rec):
         dec_us = (gen.get("decoder") or {}).get("us")
         line["sovits"] = {"conv_frac_mfma": conv["roofline"]["frac"],
                           "conv_frac_of_bound": conv.get("frac_of_bound_by_stage"),
-                          "decoder_graph_us": dec_us}
+                          "decoder_graph_us": dec_us,
+                          "decoder_eager_us": (gen.get("decoder") or {}).get("eager_us")}
         # the same algorithmic flops over the decoder graph's time (its ResBlocks run side by
         # side, so the graph takes less than the convolutions' one-at-a-time sum)
         if dec_us and conv["roofline"].get("flops"):
@@ -1870,7 +1871,8 @@ def main():
                                                   for r in full))
         conv = sovits_conv(torch, gsvk, dev)
         conv["generator"] = sovits_generator(torch, gsvk, dev)
-        progress(f"SoVITS decoder graph: {conv['generator']['decoder']['us']} us per 10 s of audio")
+        progress(f"SoVITS decoder graph: {conv['generator']['decoder']['us']} us per 10 s of audio "
+                 f"(eager on three streams: {conv['generator']['decoder'].get('eager_us')} us)")
         if not a.no_cpu:
             cpu_lines, tall = cpu_kernel_baselines()
             for rec in kernels:

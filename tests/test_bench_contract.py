@@ -76,7 +76,8 @@ def _representative_record(mod):
     full = [{"kv_len": kv, "us_per_step": 1106.9, "tokens_per_s": 57819.0, "frac_of_peak": 0.3871,
              "launches": 292, "bytes_per_step": 3430000000} for kv in (1024, 2048)]
     conv = {"roofline": {"frac": 0.0948, "achieved": 236.9, "peak": 2500.0, "flops": 914227200000.0},
-            "generator": {"decoder": {"us": 3761.2, "launches": 103}}, "stages": [{}] * 5}
+            "generator": {"decoder": {"us": 3761.2, "eager_us": 3700.5, "launches": 103}},
+            "stages": [{}] * 5}
     return {
         "metric": mod.METRIC, "value": 1389.51, "unit": "GB/s", "n_gpus": 1, "steps": 200,
         "warmup": 20, "ms_per_step": 0.01639, "higher_is_better": True, "scaling": "weak",
@@ -133,6 +134,7 @@ def test_headline_line_fits_the_captured_tail_and_keeps_its_keys():
     assert line["configs"]["4"]["cpu_best_GBps"] is not None
     assert set(line["whole_decode_step"]) == {"kv1024", "kv2048"}
     assert line["sovits"]["decoder_graph_us"] == 3761.2
+    assert line["sovits"]["decoder_eager_us"] == 3700.5
     assert line["sovits"]["decoder_frac_mfma"] == round(914227200000.0 / 3761.2 / 1e6 / 2500.0, 4)
     # the suite itself stays out of the line
     for key in ("kernels", "sovits_conv", "t2s_whole_decode_step", "per_op"):
