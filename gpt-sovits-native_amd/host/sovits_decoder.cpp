@@ -136,10 +136,10 @@ int issue(const gsvk_sovits_decoder_desc* d, const Layout& lay, void* st, const 
                            nullptr, 0, slot[kY], Tu, S.c_in, C, T, S.ups_k, S.ups_u, st)))
       return rc;
     T = Tu;
-    if (br) {
+    if (br) {  // (a failed wait still reaches the joins below)
       if (hipEventRecord(br->fork, static_cast<hipStream_t>(st)) != hipSuccess) return GSVK_E_HIP;
       for (int i = 0; i < kSide; ++i)
-        if (hipStreamWaitEvent(br->side[i], br->fork, 0) != hipSuccess) return GSVK_E_HIP;
+        if (hipStreamWaitEvent(br->side[i], br->fork, 0) != hipSuccess) rc = GSVK_E_HIP;
     }
     const void* curs[GSVK_SOVITS_RESBLOCKS];
     for (size_t j = 0; j < GSVK_SOVITS_RESBLOCKS && rc == GSVK_OK; ++j) {
