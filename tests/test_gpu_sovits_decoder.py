@@ -160,6 +160,38 @@ def test_decoder_matches_oracle_chain(c_z, c0, g_in, frames, round_x):
     assert err.max() <= tol
 
 
+def test_decoder_eager_on_a_caller_stream_equals_the_graph():
+    """The eager form runs ResBlocks 1 and 2 of each stage on the library's own streams, forked
+    after the work already on the caller's stream and joined back before the branch mean: issued
+    on a non-default stream behind a fill of the output, three calls in a row give the graph's
+    bits (a late fork would read a stale upsampler output, a missing join a partial branch)."""
+    r = np.random.default_rng(20251202)
+    m = make_decoder(r, 16, 64, 32)
+    frames = 12
+    z = r.standard_normal((16, frames)).astype(np.float32)
+    ge = r.standard_normal(32).astype(np.float32)
+    g = GpuDecoder(m)
+    zd, ged = devf(z), devf(ge)
+    n_out = frames * int(np.prod(UPS_U))
+    out_g = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    out_e = torch.full((n_out,), float("nan"), dtype=torch.float32, device="cuda")
+    say("decoder graph vs eager on a caller stream: graph")
+    g.bind(zd, ged, out_g).run()
+    torch.cuda.synchronize()
+    ref = host(out_g, F32)
+    assert np.isfinite(ref).all()
+    eager = g.bind(zd, ged, out_e, graph=False)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for i in range(3):
+            say(f"  eager call {i} on a caller stream")
+            out_e.fill_(float("nan"))
+            eager.run(stream=s)
+            got = out_e.clone()
+            s.synchronize()
+            assert np.array_equal(host(got, F32).view(np.uint32), ref.view(np.uint32)), f"call {i}"
+
+
 def test_decoder_fp16_storage():
     """fp16 activations (every stored activation rounded to fp16, arithmetic in fp32; ge, cond and
     the folded bias in fp32) against the oracle chain with the same rounding points. The only
