@@ -298,15 +298,16 @@ __device__ __forceinline__ void finish4(const ConvArgs& a, const Map& m, long o,
 // 16-wide ones, and each refill of LDS (x per chunk, weights per tap group) feeds twice the
 // matrix-core work of a workgroup.
 //
-// At least two waves per SIMD: the register budget is sized for them (every tile fits without
-// spilling; the compiler would otherwise keep two steps' fragments live). The fp16-storage 32-wide
-// tiles take three (168 VGPRs, a few spilled): with the decoder's ResBlocks sharing the chip, its
-// fp16-storage graph measured 4% faster; the exact split's tiles were slower so.
+// At least two waves per SIMD: the register budget is sized for them (the compiler would
+// otherwise keep two steps' fragments live); at two, every tile fits without spilling. The
+// fp16-storage 32-wide tiles take three (168 VGPRs, a few spilled): with the decoder's ResBlocks
+// sharing the chip, its fp16-storage graph measured 4% faster; the exact split's tiles were slower
+// so.
 template <int XM>
 constexpr int conv_waves_per_eu(int fs) { return XM == kXF16 && fs == 32 ? 3 : 2; }
 template <int XM, int NT, int NO, int HMAX, int FS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(conv_waves_per_eu<XM>(FS)))) void conv1d_mfma(
-    ConvArgs a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(conv_waves_per_eu<XM>(FS)))) void conv1d_mfma(ConvArgs a) {
   constexpr int DT = storage_dt<XM>();
   constexpr int P = planes<XM>();
   constexpr int TT = kWaves * FS * NT;  // output columns of the workgroup
