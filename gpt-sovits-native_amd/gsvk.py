@@ -368,7 +368,8 @@ class SovitsDecoder:
     """The whole SoVITS decoder (Generator::forward, dec.hpp:264-345) over one set of device
     buffers: conv_pre (+ cond(ge) folded into its bias) and LeakyReLU, the GeneratorStages, the final
     LeakyReLU(0.01), conv_post and tanh, as gsvk_sovits_decoder_* launches (a HIP graph unless
-    graph=False). conv_pre / conv_post are Conv1d, stages GeneratorStage objects, cond a pair
+    graph=False; either way each stage's three ResBlocks run concurrently: graph branches, or the
+    library's two side streams joined back into the caller's). conv_pre / conv_post are Conv1d, stages GeneratorStage objects, cond a pair
     (w16 [c0, g_in] fp16, bias [c0] fp32) or None; z [c_z, frames] fp32 or fp16 (the activation
     dtype), ge [g_in] fp32 (one frame; None without cond), out [frames * prod(u)] of z's dtype.
     The workspace is this object's own device allocation."""
