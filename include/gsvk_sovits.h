@@ -79,7 +79,9 @@ size_t gsvk_sovits_decoder_workspace_bytes(const gsvk_sovits_decoder_desc* desc)
 /* Issue the decoder's launches on `stream` (GSVK_E_NULL / E_SIZE / E_ARG on a bad descriptor).
  * ResBlocks 1 and 2 of each stage run on two streams the library keeps per device, ordered after
  * the work already on `stream` and joined back into it (each stage's branch mean waits for them), so
- * `stream` orders the whole decoder as usual. */
+ * `stream` orders the whole decoder as usual. Those streams are created on the device's first call:
+ * a caller recording this call into a graph of its own makes one call outside the capture first
+ * (gsvk_sovits_decoder_create records the same launches by itself). */
 int gsvk_sovits_decoder_eager(const gsvk_sovits_decoder_desc* desc, void* stream);
 /* Record the same launches into a HIP graph; run it with gsvk_t2s_step_run, free it with
  * gsvk_t2s_step_destroy. The graph keeps the descriptor's pointers: the buffers must outlive it. */
