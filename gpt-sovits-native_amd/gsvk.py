@@ -314,34 +314,54 @@ class GeneratorStage:
                                                   no copy of y
       out = lrelu(mean_j cur_j, slope_next)       mul_write / add_scaled_inplace + the next stage's
                                                   leaky_relu_io (dec.hpp:328-336, 284 or 342)
-    Launches: 1 upsampler, 18 convolutions, 1 branch mean."""
+    Launches: 1 upsampler, 18 convolutions, 1 branch mean. ResBlocks after the first run on side
+    streams of their own (each with its own t_a), forked after the upsampler and joined back before
+    the branch mean, as in gsvk_sovits_decoder_*."""
 
     def __init__(self, ups, resblocks):
         self.ups = ups
         self.resblocks = resblocks
         self._buf = None
+        self._side = None
 
     def _buffers(self, C, T, dtype, device):
         import torch
         key = (C, T, dtype, device)
         if self._buf is None or self._buf[0] != key:
             mk = lambda: torch.empty(C, T, dtype=dtype, device=device)
-            self._buf = (key, mk(), mk(), [mk() for _ in self.resblocks])
+            self._buf = (key, mk(), [mk() for _ in self.resblocks], [mk() for _ in self.resblocks])
         return self._buf[1:]
 
+    def _side_streams(self, device):
+        import torch
+        if self._side is None or self._side[0] != device:
+            self._side = (device, [torch.cuda.Stream(device=device)
+                                   for _ in self.resblocks[1:]])
+        return self._side[1]
+
     def forward(self, x, out, slope_next=0.1, round_x=False, stream=None):
-        y, t_a, curs = self._buffers(self.ups.out_c, x.shape[1] * self.ups.stride_u, x.dtype,
+        import torch
+        y, tas, curs = self._buffers(self.ups.out_c, x.shape[1] * self.ups.stride_u, x.dtype,
                                      x.device)
-        self.ups.forward(x, y, round_x=round_x, stream=stream)
-        for rb, cur in zip(self.resblocks, curs):
+        main = stream if stream is not None else torch.cuda.current_stream(x.device)
+        if isinstance(main, int):
+            main = torch.cuda.ExternalStream(main, device=x.device)
+        self.ups.forward(x, y, round_x=round_x, stream=main)
+        sides = self._side_streams(x.device)
+        for sd in sides:
+            sd.wait_stream(main)  # the upsampler's y before any branch reads it
+        for j, (rb, t_a, cur) in enumerate(zip(self.resblocks, tas, curs)):
+            st = main if j == 0 else sides[j - 1]
             src, res = y, y
             for c1, c2 in zip(rb.convs1, rb.convs2):
                 c1.forward(src, t_a, epi=CONV_EPI_LRELU | CONV_X_LRELU, slope=0.1, round_x=round_x,
-                           stream=stream)
+                           stream=st)
                 c2.forward(t_a, None, epi=CONV_EPI_RES, cur=cur, res=res, round_x=round_x,
-                           stream=stream)
+                           stream=st)
                 src, res = cur, None
-        resblock_branch_mean(curs, None, out, True, slope_next, stream=stream)
+        for sd in sides:
+            main.wait_stream(sd)  # every branch before the mean
+        resblock_branch_mean(curs, None, out, True, slope_next, stream=main)
         return out
 
 
